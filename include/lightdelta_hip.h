@@ -1,0 +1,139 @@
+/*
+ * C ABI of the MI355X (gfx950) Gated DeltaNet decode library, liblightdelta_hip.so.
+ *
+ * Every entry point takes plain pointers, element/byte strides and sizes, plus the
+ * HIP stream (hipStream_t passed as void*) to launch on.  Nothing here allocates,
+ * synchronises the host or reads device metadata on the host, so every launch can be
+ * recorded into a HIP graph.  All entry points return 0 on success and a non-zero
+ * LD_ERR_* code otherwise; ld_last_error() then returns a message for the calling
+ * thread.  Empty work (zero requests / rows / pairs) is a successful no-op.
+ *
+ * Tensors are caller-owned device memory.  bf16 values are raw uint16 bit patterns.
+ */
+#ifndef LIGHTDELTA_HIP_H
+#define LIGHTDELTA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LD_ABI_VERSION 1
+
+#define LD_OK 0
+#define LD_ERR_INVALID_ARGUMENT 1
+#define LD_ERR_LAUNCH 2
+
+#define LD_DTYPE_F32 0
+#define LD_DTYPE_BF16 1
+
+/* Head geometry fixed by the kernels: dk = dv = 128. */
+#define LD_HEAD_DIM 128
+/* Tokens per request accepted by the decode / MTP-verify step. */
+#define LD_MAX_TOKENS 4
+
+/*
+ * Arguments of one fused post-conv GDN decode / MTP-verify step.
+ *
+ * Replaces lightdelta::decode (reference include/lightdelta/ops.h:5-9, launcher
+ * csrc/gdn_decode.cu:360-420, kernel csrc/gdn_decode.cu:130-354), generalised from
+ * the hard-coded 16/48 heads to any num_k_heads / num_v_heads with
+ * num_v_heads % num_k_heads == 0.
+ *
+ * Element strides (not bytes).  Layouts:
+ *   qkv     bf16 [tokens, (2*H + HV)*128], row stride qkv_row_stride, unit column stride;
+ *           q of k-head kh at column kh*128, k at H*128 + kh*128, v of v-head h at 2*H*128 + h*128
+ *   a, b    bf16 [tokens, HV], row strides a_row_stride / b_row_stride
+ *   a_log   fp32 [HV]; dt_bias fp32 or bf16 [HV] (dt_bias_dtype)
+ *   indices int32 [requests, width] contiguous; cu int32 [requests+1]; accepted int32 [requests]
+ *   state   fp32 [slots, HV, 128(V), 128(K)], K contiguous, slot stride state_slot_stride
+ *   gate    bf16 [tokens, HV, 128], row stride gate_row_stride, head stride 128
+ *   norm_weight fp32 or bf16 [128] (norm_weight_dtype)
+ *   out     bf16 [tokens, HV, 128] contiguous
+ * Request r covers tokens cu[r] .. cu[r+1]-1.  Its source state is slot
+ * indices[r, accepted[r]-1] when 1 <= accepted[r] <= width; the state after token t is
+ * written to slot indices[r, t].  A slot <= 0 is padding: never read, never written.
+ * A request with an invalid source, or with more tokens than width, gets zero outputs
+ * and leaves the pool untouched; a request with no tokens writes nothing.
+ */
+typedef struct ld_gdn_decode_args {
+  const void* qkv;
+  int64_t qkv_row_stride;
+  const void* a;
+  int64_t a_row_stride;
+  const void* b;
+  int64_t b_row_stride;
+  const float* a_log;
+  const void* dt_bias;
+  int32_t dt_bias_dtype;
+  int32_t norm_weight_dtype;
+  const int32_t* indices;
+  const int32_t* cu;
+  const int32_t* accepted;
+  float* state;
+  int64_t state_slot_stride;
+  const void* gate;
+  int64_t gate_row_stride;
+  const void* norm_weight;
+  void* out;
+  int32_t num_requests;
+  int32_t width;
+  int32_t num_k_heads;
+  int32_t num_v_heads;
+  float scale; /* q scale, 128^-0.5 in the reference (csrc/gdn_decode.cu:417) */
+  float eps;   /* gated RMSNorm epsilon, > 0 */
+} ld_gdn_decode_args;
+
+/* Fused decode step; see ld_gdn_decode_args.  Replaces lightdelta::decode
+ * (reference include/lightdelta/ops.h:5-9, csrc/gdn_decode.cu:360-420). */
+int ld_gdn_decode(const ld_gdn_decode_args* args, void* stream);
+
+/*
+ * Gather pool rows into a packed buffer:
+ *   out[r] = (slots[r*slot_stride] > 0 && valid[r]) ? pool[slots[r*slot_stride]] : 0
+ * Byte-generic (serves the fp32 SSM pool and the bf16 conv pool).  row_bytes, both
+ * row strides and both base pointers must be multiples of 16 bytes.  valid is a bool
+ * (one byte per row) vector, or NULL for "all valid".
+ * Replaces lightdelta::gather_state (reference include/lightdelta/ops.h:10-11,
+ * csrc/state_io.cu:44-58).
+ */
+int ld_state_gather(const void* pool, int64_t pool_slot_stride_bytes,
+                    const int32_t* slots, int64_t slot_stride, const uint8_t* valid,
+                    void* out, int64_t out_row_stride_bytes, int64_t row_bytes,
+                    int64_t rows, void* stream);
+
+/*
+ * Scatter packed rows into the pool, skipping padding:
+ *   if slots[r*slot_stride] > 0: pool[slots[r*slot_stride]] = packed[r]
+ * Same alignment rules as ld_state_gather.  Replaces lightdelta::scatter_state
+ * (reference include/lightdelta/ops.h:12, csrc/state_io.cu:60-69).
+ */
+int ld_state_scatter(const void* packed, int64_t packed_row_stride_bytes,
+                     const int32_t* slots, int64_t slot_stride, void* pool,
+                     int64_t pool_slot_stride_bytes, int64_t row_bytes, int64_t rows,
+                     void* stream);
+
+/*
+ * Slot-to-slot copy inside one pool for `pairs` (src, dst) pairs:
+ *   if src_slots[p] > 0 && dst_slots[p] > 0: pool[dst_slots[p]] = pool[src_slots[p]]
+ * Pairs must not write the same destination twice or read a slot another pair writes.
+ * No counterpart in the reference (which commits MTP states implicitly through the
+ * next step's `accepted`, csrc/gdn_decode.cu:154-158); it is the explicit commit /
+ * slot-lifecycle copy, with the reference's padding convention (slot <= 0).
+ */
+int ld_state_copy(void* pool, int64_t pool_slot_stride_bytes, const int32_t* src_slots,
+                  const int32_t* dst_slots, int64_t pairs, int64_t slot_bytes,
+                  void* stream);
+
+/* Message for the last non-zero return on the calling thread ("" if none). */
+const char* ld_last_error(void);
+
+/* LD_ABI_VERSION of the loaded library. */
+int ld_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIGHTDELTA_HIP_H */

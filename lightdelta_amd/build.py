@@ -1,0 +1,76 @@
+"""Build liblightdelta_hip.so (gfx950) in-tree with hipcc.
+
+Usage: python -m lightdelta_amd.build   (or __graft_entry__.build()).
+Every call recompiles; objects go to lightdelta_amd/_build/, the library next to this file.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+CSRC = PACKAGE / "csrc"
+BUILD = PACKAGE / "_build"
+LIBRARY = PACKAGE / "liblightdelta_hip.so"
+SOURCES = ("abi.hip", "gdn_decode.hip", "state_io.hip")
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fno-gpu-rdc",
+    "-Wall",
+    "-Werror=return-type",
+    # Packed fp32 VALU forms are kept out of the generated code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{ROOT / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def _hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; the HIP library needs ROCm's hipcc to build")
+    return path
+
+
+def _run(cmd: list[str]) -> None:
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(
+            "build step failed:\n" + " ".join(cmd) + "\n" + result.stdout + result.stderr
+        )
+
+
+def build(verbose: bool = False) -> Path:
+    hipcc = _hipcc()
+    BUILD.mkdir(exist_ok=True)
+    objects = []
+    commands = []
+    for name in SOURCES:
+        obj = BUILD / (Path(name).stem + ".o")
+        objects.append(obj)
+        commands.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / name), "-o", str(obj)])
+    workers = max(1, min(len(commands), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(workers) as pool:
+        list(pool.map(_run, commands))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          *map(str, objects)])
+    os.replace(tmp, LIBRARY)
+    if verbose:
+        print(f"built {LIBRARY}", file=sys.stderr)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build(verbose=True)

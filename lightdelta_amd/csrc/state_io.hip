@@ -1,0 +1,152 @@
+// Slot-indexed state-pool copies for gfx950: gather into a packed buffer, scatter back, and
+// slot-to-slot copy.  Byte-generic (fp32 SSM pool, bf16 conv pool); bit-exact.
+//
+// Semantics follow the reference's copy kernel (csrc/state_io.cu:11-27): a slot <= 0 is
+// padding; gather zero-fills rows whose slot is padding or whose `valid` flag is false,
+// scatter and copy skip padding.  Unlike the reference (one 4-byte element per thread per
+// iteration, csrc/state_io.cu:22-26), every thread here moves 128-bit vectors with eight
+// loads in flight before the first store, and each workgroup owns one 32 KiB chunk of a row.
+#include "common.h"
+
+namespace ld {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kVecsPerThread = 8;
+constexpr int64_t kVecsPerChunk = static_cast<int64_t>(kThreads) * kVecsPerThread;  // 32 KiB
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+enum Mode { kGather = 0, kScatter = 1, kCopy = 2 };
+
+struct CopyParams {
+  const char* src;        // gather: pool; scatter: packed; copy: pool
+  char* dst;              // gather: out; scatter: pool; copy: pool
+  int64_t src_stride;     // bytes between consecutive src rows / slots
+  int64_t dst_stride;     // bytes between consecutive dst rows / slots
+  const int32_t* slots;   // gather/scatter: slot per row; copy: source slot per pair
+  int64_t slot_stride;    // elements between consecutive slots entries (gather/scatter)
+  const int32_t* dst_slots;  // copy only
+  const uint8_t* valid;   // gather only; NULL = all valid
+  int64_t vecs;           // 16-byte vectors per row
+  int64_t chunks;         // chunks per row
+};
+
+template <int M>
+__global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p) {
+  const int64_t block = blockIdx.x;
+  const int64_t row = block / p.chunks;
+  const int64_t chunk = block - row * p.chunks;
+
+  const u32x4* src;
+  u32x4* dst;
+  bool live = true;
+  if (M == kGather) {
+    const int slot = p.slots[row * p.slot_stride];
+    live = slot > 0 && (p.valid == nullptr || p.valid[row] != 0);
+    src = reinterpret_cast<const u32x4*>(p.src + (live ? slot : 0) * p.src_stride);
+    dst = reinterpret_cast<u32x4*>(p.dst + row * p.dst_stride);
+  } else if (M == kScatter) {
+    const int slot = p.slots[row * p.slot_stride];
+    if (slot <= 0) return;
+    src = reinterpret_cast<const u32x4*>(p.src + row * p.src_stride);
+    dst = reinterpret_cast<u32x4*>(p.dst + slot * p.dst_stride);
+  } else {
+    const int from = p.slots[row];
+    const int to = p.dst_slots[row];
+    if (from <= 0 || to <= 0) return;
+    src = reinterpret_cast<const u32x4*>(p.src + from * p.src_stride);
+    dst = reinterpret_cast<u32x4*>(p.dst + to * p.dst_stride);
+  }
+
+  const int64_t first = chunk * kVecsPerChunk + threadIdx.x;
+  u32x4 v[kVecsPerThread];
+#pragma unroll
+  for (int i = 0; i < kVecsPerThread; ++i) {
+    const int64_t idx = first + i * kThreads;
+    v[i] = u32x4{0u, 0u, 0u, 0u};
+    if (live && idx < p.vecs) v[i] = __builtin_nontemporal_load(src + idx);
+  }
+#pragma unroll
+  for (int i = 0; i < kVecsPerThread; ++i) {
+    const int64_t idx = first + i * kThreads;
+    if (idx < p.vecs) __builtin_nontemporal_store(v[i], dst + idx);
+  }
+}
+
+int launch(const char* what, int mode, CopyParams p, int64_t rows, int64_t row_bytes,
+           void* stream) {
+  if (rows < 0 || row_bytes < 0) return fail(LD_ERR_INVALID_ARGUMENT, "negative size");
+  if (rows == 0 || row_bytes == 0) return LD_OK;
+  if ((row_bytes & 15) != 0 || (p.src_stride & 15) != 0 || (p.dst_stride & 15) != 0 ||
+      !aligned16(p.src) || !aligned16(p.dst))
+    return fail(LD_ERR_INVALID_ARGUMENT,
+                "state rows, strides and base pointers must be 16-byte aligned");
+  p.vecs = row_bytes / 16;
+  p.chunks = (p.vecs + kVecsPerChunk - 1) / kVecsPerChunk;
+  const int64_t blocks = rows * p.chunks;
+  if (blocks > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "copy too large for one launch");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  if (mode == kGather)
+    hipLaunchKernelGGL(slot_copy_kernel<kGather>, grid, dim3(kThreads), 0, s, p);
+  else if (mode == kScatter)
+    hipLaunchKernelGGL(slot_copy_kernel<kScatter>, grid, dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(slot_copy_kernel<kCopy>, grid, dim3(kThreads), 0, s, p);
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace ld
+
+extern "C" int ld_state_gather(const void* pool, int64_t pool_slot_stride_bytes,
+                               const int32_t* slots, int64_t slot_stride, const uint8_t* valid,
+                               void* out, int64_t out_row_stride_bytes, int64_t row_bytes,
+                               int64_t rows, void* stream) {
+  using namespace ld;
+  if (rows > 0 && (!pool || !slots || !out))
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_state_gather: NULL pointer");
+  CopyParams p{};
+  p.src = static_cast<const char*>(pool);
+  p.dst = static_cast<char*>(out);
+  p.src_stride = pool_slot_stride_bytes;
+  p.dst_stride = out_row_stride_bytes;
+  p.slots = slots;
+  p.slot_stride = slot_stride;
+  p.valid = valid;
+  return launch("ld_state_gather", kGather, p, rows, row_bytes, stream);
+}
+
+extern "C" int ld_state_scatter(const void* packed, int64_t packed_row_stride_bytes,
+                                const int32_t* slots, int64_t slot_stride, void* pool,
+                                int64_t pool_slot_stride_bytes, int64_t row_bytes, int64_t rows,
+                                void* stream) {
+  using namespace ld;
+  if (rows > 0 && (!pool || !slots || !packed))
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_state_scatter: NULL pointer");
+  CopyParams p{};
+  p.src = static_cast<const char*>(packed);
+  p.dst = static_cast<char*>(pool);
+  p.src_stride = packed_row_stride_bytes;
+  p.dst_stride = pool_slot_stride_bytes;
+  p.slots = slots;
+  p.slot_stride = slot_stride;
+  return launch("ld_state_scatter", kScatter, p, rows, row_bytes, stream);
+}
+
+extern "C" int ld_state_copy(void* pool, int64_t pool_slot_stride_bytes, const int32_t* src_slots,
+                             const int32_t* dst_slots, int64_t pairs, int64_t slot_bytes,
+                             void* stream) {
+  using namespace ld;
+  if (pairs > 0 && (!pool || !src_slots || !dst_slots))
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_state_copy: NULL pointer");
+  CopyParams p{};
+  p.src = static_cast<const char*>(pool);
+  p.dst = static_cast<char*>(pool);
+  p.src_stride = pool_slot_stride_bytes;
+  p.dst_stride = pool_slot_stride_bytes;
+  p.slots = src_slots;
+  p.dst_slots = dst_slots;
+  return launch("ld_state_copy", kCopy, p, pairs, slot_bytes, stream);
+}

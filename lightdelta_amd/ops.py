@@ -1,0 +1,398 @@
+"""`torch.ops.lightdelta.*` on PyTorch-ROCm, backed by the gfx950 HIP library.
+
+The three reference ops keep their schema strings verbatim (reference csrc/register.cpp:5-9)
+and are registered for the CUDA dispatch key, under which HIP tensors dispatch on ROCm; the
+fake (meta) impls return None like the reference's (python/lightdelta/ops/__init__.py:10-22).
+Argument validation raises RuntimeError with the reference's messages
+(csrc/gdn_decode.cu:367-403, csrc/state_io.cu:29-49), generalised from the hard-coded
+16 k-heads / 48 v-heads / qkv width 10240 to any H, HV with HV % H == 0 (dk = dv = 128).
+
+Additive ops (no reference counterpart):
+  copy_state(pool, src, dst)            slot -> slot copy inside one pool (MTP commit,
+                                        slot reuse), any dtype, padding slot <= 0 skipped
+  gather_slots / scatter_slots          dtype-generic gather_state / scatter_state, for the
+                                        bf16 conv-state pool and any dense-inner pool
+
+Every impl launches on the caller's current stream, allocates nothing and reads no device
+memory on the host, so it can be captured in a HIP graph.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+SCHEMAS = {
+    "decode": (
+        "decode(Tensor qkv, Tensor a, Tensor b, Tensor a_log, Tensor dt_bias, "
+        "Tensor indices, Tensor cu, Tensor accepted, Tensor(s!) state, Tensor gate, "
+        "Tensor weight, Tensor(o!) out, float eps) -> ()"
+    ),
+    "gather_state": "gather_state(Tensor pool, Tensor slots, Tensor valid, Tensor(o!) out) -> ()",
+    "scatter_state": "scatter_state(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
+    "copy_state": "copy_state(Tensor(p!) pool, Tensor src, Tensor dst) -> ()",
+    "gather_slots": "gather_slots(Tensor pool, Tensor slots, Tensor valid, Tensor(o!) out) -> ()",
+    "scatter_slots": "scatter_slots(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
+}
+
+HEAD_DIM = _lib.HEAD_DIM
+QK_SCALE = HEAD_DIM**-0.5  # reference csrc/gdn_decode.cu:417
+
+_FLOATS = (torch.float32, torch.bfloat16)
+
+
+def _require(condition: bool, message: str) -> None:
+    if not condition:
+        raise RuntimeError(message)
+
+
+def _is_gpu(t: torch.Tensor) -> bool:
+    return t.device.type == "cuda"
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _DeviceGuard:
+    """Makes `device` current for the duration of a launch (the reference's CUDAGuard)."""
+
+    __slots__ = ("index", "previous")
+
+    def __init__(self, device: torch.device):
+        self.index = device.index if device.index is not None else torch.cuda.current_device()
+        self.previous = None
+
+    def __enter__(self):
+        current = torch.cuda.current_device()
+        if current != self.index:
+            self.previous = current
+            torch.cuda.set_device(self.index)
+
+    def __exit__(self, *exc):
+        if self.previous is not None:
+            torch.cuda.set_device(self.previous)
+
+
+# ---------------------------------------------------------------------------------------
+# decode
+# ---------------------------------------------------------------------------------------
+
+
+def decode_geometry(qkv: torch.Tensor, state: torch.Tensor) -> tuple[int, int]:
+    """(H, HV) implied by qkv's width (2*H + HV)*128 and the state's head count."""
+    hv = state.shape[1] if state.dim() == 4 else 0
+    cols = qkv.shape[1] if qkv.dim() == 2 else 0
+    h2 = cols // HEAD_DIM - hv
+    h = h2 // 2
+    valid = (
+        hv > 0
+        and cols % HEAD_DIM == 0
+        and h2 > 0
+        and h2 % 2 == 0
+        and hv % h == 0
+    )
+    return (h, hv) if valid else (0, hv)
+
+
+def check_decode(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out, eps):
+    """Validation of lightdelta::decode (reference csrc/gdn_decode.cu:366-403)."""
+    _require(_is_gpu(qkv) and qkv.dtype == torch.bfloat16, "qkv must be CUDA BF16")
+    device = qkv.device
+    for t in (a, b, gate, out):
+        _require(
+            t.device == device and t.dtype == torch.bfloat16 and t.dim() > 0 and t.stride(-1) == 1,
+            "activations must be BF16 with dense rows",
+        )
+    for t in (a_log, state):
+        _require(
+            t.device == device and t.dtype == torch.float32 and t.dim() > 0 and t.stride(-1) == 1,
+            "state and A_log must be CUDA FP32 with dense rows",
+        )
+    for t in (indices, cu, accepted):
+        _require(
+            t.device == device and t.dtype == torch.int32 and t.is_contiguous(),
+            "metadata must be contiguous CUDA int32",
+        )
+    for t in (dt_bias, weight):
+        _require(
+            t.device == device and t.is_contiguous() and t.dtype in _FLOATS,
+            "weights must be contiguous FP32/BF16",
+        )
+    h, hv = decode_geometry(qkv, state)
+    _require(
+        qkv.dim() == 2 and h > 0 and qkv.stride(1) == 1,
+        "qkv must be [tokens,(2*H+HV)*128] with HV a multiple of H",
+    )
+    _require(
+        state.dim() == 4
+        and state.shape[2] == HEAD_DIM
+        and state.shape[3] == HEAD_DIM
+        and state.stride(2) == HEAD_DIM
+        and state.stride(1) == HEAD_DIM * HEAD_DIM,
+        "state must be [slots,HV,128,128]",
+    )
+    _require(
+        indices.dim() == 2 and 1 <= indices.shape[1] <= _lib.MAX_TOKENS,
+        "decode/MTP supports 1 through 4 tokens per request",
+    )
+    n = qkv.shape[0]
+    _require(
+        tuple(a.shape) == (n, hv)
+        and tuple(b.shape) == (n, hv)
+        and tuple(gate.shape) == (n, hv, HEAD_DIM)
+        and tuple(out.shape) == (n, hv, HEAD_DIM)
+        and out.is_contiguous()
+        and gate.stride(1) == HEAD_DIM,
+        "invalid activation shape or output layout",
+    )
+    _require(
+        a_log.numel() == hv and dt_bias.numel() == hv and weight.numel() == HEAD_DIM,
+        "invalid weight shapes",
+    )
+    requests = indices.shape[0]
+    _require(
+        cu.dim() == 1
+        and cu.numel() == requests + 1
+        and accepted.dim() == 1
+        and accepted.numel() == requests,
+        "invalid request metadata shapes",
+    )
+    _require(eps > 0, "norm epsilon must be positive")
+    return h, hv
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    return _lib.DTYPE_BF16 if t.dtype == torch.bfloat16 else _lib.DTYPE_F32
+
+
+def _decode_impl(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out, eps):
+    h, hv = check_decode(
+        qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out, eps
+    )
+    requests = indices.shape[0]
+    if requests == 0:
+        return
+    args = _lib.DecodeArgs(
+        qkv.data_ptr(),
+        qkv.stride(0),
+        a.data_ptr(),
+        a.stride(0),
+        b.data_ptr(),
+        b.stride(0),
+        a_log.data_ptr(),
+        dt_bias.data_ptr(),
+        _dtype_code(dt_bias),
+        _dtype_code(weight),
+        indices.data_ptr(),
+        cu.data_ptr(),
+        accepted.data_ptr(),
+        state.data_ptr(),
+        state.stride(0),
+        gate.data_ptr(),
+        gate.stride(0),
+        weight.data_ptr(),
+        out.data_ptr(),
+        requests,
+        indices.shape[1],
+        h,
+        hv,
+        QK_SCALE,
+        eps,
+    )
+    lib = _lib.load()
+    with _DeviceGuard(qkv.device):
+        _lib.check(lib.ld_gdn_decode(args, _stream(qkv.device)))
+
+
+# ---------------------------------------------------------------------------------------
+# state-pool copies
+# ---------------------------------------------------------------------------------------
+
+
+def _dense_inner(t: torch.Tensor) -> bool:
+    """Every dimension after the first is densely packed (row-major)."""
+    expected = 1
+    for size, stride in zip(reversed(t.shape[1:]), reversed(t.stride()[1:])):
+        if size != 1 and stride != expected:
+            return False
+        expected *= size
+    return True
+
+
+def _row_bytes(t: torch.Tensor) -> int:
+    count = 1
+    for size in t.shape[1:]:
+        count *= size
+    return count * t.element_size()
+
+
+def check_state_layout(pool, slots, packed, *, fp32_4d: bool):
+    """The reference's `check` (csrc/state_io.cu:29-41); `fp32_4d=False` drops the fp32 /
+    4-D requirement for the dtype-generic ops."""
+    if fp32_4d:
+        _require(
+            _is_gpu(pool)
+            and pool.dtype == torch.float32
+            and pool.dim() == 4
+            and pool.stride(3) == 1
+            and pool.stride(2) == pool.shape[3]
+            and pool.stride(1) == pool.shape[2] * pool.shape[3],
+            "pool must be CUDA FP32 with dense inner dimensions",
+        )
+    else:
+        _require(
+            _is_gpu(pool) and pool.dim() >= 1 and _dense_inner(pool),
+            "pool must be a CUDA tensor with dense inner dimensions",
+        )
+    _require(
+        slots.device == pool.device and slots.dtype == torch.int32 and slots.dim() == 1,
+        "slots must be a CUDA int32 vector",
+    )
+    _require(
+        packed.device == pool.device
+        and packed.dtype == pool.dtype
+        and packed.dim() == pool.dim()
+        and packed.shape[0] == slots.numel()
+        and tuple(packed.shape[1:]) == tuple(pool.shape[1:])
+        and _dense_inner(packed),
+        "invalid packed layout",
+    )
+
+
+def _check_valid(valid, slots, pool):
+    _require(
+        valid.device == pool.device
+        and valid.dtype == torch.bool
+        and tuple(valid.shape) == tuple(slots.shape)
+        and valid.is_contiguous(),
+        "valid must be a CUDA bool vector",
+    )
+
+
+def _gather(pool, slots, valid, out):
+    if slots.numel() == 0:
+        return
+    size = pool.element_size()
+    lib = _lib.load()
+    with _DeviceGuard(pool.device):
+        _lib.check(
+            lib.ld_state_gather(
+                pool.data_ptr(),
+                pool.stride(0) * size,
+                slots.data_ptr(),
+                slots.stride(0),
+                valid.data_ptr(),
+                out.data_ptr(),
+                out.stride(0) * size,
+                _row_bytes(pool),
+                slots.numel(),
+                _stream(pool.device),
+            )
+        )
+
+
+def _scatter(packed, slots, pool):
+    if slots.numel() == 0:
+        return
+    size = pool.element_size()
+    lib = _lib.load()
+    with _DeviceGuard(pool.device):
+        _lib.check(
+            lib.ld_state_scatter(
+                packed.data_ptr(),
+                packed.stride(0) * size,
+                slots.data_ptr(),
+                slots.stride(0),
+                pool.data_ptr(),
+                pool.stride(0) * size,
+                _row_bytes(pool),
+                slots.numel(),
+                _stream(pool.device),
+            )
+        )
+
+
+def _gather_state_impl(pool, slots, valid, out):
+    check_state_layout(pool, slots, out, fp32_4d=True)
+    _check_valid(valid, slots, pool)
+    _gather(pool, slots, valid, out)
+
+
+def _scatter_state_impl(packed, slots, pool):
+    check_state_layout(pool, slots, packed, fp32_4d=True)
+    _scatter(packed, slots, pool)
+
+
+def _gather_slots_impl(pool, slots, valid, out):
+    check_state_layout(pool, slots, out, fp32_4d=False)
+    _check_valid(valid, slots, pool)
+    _gather(pool, slots, valid, out)
+
+
+def _scatter_slots_impl(packed, slots, pool):
+    check_state_layout(pool, slots, packed, fp32_4d=False)
+    _scatter(packed, slots, pool)
+
+
+def check_copy(pool, src, dst):
+    _require(
+        _is_gpu(pool) and pool.dim() >= 1 and _dense_inner(pool),
+        "pool must be a CUDA tensor with dense inner dimensions",
+    )
+    for t in (src, dst):
+        _require(
+            t.device == pool.device and t.dtype == torch.int32 and t.dim() == 1 and t.is_contiguous(),
+            "src and dst must be contiguous CUDA int32 vectors",
+        )
+    _require(src.numel() == dst.numel(), "src and dst must have the same length")
+
+
+def _copy_state_impl(pool, src, dst):
+    check_copy(pool, src, dst)
+    if src.numel() == 0:
+        return
+    lib = _lib.load()
+    with _DeviceGuard(pool.device):
+        _lib.check(
+            lib.ld_state_copy(
+                pool.data_ptr(),
+                pool.stride(0) * pool.element_size(),
+                src.data_ptr(),
+                dst.data_ptr(),
+                src.numel(),
+                _row_bytes(pool),
+                _stream(pool.device),
+            )
+        )
+
+
+# ---------------------------------------------------------------------------------------
+# registration
+# ---------------------------------------------------------------------------------------
+
+_IMPLS = {
+    "decode": _decode_impl,
+    "gather_state": _gather_state_impl,
+    "scatter_state": _scatter_state_impl,
+    "copy_state": _copy_state_impl,
+    "gather_slots": _gather_slots_impl,
+    "scatter_slots": _scatter_slots_impl,
+}
+
+
+def _fake(*args, **kwargs):
+    return None
+
+
+def _register() -> torch.library.Library:
+    library = torch.library.Library("lightdelta", "DEF")
+    for name, schema in SCHEMAS.items():
+        library.define(schema)
+        library.impl(name, _IMPLS[name], "CUDA")
+        torch.library.register_fake(f"lightdelta::{name}", _fake, lib=library)
+    return library
+
+
+_LIBRARY = _register()

@@ -1,0 +1,36 @@
+"""numpy restatement of the slot-indexed state-pool copies -- test infrastructure.
+
+Semantics (reference csrc/state_io.cu:16-26; slot <= 0 is padding):
+  gather   out[r] = pool[slot_r] if slot_r > 0 and valid[r] else 0
+  scatter  pool[slot_r] = packed[r] for slot_r > 0; other rows skipped
+  copy     pool[dst_p] = pool[src_p] when src_p > 0 and dst_p > 0 (all reads before writes)
+Arrays may have any dtype; comparisons against the HIP kernels are bit-exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def gather(pool: np.ndarray, slots: np.ndarray, valid: np.ndarray | None) -> np.ndarray:
+    out = np.zeros((len(slots), *pool.shape[1:]), dtype=pool.dtype)
+    for r, slot in enumerate(slots):
+        if slot > 0 and (valid is None or bool(valid[r])):
+            out[r] = pool[slot]
+    return out
+
+
+def scatter(packed: np.ndarray, slots: np.ndarray, pool: np.ndarray) -> np.ndarray:
+    result = pool.copy()
+    for r, slot in enumerate(slots):
+        if slot > 0:
+            result[slot] = packed[r]
+    return result
+
+
+def copy(pool: np.ndarray, src: np.ndarray, dst: np.ndarray) -> np.ndarray:
+    result = pool.copy()
+    for s, d in zip(src, dst):
+        if s > 0 and d > 0:
+            result[d] = pool[s]
+    return result

@@ -1,0 +1,80 @@
+"""The C-ABI library loads and exports every entry point include/lightdelta_hip.h declares
+(no GPU calls), and its argument checks fail with the documented codes without launching."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from lightdelta_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "lightdelta_hip.h"
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ld_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_functions() == {
+        "ld_gdn_decode", "ld_state_gather", "ld_state_scatter", "ld_state_copy",
+        "ld_last_error", "ld_abi_version",
+    }
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(_lib.SIGNATURES) == declared_functions()
+    assert lib.ld_abi_version() == _lib.ABI_VERSION
+
+
+def test_decode_args_layout_matches_header():
+    """ctypes mirror of ld_gdn_decode_args: same field names in the same order."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct ld_gdn_decode_args \{(.*?)\}", text, flags=re.S).group(1)
+    fields = re.findall(r"(\w+);", body)
+    assert fields == [name for name, _ in _lib.DecodeArgs._fields_]
+
+
+@pytest.mark.parametrize("width,heads,eps,message", [
+    (0, (16, 32), 1e-6, "1 through 4 tokens"),
+    (5, (16, 32), 1e-6, "1 through 4 tokens"),
+    (1, (16, 24), 1e-6, "multiple of num_k_heads"),
+    (1, (16, 32), 0.0, "epsilon must be positive"),
+])
+def test_decode_rejects_bad_arguments_without_launching(width, heads, eps, message):
+    lib = _lib.load()
+    args = _lib.DecodeArgs()
+    args.num_requests = 1
+    args.width = width
+    args.num_k_heads, args.num_v_heads = heads
+    args.eps = eps
+    args.scale = 128 ** -0.5
+    code = lib.ld_gdn_decode(ctypes.byref(args), None)
+    assert code == 1
+    assert message in lib.ld_last_error().decode()
+
+
+def test_empty_work_is_a_no_op():
+    lib = _lib.load()
+    args = _lib.DecodeArgs()
+    args.num_requests = 0
+    args.width = 1
+    args.num_k_heads, args.num_v_heads = 16, 32
+    args.eps = 1e-6
+    assert lib.ld_gdn_decode(ctypes.byref(args), None) == 0
+    assert lib.ld_state_copy(None, 0, None, None, 0, 2048, None) == 0
+    assert lib.ld_state_gather(None, 0, None, 1, None, None, 0, 2048, 0, None) == 0
+
+
+def test_copy_rejects_misaligned_rows():
+    lib = _lib.load()
+    code = lib.ld_state_gather(16, 24, 32, 1, None, 48, 24, 24, 1, None)
+    assert code == 1 and "16-byte aligned" in lib.ld_last_error().decode()

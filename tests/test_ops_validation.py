@@ -1,0 +1,125 @@
+"""Argument validation of the torch.ops.lightdelta impls raises the reference's messages
+(csrc/gdn_decode.cu:367-403, csrc/state_io.cu:29-49).  Runs on CPU: tensors live on the
+meta device and the impls' device predicate is pointed at it, so no kernel is reached."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from lightdelta_amd import ops
+
+
+@pytest.fixture
+def meta(monkeypatch):
+    monkeypatch.setattr(ops, "_is_gpu", lambda t: t.device.type == "meta")
+    return torch.device("meta")
+
+
+def decode_args(device, n=4, h=16, hv=32, width=1, slots=10):
+    def t(*shape, dtype=torch.bfloat16):
+        return torch.empty(*shape, dtype=dtype, device=device)
+
+    qkvz = t(n, (2 * h + hv) * 128 + hv * 128)
+    ba = t(n, 2 * hv)
+    return dict(
+        qkv=qkvz[:, : (2 * h + hv) * 128], a=ba[:, hv:], b=ba[:, :hv],
+        a_log=t(hv, dtype=torch.float32), dt_bias=t(hv, dtype=torch.float32),
+        indices=t(n // width, width, dtype=torch.int32), cu=t(n // width + 1, dtype=torch.int32),
+        accepted=t(n // width, dtype=torch.int32), state=t(slots, hv, 128, 128, dtype=torch.float32),
+        gate=qkvz[:, (2 * h + hv) * 128:].view(n, hv, 128), weight=t(128), out=t(n, hv, 128),
+        eps=1e-6,
+    )
+
+
+def check(args):
+    return ops.check_decode(*args.values())
+
+
+def test_valid_geometries(meta):
+    assert check(decode_args(meta)) == (16, 32)
+    assert check(decode_args(meta, h=16, hv=48)) == (16, 48)
+    assert check(decode_args(meta, h=4, hv=8, width=4)) == (4, 8)
+
+
+@pytest.mark.parametrize("mutate,message", [
+    (lambda d, m: d.update(qkv=d["qkv"].float()), "qkv must be CUDA BF16"),
+    (lambda d, m: d.update(qkv=torch.empty(4, 8192, dtype=torch.bfloat16)), "qkv must be CUDA BF16"),
+    (lambda d, m: d.update(a=d["a"].float()), "activations must be BF16"),
+    (lambda d, m: d.update(gate=torch.empty(4, 32, 256, dtype=torch.bfloat16, device=m)[..., ::2]),
+     "activations must be BF16 with dense rows"),
+    (lambda d, m: d.update(out=torch.empty(32, 4, 128, dtype=torch.bfloat16, device=m).transpose(0, 1)),
+     "invalid activation shape or output layout"),
+    (lambda d, m: d.update(state=d["state"].double()), "state and A_log must be CUDA FP32"),
+    (lambda d, m: d.update(a_log=d["a_log"].bfloat16()), "state and A_log must be CUDA FP32"),
+    (lambda d, m: d.update(indices=d["indices"].long()), "metadata must be contiguous CUDA int32"),
+    (lambda d, m: d.update(cu=torch.empty(10, dtype=torch.int32, device=m)[::2]),
+     "metadata must be contiguous CUDA int32"),
+    (lambda d, m: d.update(dt_bias=d["dt_bias"].half()), "weights must be contiguous FP32/BF16"),
+    (lambda d, m: d.update(qkv=torch.empty(4, 10000, dtype=torch.bfloat16, device=m)), "qkv must be"),
+    (lambda d, m: d.update(state=torch.empty(4, 32, 128, 64, device=m)), "state must be"),
+    (lambda d, m: d.update(state=torch.empty(4, 128, 32, 128, device=m).transpose(1, 2)),
+     "state must be"),
+    (lambda d, m: d.update(indices=torch.empty(1, 5, dtype=torch.int32, device=m),
+                           cu=torch.empty(2, dtype=torch.int32, device=m),
+                           accepted=torch.empty(1, dtype=torch.int32, device=m)),
+     "1 through 4 tokens"),
+    (lambda d, m: d.update(a=torch.empty(4, 31, dtype=torch.bfloat16, device=m)),
+     "invalid activation shape"),
+    (lambda d, m: d.update(out=torch.empty(4, 32, 256, dtype=torch.bfloat16, device=m)[..., :128]),
+     "activations must be BF16 with dense rows|invalid activation shape"),
+    (lambda d, m: d.update(weight=torch.empty(64, dtype=torch.bfloat16, device=m)),
+     "invalid weight shapes"),
+    (lambda d, m: d.update(cu=torch.empty(4, dtype=torch.int32, device=m)),
+     "invalid request metadata shapes"),
+    (lambda d, m: d.update(eps=0.0), "norm epsilon must be positive"),
+])
+def test_decode_validation_messages(meta, mutate, message):
+    args = decode_args(meta)
+    mutate(args, meta)
+    with pytest.raises(RuntimeError, match=message):
+        check(args)
+
+
+def test_state_io_validation_messages(meta):
+    pool = torch.empty(8, 4, 128, 128, device=meta)
+    slots = torch.empty(3, dtype=torch.int32, device=meta)
+    packed = torch.empty(3, 4, 128, 128, device=meta)
+    ops.check_state_layout(pool, slots, packed, fp32_4d=True)
+    with pytest.raises(RuntimeError, match="pool must be CUDA FP32"):
+        ops.check_state_layout(pool.bfloat16(), slots, packed, fp32_4d=True)
+    with pytest.raises(RuntimeError, match="pool must be CUDA FP32"):
+        ops.check_state_layout(torch.empty(8, 4, 128, 256, device=meta)[..., :128], slots, packed,
+                               fp32_4d=True)
+    with pytest.raises(RuntimeError, match="slots must be a CUDA int32 vector"):
+        ops.check_state_layout(pool, slots.long(), packed, fp32_4d=True)
+    with pytest.raises(RuntimeError, match="invalid packed layout"):
+        ops.check_state_layout(pool, slots, packed[:2], fp32_4d=True)
+    with pytest.raises(RuntimeError, match="valid must be a CUDA bool vector"):
+        ops._check_valid(torch.empty(3, dtype=torch.int32, device=meta), slots, pool)
+    conv = torch.empty(8, 4, 8192, dtype=torch.bfloat16, device=meta)
+    ops.check_state_layout(conv, slots, torch.empty(3, 4, 8192, dtype=torch.bfloat16, device=meta),
+                           fp32_4d=False)
+    with pytest.raises(RuntimeError, match="invalid packed layout"):
+        ops.check_state_layout(conv, slots, torch.empty(3, 4, 8192, device=meta), fp32_4d=False)
+    with pytest.raises(RuntimeError, match="same length"):
+        ops.check_copy(pool, slots, slots[:2])
+
+
+def test_cpu_tensors_are_rejected():
+    args = decode_args("cpu")
+    with pytest.raises(RuntimeError, match="qkv must be CUDA BF16"):
+        check(args)
+
+
+def test_schemas_match_reference_strings():
+    expected = {
+        "decode": "decode(Tensor qkv, Tensor a, Tensor b, Tensor a_log, Tensor dt_bias, "
+                  "Tensor indices, Tensor cu, Tensor accepted, Tensor(s!) state, Tensor gate, "
+                  "Tensor weight, Tensor(o!) out, float eps) -> ()",
+        "gather_state": "gather_state(Tensor pool, Tensor slots, Tensor valid, Tensor(o!) out) -> ()",
+        "scatter_state": "scatter_state(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
+    }
+    for name, schema in expected.items():
+        assert ops.SCHEMAS[name] == schema
+        assert str(getattr(torch.ops.lightdelta, name).default._schema) == "lightdelta::" + schema
