@@ -1,0 +1,291 @@
+"""Benchmark of the fused GDN decode step on one MI355X.
+
+Workload (the headline configuration): one Qwen3-Next-shape GDN decode layer, batch 32,
+16 qk heads / 32 v heads, dk = dv = 128, bf16 activations, fp32 state pool of 256 slots x
+32 heads x 128 x 128 (2 MiB per slot); batch rows map to random distinct slot ids and the
+state is updated in place for consecutive steps.  A step is one `torch.ops.lightdelta.decode`
+launch over the batch.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Timed region: K steps captured in one HIP graph and replayed once, bracketed by
+torch.cuda.synchronize(); inputs are resident in HBM before it starts.  Printed: ONE JSON
+line with steps/s (`value`), tokens/s, the roofline of the decode kernel and a CPU
+baseline.
+
+Roofline: algorithmic bytes per launch = B * HV * 128 * 128 * 4 B * 2 (read + write of every
+state tile) = 134,217,728 B; `achieved` divides that by the kernel's average duration,
+measured with HIP events around each of K eager launches on the launch stream right after
+the timed region.  `traffic` (HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE,
+scaled by the counters' reading on a plain copy of known size) is read from
+profiles/gdn_decode_b32_traffic.json when that measurement exists, else null.
+A second, cache-cold figure rotates 16 disjoint slot sets through a 1024-slot (2 GiB) pool
+so that the working set exceeds the 256 MB Infinity Cache.
+
+CPU baseline: the reference's packed Torch path (index_select gather, unfused GDN,
+index_copy_ write-back; oracle/decode.py) on the host cores at the same shapes, timed for a
+bounded number of steps.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "GDN decode steps/s + achieved HBM TB/s on state R/W, B=32, 32 v-heads"
+BATCH, H, HV, DIM, POOL = 32, 16, 32, 128, 256
+STATE_BYTES = BATCH * HV * DIM * DIM * 4 * 2  # one read + one write per state tile
+HBM_PEAK_GBS = 8000.0
+ORDER = ("qkv", "a", "b", "a_log", "dt_bias", "slots", "cu", "accepted", "pool", "gate",
+         "weight", "out")
+TRAFFIC_FILE = ROOT / "profiles" / "gdn_decode_b32_traffic.json"
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=64)
+    p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--cpu-seconds", type=float, default=15.0,
+                   help="bound on the CPU-baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-cold", action="store_true")
+    p.add_argument("--no-graph", action="store_true",
+                   help="time K eager launches instead of one K-step graph replay")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run the plain slot-copy kernel (64 MiB read + 64 MiB write per "
+                        "launch) K times, for scaling rocprofv3 byte counters")
+    return p.parse_args()
+
+
+def events():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def capture(fn, steps):
+    """One HIP graph holding `steps` calls of fn (warmed up on a side stream first)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            fn()
+    return graph
+
+
+def per_launch_us(fn, launches):
+    """Mean / median kernel duration from HIP events around each eager launch."""
+    import torch
+
+    pairs = [events() for _ in range(launches)]
+    for start, end in pairs:
+        start.record()
+        fn()
+        end.record()
+    torch.cuda.synchronize()
+    times = sorted(s.elapsed_time(e) * 1000.0 for s, e in pairs)
+    return sum(times) / len(times), times[len(times) // 2]
+
+
+def timed_replay(graph):
+    import torch
+
+    start, end = events()
+    torch.cuda.synchronize()
+    start.record()
+    graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1000.0
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The reference Torch path on the host CPU, same shapes, bounded sample."""
+    import torch
+
+    from lightdelta_amd.workloads import decode_case
+    from oracle.decode import packed_reference_step
+
+    threads = torch.get_num_threads()
+    case = decode_case(BATCH, 1, num_k_heads=H, num_v_heads=HV, pool_slots=POOL, seed=0,
+                       device="cpu")
+    scratch = case["pool"].new_empty((1 + BATCH, *case["pool"].shape[1:]))
+    args = [case[k] for k in ORDER]
+    packed_reference_step(*args, 1e-6, scratch=scratch)  # warm-up
+    times = []
+    deadline = time.perf_counter() + seconds
+    while len(times) < 3 or (time.perf_counter() < deadline and len(times) < 200):
+        t0 = time.perf_counter()
+        packed_reference_step(*args, 1e-6, scratch=scratch)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    median = times[len(times) // 2]
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(1.0 / median, 3),
+        "unit": "steps/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(times)} steps of the packed Torch reference path (index_select gather, "
+                  f"unfused GDN, index_copy_ write-back) at B=32, 16/32 heads, 256-slot pool; "
+                  f"median step {median * 1e3:.1f} ms; {cpu}",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for {args.gpus}); this build has no "
+              "multi-GPU path -- the op needs no cross-GPU exchange and shards by slots or "
+              "heads outside it.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import lightdelta_amd  # noqa: F401  (registers torch.ops.lightdelta)
+    from lightdelta_amd import _lib
+    from lightdelta_amd.workloads import decode_case
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    device = torch.device("cuda:0")
+    torch.manual_seed(0)
+
+    if args.calibrate_copy:
+        pool = torch.empty(2 * BATCH + 1, HV, DIM, DIM, device=device).normal_()
+        src = torch.arange(1, BATCH + 1, device=device, dtype=torch.int32)
+        dst = src + BATCH
+        copy = lambda: torch.ops.lightdelta.copy_state(pool, src, dst)  # noqa: E731
+        for _ in range(args.warmup):
+            copy()
+        mean_us, median_us = per_launch_us(copy, args.steps)
+        print(json.dumps({"calibration": "copy_state", "bytes_read": STATE_BYTES // 2,
+                          "bytes_written": STATE_BYTES // 2, "launches": args.steps,
+                          "mean_us": round(mean_us, 3),
+                          "achieved_GBps": round(STATE_BYTES / mean_us / 1e3, 1)}))
+        return
+
+    case = decode_case(BATCH, 1, num_k_heads=H, num_v_heads=HV, pool_slots=POOL, seed=0,
+                       device=device)
+    op_args = [case[k] for k in ORDER]
+    step = lambda: torch.ops.lightdelta.decode(*op_args, 1e-6)  # noqa: E731
+
+    for _ in range(args.warmup):
+        step()
+    if args.no_graph:
+        torch.cuda.synchronize()
+        start, end = events()
+        start.record()
+        for _ in range(args.steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        elapsed = start.elapsed_time(end) / 1000.0
+    else:
+        graph = capture(step, args.steps)
+        graph.replay()  # upload + warm the graph (untimed)
+        torch.cuda.synchronize()
+        elapsed = timed_replay(graph)  # exactly K steps
+    ms_per_step = elapsed * 1000.0 / args.steps
+    steps_per_s = args.steps / elapsed
+
+    mean_us, median_us = per_launch_us(step, args.steps)
+    achieved = STATE_BYTES / (mean_us * 1e-6) / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(steps_per_s, 1),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "GDN decode layer, B=32, 16 qk / 32 v heads, dk=dv=128, bf16 "
+                        "activations, fp32 state pool 256 x 32 x 128 x 128, random distinct "
+                        "slots, in-place consecutive steps, "
+                        + ("eager launches" if args.no_graph else "HIP-graph replay"),
+            "batch": BATCH, "qk_heads": H, "v_heads": HV, "head_dim": DIM, "pool_slots": POOL,
+        },
+        "tokens_per_s": round(steps_per_s * BATCH, 1),
+        "state_TBps": round(STATE_BYTES * steps_per_s / 1e12, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "gdn_decode_kernel",
+            "kernel_mean_us": round(mean_us, 3),
+            "kernel_median_us": round(median_us, 3),
+            "algorithmic_bytes": STATE_BYTES,
+        },
+    }
+
+    if not args.no_cold:
+        # Cache-cold variant: 16 disjoint slot sets rotated through a 1024-slot pool.
+        big = torch.empty(1024, HV, DIM, DIM, device=device).normal_(0.0, 0.02)
+        perm = torch.randperm(1023, device=device)[: 16 * BATCH] + 1
+        sets = [perm[i * BATCH:(i + 1) * BATCH].to(torch.int32).view(BATCH, 1) for i in range(16)]
+        cold_args = list(op_args)
+        cold_args[ORDER.index("pool")] = big
+
+        def cold_pass():
+            for slots in sets:
+                cold_args[ORDER.index("slots")] = slots
+                torch.ops.lightdelta.decode(*cold_args, 1e-6)
+
+        cold_graph = capture(cold_pass, max(1, args.steps // 16))
+        cold_graph.replay()
+        cold_elapsed = timed_replay(cold_graph)
+        cold_steps = 16 * max(1, args.steps // 16)
+        cold_rate = cold_steps / cold_elapsed
+        result["cold"] = {
+            "workload": "same step, 16 disjoint slot sets rotated through a 1024-slot (2 GiB) "
+                        "pool; working set exceeds the 256 MB Infinity Cache",
+            "steps_per_s": round(cold_rate, 1),
+            "state_TBps": round(STATE_BYTES * cold_rate / 1e12, 3),
+            "frac": round(STATE_BYTES * cold_rate / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        del big
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 1
+#define LD_ABI_VERSION 2
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -27,6 +27,13 @@ extern "C" {
 
 #define LD_DTYPE_F32 0
 #define LD_DTYPE_BF16 1
+
+/* State cache policy of ld_gdn_decode.  KEEP: ordinary loads and stores, so a working set
+ * that fits the 256 MB Infinity Cache stays there for the next step (one layer stepped
+ * repeatedly).  STREAM: non-temporal loads and stores, for working sets far larger than the
+ * caches (many layers between two steps of one layer). */
+#define LD_CACHE_KEEP 0
+#define LD_CACHE_STREAM 1
 
 /* Head geometry fixed by the kernels: dk = dv = 128. */
 #define LD_HEAD_DIM 128
@@ -81,8 +88,9 @@ typedef struct ld_gdn_decode_args {
   int32_t width;
   int32_t num_k_heads;
   int32_t num_v_heads;
-  float scale; /* q scale, 128^-0.5 in the reference (csrc/gdn_decode.cu:417) */
-  float eps;   /* gated RMSNorm epsilon, > 0 */
+  float scale;          /* q scale, 128^-0.5 in the reference (csrc/gdn_decode.cu:417) */
+  float eps;            /* gated RMSNorm epsilon, > 0 */
+  int32_t cache_policy; /* LD_CACHE_KEEP or LD_CACHE_STREAM (no effect on results) */
 } ld_gdn_decode_args;
 
 /* Fused decode step; see ld_gdn_decode_args.  Replaces lightdelta::decode

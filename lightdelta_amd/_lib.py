@@ -15,9 +15,11 @@ from pathlib import Path
 import torch  # noqa: F401  -- must precede the CDLL load (see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("liblightdelta_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+CACHE_KEEP = 0
+CACHE_STREAM = 1
 HEAD_DIM = 128
 MAX_TOKENS = 4
 
@@ -55,6 +57,7 @@ class DecodeArgs(ctypes.Structure):
         ("num_v_heads", _c_i32),
         ("scale", ctypes.c_float),
         ("eps", ctypes.c_float),
+        ("cache_policy", _c_i32),
     ]
 
 

@@ -14,12 +14,15 @@
 //   * Inside a wave, the 16 lanes of a DPP row span one 512-byte K row: lane kq holds
 //     k = 4kq..4kq+3 and 64+4kq..64+4kq+3 (two 16-byte pieces); the 4 DPP rows of the wave
 //     take 4 consecutive V rows.  One global_load_dwordx4 therefore reads four half rows,
-//     i.e. eight whole 128-byte lines, and a lane keeps 8 V rows x 8 K values = 64 fp32
+//     i.e. eight whole 128-byte lines.  A lane keeps 8 V rows x 8 K values = 64 fp32
 //     (16 x 128-bit loads) of the tile in VGPRs for the whole step.
-//   * All 16 tile loads are issued before any arithmetic; the per-row dot products
-//     S k^ and S q^ are 8 products per lane followed by a DPP reduce-scatter inside the
-//     16-lane row (row_mirror, row_half_mirror, quad_perm), so no LDS round trip and no
-//     cross-row lane traffic is needed for the contractions.
+//   * All 16 tile loads are issued up front, then the slice is processed in 4 chunks of
+//     8 V rows in load order: each chunk waits only for its own 4 loads, runs every token
+//     on its rows and stores them, so arithmetic on chunk c overlaps the loads of the later
+//     chunks and the stores of the earlier ones.
+//   * Row dot products S k^ and S q^ are 8 products per lane plus a 4-step DPP butterfly
+//     over the 16-lane row (quad_perm, row_half_mirror, row_mirror); every lane ends with
+//     the full sums, so no LDS round trip and no broadcast step is needed.
 //   * T <= 4 tokens (MTP verify) reuse the registers: 1 tile read, T tile writes.
 #include "common.h"
 
@@ -28,8 +31,9 @@ namespace {
 
 constexpr int kDim = LD_HEAD_DIM;
 constexpr int kThreads = 256;
+constexpr int kWaves = 4;
 constexpr int kRowsPerWave = 32;
-constexpr int kRowGroups = 8;  // V rows per lane
+constexpr int kPieces = 16;        // 16-byte pieces of the tile per lane
 constexpr int kMaxTokens = LD_MAX_TOKENS;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -65,52 +69,36 @@ __device__ __forceinline__ float load_param(const void* p, int i, bool bf16) {
               : static_cast<const float*>(p)[i];
 }
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// The per-token scalars and norms below use the hardware approximations (v_exp_f32,
+// v_log_f32, v_rcp_f32, v_rsq_f32; about 1 ulp): they sit between the arrival of the data
+// and the first state update of every wave, where exactly rounded sequences cost ~1 us per
+// step, and their error (~1e-7 relative) is four orders of magnitude below the bf16 output
+// resolution.
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
 
-// softplus with the threshold torch's F.softplus uses (beta=1, threshold=20).
-__device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid(float x) { return fast_rcp(1.0f + __expf(-x)); }
 
-// Reduce-scatter of 8 per-row partial sums over the 16 lanes of a DPP row: each step pairs
-// lanes that differ in one bit of kq (bit 3 via row_mirror, bit 2 via row_half_mirror,
-// bits 1 and 0 via quad_perm); the lane with the bit clear keeps the lower half of its list,
-// the partner the upper half.  Lane kq ends with the full sum for row group kq >> 1.
-__device__ __forceinline__ float reduce_scatter8(const float (&p)[kRowGroups], int kq) {
-  const bool b3 = kq & 8, b2 = kq & 4, b1 = kq & 2;
-  float q4[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const float keep = b3 ? p[m + 4] : p[m];
-    const float send = b3 ? p[m] : p[m + 4];
-    q4[m] = keep + dpp<kDppRowMirror>(send);
-  }
-  float q2[2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const float keep = b2 ? q4[m + 2] : q4[m];
-    const float send = b2 ? q4[m] : q4[m + 2];
-    q2[m] = keep + dpp<kDppRowHalfMirror>(send);
-  }
-  const float keep = b1 ? q2[1] : q2[0];
-  const float send = b1 ? q2[0] : q2[1];
-  const float s = keep + dpp<kDppQuadXor2>(send);
-  return s + dpp<kDppQuadXor1>(s);
+__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
+
+// softplus with the threshold torch's F.softplus uses (beta=1, threshold=20); log1p(y) for
+// small y = e^x by its series, where log(1 + y) would lose y to the rounding of 1 + y.
+__device__ __forceinline__ float softplus(float x) {
+  if (x > 20.0f) return x;
+  const float y = __expf(x);
+  return y < 1e-4f ? y * (1.0f - 0.5f * y) : __logf(1.0f + y);
 }
 
-// Inverse of reduce_scatter8's placement: lane kq holds the value of row group kq >> 1;
-// afterwards every lane holds all 8 row-group values of its DPP row, in row-group order.
-__device__ __forceinline__ void all_gather8(float x, int kq, float (&out)[kRowGroups]) {
-  const bool b3 = kq & 8, b2 = kq & 4, b1 = kq & 2;
-  const float o1 = dpp<kDppQuadXor2>(x);
-  const float g2[2] = {b1 ? o1 : x, b1 ? x : o1};
-  const float h0 = dpp<kDppRowHalfMirror>(g2[0]);
-  const float h1 = dpp<kDppRowHalfMirror>(g2[1]);
-  const float g4[4] = {b2 ? h0 : g2[0], b2 ? h1 : g2[1], b2 ? g2[0] : h0, b2 ? g2[1] : h1};
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const float o = dpp<kDppRowMirror>(g4[m]);
-    out[m] = b3 ? o : g4[m];
-    out[m + 4] = b3 ? g4[m] : o;
-  }
+// Sums over the 16 lanes of a DPP row; every lane of the row receives the totals.
+__device__ __forceinline__ void row_sum2(float& x, float& y) {
+  x += dpp<kDppQuadXor1>(x);
+  y += dpp<kDppQuadXor1>(y);
+  x += dpp<kDppQuadXor2>(x);
+  y += dpp<kDppQuadXor2>(y);
+  x += dpp<kDppRowHalfMirror>(x);
+  y += dpp<kDppRowHalfMirror>(y);
+  x += dpp<kDppRowMirror>(x);
+  y += dpp<kDppRowMirror>(y);
 }
 
 // Byte offset of a lane's 16-byte piece j of the tile, relative to its first piece: piece j
@@ -131,48 +119,133 @@ __device__ __forceinline__ float dot8(f32x4 s0, f32x4 s1, f32x4 x0, f32x4 x1) {
   return acc;
 }
 
-// One token of the recurrence on the lane's 8x8 slice of the tile:
+// Normalised k^ and q^ pieces a lane multiplies with (k = 4kq.. and 64+4kq..).
+struct Vectors {
+  f32x4 k0, k1, q0, q1;
+};
+
+// qk[0] holds q^, qk[1] holds k^, as 32 float4 pieces each.
+__device__ __forceinline__ Vectors load_vectors(const f32x4 (&qk)[2][kDim / 4], int kq) {
+  Vectors x;
+  x.q0 = qk[0][kq];
+  x.q1 = qk[0][16 + kq];
+  x.k0 = qk[1][kq];
+  x.k1 = qk[1][16 + kq];
+  return x;
+}
+
+// Raw bf16 activations of one token as a lane needs them: four q and four k pieces of 2
+// bf16 each (k = 4kq..4kq+3 and 64+4kq..), one v value (column v_col of the row), a and b.
+struct TokenIn {
+  uint32_t q[4], k[4];
+  uint16_t v, a, b;
+};
+
+__device__ __forceinline__ TokenIn load_token(const DecodeParams& p, int64_t token, int q_col,
+                                              int k_col, int v_col, int head, int kq) {
+  const uint16_t* row = p.qkv + token * p.qkv_row;
+  TokenIn in;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int off = (e == 0 ? 0 : 64) + kq * 4;
+    in.q[2 * e] = row[q_col + off] | (static_cast<uint32_t>(row[q_col + off + 1]) << 16);
+    in.q[2 * e + 1] = row[q_col + off + 2] | (static_cast<uint32_t>(row[q_col + off + 3]) << 16);
+    in.k[2 * e] = row[k_col + off] | (static_cast<uint32_t>(row[k_col + off + 1]) << 16);
+    in.k[2 * e + 1] = row[k_col + off + 2] | (static_cast<uint32_t>(row[k_col + off + 3]) << 16);
+  }
+  in.v = row[v_col];
+  in.a = p.a[token * p.a_row + head];
+  in.b = p.b[token * p.b_row + head];
+  return in;
+}
+
+// A token's q^ / k^ pieces of this lane (q^ scaled by `scale`), decay and beta.
+struct Staged {
+  f32x4 q0, q1, k0, k1;
+  float decay, beta;
+};
+
+// q/k L2 norm over the 16 lanes of the DPP row (each holds 8 of the 128 values), then the
+// gates: decay = exp(-exp(A_log) * softplus(a + dt_bias)), beta = sigmoid(b).
+__device__ __forceinline__ Staged stage_token(const TokenIn& in, float a_log, float dt_bias,
+                                              float scale) {
+  float qf[8], kf[8];
+  float qq = 0.0f, kk = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    qf[2 * e] = bf16_to_f32(static_cast<uint16_t>(in.q[e]));
+    qf[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(in.q[e] >> 16));
+    kf[2 * e] = bf16_to_f32(static_cast<uint16_t>(in.k[e]));
+    kf[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(in.k[e] >> 16));
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    qq = fmaf(qf[e], qf[e], qq);
+    kk = fmaf(kf[e], kf[e], kk);
+  }
+  row_sum2(qq, kk);
+  const float rq = fast_rsqrt(qq + 1e-6f);
+  const float rk = fast_rsqrt(kk + 1e-6f);
+  Staged x;
+  x.q0 = f32x4{qf[0] * rq, qf[1] * rq, qf[2] * rq, qf[3] * rq} * scale;
+  x.q1 = f32x4{qf[4] * rq, qf[5] * rq, qf[6] * rq, qf[7] * rq} * scale;
+  x.k0 = f32x4{kf[0] * rk, kf[1] * rk, kf[2] * rk, kf[3] * rk};
+  x.k1 = f32x4{kf[4] * rk, kf[5] * rk, kf[6] * rk, kf[7] * rk};
+  x.decay = __expf(-__expf(a_log) * softplus(bf16_to_f32(in.a) + dt_bias));
+  x.beta = sigmoid(bf16_to_f32(in.b));
+  return x;
+}
+
+// One token on chunk C of the lane's slice (pieces 4C..4C+3 = V rows row0 and row0 + 4,
+// whose v values are v0 and v1):
 //   S <- decay*S ; delta = (v - S k^) * beta ; S += delta k^ ; raw = bf16(S q^)
-// then the updated slice is stored to `dst_tile` (skipped for a padding slot, NULL).
-__device__ __forceinline__ void token_step(f32x4 (&s)[2 * kRowGroups], const float* q,
-                                           const float* k, float v_row, float* o,
-                                           float decay, float beta, int kq, int my_row,
-                                           char* dst_tile, uint32_t lane_bytes) {
-  const f32x4 k0 = *reinterpret_cast<const f32x4*>(k + kq * 4);
-  const f32x4 k1 = *reinterpret_cast<const f32x4*>(k + 64 + kq * 4);
-  const f32x4 q0 = *reinterpret_cast<const f32x4*>(q + kq * 4);
-  const f32x4 q1 = *reinterpret_cast<const f32x4*>(q + 64 + kq * 4);
-
-  float part[kRowGroups];
+// The updated pieces are stored to `dst_tile` (NULL: padding slot, nothing stored) and the
+// two rows' raw outputs go to LDS (one lane per row).
+template <int C, bool Stream>
+__device__ __forceinline__ void chunk_step(f32x4 (&s)[kPieces], const Vectors& x, float v0,
+                                           float v1, float* o, float decay, float beta,
+                                           int kq, int row0, char* dst_tile,
+                                           uint32_t lane_bytes) {
+  constexpr int j0 = 4 * C;
 #pragma unroll
-  for (int g = 0; g < kRowGroups; ++g) {
-    s[2 * g] *= decay;
-    s[2 * g + 1] *= decay;
-    part[g] = dot8(s[2 * g], s[2 * g + 1], k0, k1);
+  for (int j = j0; j < j0 + 4; ++j) s[j] *= decay;
+  float pred0 = dot8(s[j0], s[j0 + 1], x.k0, x.k1);
+  float pred1 = dot8(s[j0 + 2], s[j0 + 3], x.k0, x.k1);
+  row_sum2(pred0, pred1);
+  const float d0 = (v0 - pred0) * beta;
+  const float d1 = (v1 - pred1) * beta;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    s[j0][e] = fmaf(d0, x.k0[e], s[j0][e]);
+    s[j0 + 1][e] = fmaf(d0, x.k1[e], s[j0 + 1][e]);
+    s[j0 + 2][e] = fmaf(d1, x.k0[e], s[j0 + 2][e]);
+    s[j0 + 3][e] = fmaf(d1, x.k1[e], s[j0 + 3][e]);
   }
-  const float pred = reduce_scatter8(part, kq);
-  const float delta = (v_row - pred) * beta;
-  float d[kRowGroups];
-  all_gather8(delta, kq, d);
-#pragma unroll
-  for (int g = 0; g < kRowGroups; ++g) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      s[2 * g][e] = fmaf(d[g], k0[e], s[2 * g][e]);
-      s[2 * g + 1][e] = fmaf(d[g], k1[e], s[2 * g + 1][e]);
-    }
-    part[g] = dot8(s[2 * g], s[2 * g + 1], q0, q1);
-  }
-  const float out = reduce_scatter8(part, kq);
-  if ((kq & 1) == 0) o[my_row] = round_bf16(out);
-
   if (dst_tile != nullptr) {
 #pragma unroll
-    for (int j = 0; j < 2 * kRowGroups; ++j) {
-      __builtin_nontemporal_store(
-          s[j], reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j))));
+    for (int j = j0; j < j0 + 4; ++j) {
+      f32x4* dst = reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j)));
+      if (Stream)
+        __builtin_nontemporal_store(s[j], dst);
+      else
+        *dst = s[j];
     }
   }
+  float out0 = dot8(s[j0], s[j0 + 1], x.q0, x.q1);
+  float out1 = dot8(s[j0 + 2], s[j0 + 3], x.q0, x.q1);
+  row_sum2(out0, out1);
+  if (kq == 0) {
+    o[row0] = round_bf16(out0);
+    o[row0 + 4] = round_bf16(out1);
+  }
+}
+
+// Uses a wave-uniform value (in SGPRs) at this point of the program, so its computation (a
+// kernel-argument or metadata load) cannot be sunk past later branches.  Input-only: the
+// value itself, and for pointers their global address space, stay visible to the compiler.
+template <typename T>
+__device__ __forceinline__ void pin_sgpr(const T& x) {
+  asm volatile("" ::"s"(x));
 }
 
 // Waits for this wave's LDS traffic, then joins the workgroup barrier.  Global loads that
@@ -182,10 +255,19 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Four waves per SIMD (<= 128 VGPRs) keep four workgroups, i.e. four tiles, resident per CU.
-// DtBf16 / WBf16: dt_bias / norm_weight stored as bf16 (else fp32).
-template <bool DtBf16, bool WBf16>
+// DtBf16 / WBf16: dt_bias / norm_weight stored as bf16 (else fp32).  Stream: non-temporal
+// state loads and stores (for working sets larger than the caches).  Width: the indices
+// width W (tokens per request at most); fixing it at compile time unrolls every token loop
+// into straight-line code, which keeps the tile's per-piece load waits exact.
+template <bool DtBf16, bool WBf16, bool Stream, int Width>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
-void gdn_decode_kernel(const DecodeParams p) {
+void gdn_decode_kernel(const DecodeParams args) {
+  // Every kernel argument, then all request metadata, is loaded before the first branch:
+  // two dependent scalar round trips (kernel-argument segment; cu/accepted/indices) instead
+  // of the compiler's default of sinking each load to its first use behind the early exits.
+  // The pins come after the metadata loads: a pin is opaque to the compiler, and scalar
+  // (s_load) metadata loads must not follow anything that might have written memory.
+  const DecodeParams& p = args;
   const int tile = blockIdx.x;
   const int request = tile / p.num_v_heads;
   const int head = tile - request * p.num_v_heads;
@@ -193,13 +275,45 @@ void gdn_decode_kernel(const DecodeParams p) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
+  // Request metadata in one round trip: token range, accepted count and the (at most 4)
+  // slots of the request, read before any state store.
+  const int32_t* req_slots = p.indices + static_cast<int64_t>(request) * Width;
   const int bos = p.cu[request];
-  const int num_tokens = p.cu[request + 1] - bos;
-  if (num_tokens <= 0) return;
+  const int eos = p.cu[request + 1];
   const int accepted = p.accepted[request];
-  const int32_t* req_slots = p.indices + static_cast<int64_t>(request) * p.width;
-  const int source = (accepted >= 1 && accepted <= p.width) ? req_slots[accepted - 1] : 0;
-  if (source <= 0 || num_tokens > p.width) {
+  int slot[Width];
+#pragma unroll
+  for (int t = 0; t < Width; ++t) slot[t] = req_slots[t];
+#pragma unroll
+  for (int t = 0; t < Width; ++t) pin_sgpr(slot[t]);
+  pin_sgpr(bos);
+  pin_sgpr(eos);
+  pin_sgpr(accepted);
+  pin_sgpr(p.qkv);
+  pin_sgpr(p.qkv_row);
+  pin_sgpr(p.a);
+  pin_sgpr(p.a_row);
+  pin_sgpr(p.b);
+  pin_sgpr(p.b_row);
+  pin_sgpr(p.a_log);
+  pin_sgpr(p.dt_bias);
+  pin_sgpr(p.state);
+  pin_sgpr(p.state_slot);
+  pin_sgpr(p.gate);
+  pin_sgpr(p.gate_row);
+  pin_sgpr(p.norm_weight);
+  pin_sgpr(p.out);
+  pin_sgpr(p.num_k_heads);
+  pin_sgpr(p.group);
+  pin_sgpr(p.scale);
+  pin_sgpr(p.eps);
+  const int num_tokens = eos - bos;
+  if (num_tokens <= 0) return;
+  int source = 0;
+#pragma unroll
+  for (int t = 0; t < Width; ++t)
+    if (accepted == t + 1) source = slot[t];
+  if (source <= 0 || num_tokens > Width) {
     // Invalid request: zero outputs, state untouched.
     for (int i = tid; i < num_tokens * kDim; i += kThreads) {
       const int64_t token = bos + (i >> 7);
@@ -208,116 +322,135 @@ void gdn_decode_kernel(const DecodeParams p) {
     return;
   }
 
-  __shared__ float s_q[kMaxTokens][kDim];
-  __shared__ float s_k[kMaxTokens][kDim];
-  __shared__ float s_v[kMaxTokens][kDim];
-  __shared__ float s_o[kMaxTokens][kDim];
-  __shared__ float s_silu[kMaxTokens][kDim];  // silu(gate)
-  __shared__ float s_w[kDim];                  // norm weight
-  __shared__ float s_decay[kMaxTokens];
-  __shared__ float s_beta[kMaxTokens];
+  // Token 0 is staged by every wave for itself (wave-private LDS, no barrier before the
+  // recurrence): q^ and k^ (128 each), v of the wave's 32 rows, decay and beta.  MTP tokens
+  // t >= 1 are staged once, by wave t, in the shared area (one barrier, after chunk 0's
+  // token 0).  s_o collects the raw outputs of all rows for the epilogue.
+  __shared__ f32x4 s_qk0[kWaves][2][kDim / 4];
+  __shared__ float s_v0[kWaves][kRowsPerWave];
+  __shared__ float s_db0[kWaves][2];
+  __shared__ f32x4 s_qkt[Width][2][kDim / 4];
+  __shared__ float s_vt[Width][kDim];
+  __shared__ float s_dbt[Width][2];
+  __shared__ float s_o[Width][kDim];
 
   const int key_head = head / p.group;
-  const bool has_token = wave < num_tokens;  // wave t prepares token t
-  // Destination slots of the (at most 4) tokens, read before any state store.
-  int dest_slot[kMaxTokens];
-#pragma unroll
-  for (int t = 0; t < kMaxTokens; ++t) dest_slot[t] = t < p.width ? req_slots[t] : 0;
+  const int kq = lane & 15;
+  const int rsub = lane >> 4;
+  const int row_base = wave * kRowsPerWave + rsub;  // V row of the lane's piece 0
+  const int q_col = key_head * kDim;
+  const int k_col = (p.num_k_heads + key_head) * kDim;
+  const int v_col = (2 * p.num_k_heads + head) * kDim;
 
-  // ---- small activation loads first, so the tile loads below do not delay them.  Every
-  // wave loads (waves past the request's last token re-read that token) so the loads stay
-  // in one basic block with the tile loads and their waits sink to the first use. ----
+  // ---- small activation loads go out before the tile, so they return first: token 0 in
+  // the lane layout of the tile (q, k at 4kq.. and 64+4kq..; v of the wave's 32 rows), the
+  // MTP token `wave` for the shared staging, and the epilogue inputs of token `wave` ----
+  const TokenIn in0 = load_token(p, bos, q_col, k_col, v_col + wave * kRowsPerWave + (lane & 31),
+                                 head, kq);
+  const bool stages_mtp = Width > 1 && wave >= 1 && wave < num_tokens;
   const int64_t token_w = bos + min(wave, num_tokens - 1);
-  uint16_t qh[2], kh[2], vh[2], gh[2];
+  TokenIn inw;
+  uint16_t vw_hi = 0;
+  if (Width > 1) {
+    inw = load_token(p, token_w, q_col, k_col, v_col + 2 * lane, head, kq);
+    vw_hi = p.qkv[token_w * p.qkv_row + v_col + 2 * lane + 1];
+  }
+  uint16_t gh[2];
   float w[2];
   {
-    const uint16_t* row = p.qkv + token_w * p.qkv_row;
-    const uint16_t* qrow = row + key_head * kDim;
-    const uint16_t* krow = row + (p.num_k_heads + key_head) * kDim;
-    const uint16_t* vrow = row + (2 * p.num_k_heads + head) * kDim;
     const uint16_t* grow = p.gate + token_w * p.gate_row + head * kDim;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      qh[e] = qrow[2 * lane + e];
-      kh[e] = krow[2 * lane + e];
-      vh[e] = vrow[2 * lane + e];
       gh[e] = grow[2 * lane + e];
       w[e] = load_param(p.norm_weight, 2 * lane + e, WBf16);
     }
   }
-  const uint16_t a_bits = p.a[token_w * p.a_row + head];
-  const uint16_t b_bits = p.b[token_w * p.b_row + head];
   const float dt_bias = load_param(p.dt_bias, head, DtBf16);
   const float a_log = p.a_log[head];
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- the whole 64 KiB source tile: 16 x 128-bit loads per lane (uniform base address,
-  // 32-bit per-lane byte offsets) ----
-  const int kq = lane & 15;
-  const int rsub = lane >> 4;
+  // 32-bit per-lane byte offsets), issued in chunk order ----
   const int64_t head_offset = static_cast<int64_t>(head) * kDim * kDim;
-  const uint32_t lane_bytes = static_cast<uint32_t>((wave * kRowsPerWave + rsub) * kDim + kq * 4) * 4u;
+  const uint32_t lane_bytes = static_cast<uint32_t>(row_base * kDim + kq * 4) * 4u;
   const char* src_tile = reinterpret_cast<const char*>(
       p.state + static_cast<int64_t>(source) * p.state_slot + head_offset);
-  f32x4 s[2 * kRowGroups];
+  f32x4 s[kPieces];
 #pragma unroll
-  for (int j = 0; j < 2 * kRowGroups; ++j) {
-    s[j] = *reinterpret_cast<const f32x4*>(src_tile + (lane_bytes + tile_piece_bytes(j)));
+  for (int j = 0; j < kPieces; ++j) {
+    const f32x4* src =
+        reinterpret_cast<const f32x4*>(src_tile + (lane_bytes + tile_piece_bytes(j)));
+    s[j] = Stream ? __builtin_nontemporal_load(src) : *src;
+    __builtin_amdgcn_sched_barrier(0);  // keep program order: chunk c's loads issue first
   }
-  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- prologue: q/k L2 norm, decay and beta for token `wave`.  Waves past the last token
-  // compute on a copy of it and their LDS rows are never read. ----
+  // ---- staging, while the tile streams in ----
   {
-    float q[2], k[2];
-    float qq = 0.0f, kk = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      q[e] = bf16_to_f32(qh[e]);
-      k[e] = bf16_to_f32(kh[e]);
-      qq = fmaf(q[e], q[e], qq);
-      kk = fmaf(k[e], k[e], kk);
+    const Staged x = stage_token(in0, a_log, dt_bias, p.scale);
+    if (rsub == 0) {
+      s_qk0[wave][0][kq] = x.q0;
+      s_qk0[wave][0][16 + kq] = x.q1;
+      s_qk0[wave][1][kq] = x.k0;
+      s_qk0[wave][1][16 + kq] = x.k1;
     }
-    qq = wave_sum(qq);
-    kk = wave_sum(kk);
-    const float rq = 1.0f / sqrtf(qq + 1e-6f);
-    const float rk = 1.0f / sqrtf(kk + 1e-6f);
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      s_q[wave][2 * lane + e] = (q[e] * rq) * p.scale;
-      s_k[wave][2 * lane + e] = k[e] * rk;
-      s_v[wave][2 * lane + e] = bf16_to_f32(vh[e]);
-      const float gate = bf16_to_f32(gh[e]);
-      s_silu[wave][2 * lane + e] = gate / (1.0f + expf(-gate));
-      if (wave == 0) s_w[2 * lane + e] = w[e];
-    }
-    const float g = -expf(a_log) * softplus(bf16_to_f32(a_bits) + dt_bias);
-    const float decay = expf(g);
-    const float beta = sigmoid(bf16_to_f32(b_bits));
+    if (lane < kRowsPerWave) s_v0[wave][lane] = bf16_to_f32(in0.v);
     if (lane == 0) {
-      s_decay[wave] = decay;
-      s_beta[wave] = beta;
+      s_db0[wave][0] = x.decay;
+      s_db0[wave][1] = x.beta;
     }
   }
-  lds_barrier();
+  if (stages_mtp) {
+    const Staged x = stage_token(inw, a_log, dt_bias, p.scale);
+    if (rsub == 0) {
+      s_qkt[wave][0][kq] = x.q0;
+      s_qkt[wave][0][16 + kq] = x.q1;
+      s_qkt[wave][1][kq] = x.k0;
+      s_qkt[wave][1][16 + kq] = x.k1;
+    }
+    s_vt[wave][2 * lane] = bf16_to_f32(inw.v);
+    s_vt[wave][2 * lane + 1] = bf16_to_f32(vw_hi);
+    if (lane == 0) {
+      s_dbt[wave][0] = x.decay;
+      s_dbt[wave][1] = x.beta;
+    }
+  }
 
-  // ---- recurrence: 1 tile read, one tile write per token.  Token 0 is peeled off the loop
-  // so its first uses of the tile wait for each 16-byte piece separately (s_waitcnt vmcnt(N)
-  // per piece) instead of for the whole tile. ----
-  const int my_row = wave * kRowsPerWave + (kq >> 1) * 4 + rsub;  // row of reduce results
+  // The token-0 staging above is read back by other lanes of the same wave.  A wave executes
+  // its LDS instructions in program order, so only the compiler must not move the reads
+  // above the writes.
+  asm volatile("" ::: "memory");
+
+  // ---- recurrence, chunk by chunk in load order (each chunk's first use of a piece waits
+  // for that piece alone: s_waitcnt vmcnt(N)); every token of a chunk before the next ----
   char* const state_bytes = reinterpret_cast<char*>(p.state + head_offset);
   const int64_t slot_bytes = p.state_slot * 4;
-  token_step(s, s_q[0], s_k[0], s_v[0][my_row], s_o[0], s_decay[0], s_beta[0], kq, my_row,
-             dest_slot[0] > 0 ? state_bytes + dest_slot[0] * slot_bytes : nullptr, lane_bytes);
-  for (int t = 1; t < num_tokens; ++t) {
-    const int dest = t == 1 ? dest_slot[1] : t == 2 ? dest_slot[2] : dest_slot[3];
-    token_step(s, s_q[t], s_k[t], s_v[t][my_row], s_o[t], s_decay[t], s_beta[t], kq, my_row,
-               dest > 0 ? state_bytes + dest * slot_bytes : nullptr, lane_bytes);
+  char* dst[Width];
+#pragma unroll
+  for (int t = 0; t < Width; ++t)
+    dst[t] = slot[t] > 0 ? state_bytes + slot[t] * slot_bytes : nullptr;
+
+#define LD_CHUNK(C)                                                                         \
+  {                                                                                         \
+    const int r = row_base + 8 * (C);                                                       \
+    chunk_step<C, Stream>(s, load_vectors(s_qk0[wave], kq), s_v0[wave][8 * (C) + rsub],     \
+                          s_v0[wave][8 * (C) + 4 + rsub], s_o[0], s_db0[wave][0],           \
+                          s_db0[wave][1], kq, r, dst[0], lane_bytes);                       \
+    if ((C) == 0 && Width > 1 && num_tokens > 1) lds_barrier();                             \
+    _Pragma("unroll") for (int t = 1; t < Width; ++t) {                                     \
+      if (t < num_tokens)                                                                   \
+        chunk_step<C, Stream>(s, load_vectors(s_qkt[t], kq), s_vt[t][r], s_vt[t][r + 4],    \
+                              s_o[t], s_dbt[t][0], s_dbt[t][1], kq, r, dst[t], lane_bytes); \
+    }                                                                                       \
   }
+  LD_CHUNK(0)
+  LD_CHUNK(1)
+  LD_CHUNK(2)
+  LD_CHUNK(3)
+#undef LD_CHUNK
   lds_barrier();
 
   // ---- gated RMSNorm epilogue for token `wave` ----
-  if (has_token) {
+  if (wave < num_tokens) {
     const int64_t token = bos + wave;
     float raw[2];
     float ss = 0.0f;
@@ -327,13 +460,35 @@ void gdn_decode_kernel(const DecodeParams p) {
       ss = fmaf(raw[e], raw[e], ss);
     }
     ss = wave_sum(ss);
-    const float rstd = 1.0f / sqrtf(ss / static_cast<float>(kDim) + p.eps);
+    const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
     uint16_t* orow = p.out + (token * p.num_v_heads + head) * kDim;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int v = 2 * lane + e;
-      orow[v] = f32_to_bf16(((raw[e] * rstd) * s_w[v]) * s_silu[wave][v]);
+      const float gate = bf16_to_f32(gh[e]);
+      orow[v] = f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(gate));
     }
+  }
+}
+
+template <bool Stream, int Width>
+void launch_decode(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
+                   hipStream_t stream) {
+  auto kernel = dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, Stream, Width>
+                                  : gdn_decode_kernel<true, false, Stream, Width>)
+                        : (w_bf16 ? gdn_decode_kernel<false, true, Stream, Width>
+                                  : gdn_decode_kernel<false, false, Stream, Width>);
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, stream, p);
+}
+
+template <bool Stream>
+void launch_decode(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
+                   hipStream_t stream) {
+  switch (p.width) {
+    case 1: launch_decode<Stream, 1>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 2: launch_decode<Stream, 2>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 3: launch_decode<Stream, 3>(p, dt_bf16, w_bf16, blocks, stream); break;
+    default: launch_decode<Stream, 4>(p, dt_bf16, w_bf16, blocks, stream); break;
   }
 }
 
@@ -353,6 +508,8 @@ extern "C" int ld_gdn_decode(const ld_gdn_decode_args* args, void* stream) {
   if ((a.dt_bias_dtype != LD_DTYPE_F32 && a.dt_bias_dtype != LD_DTYPE_BF16) ||
       (a.norm_weight_dtype != LD_DTYPE_F32 && a.norm_weight_dtype != LD_DTYPE_BF16))
     return fail(LD_ERR_INVALID_ARGUMENT, "weights must be FP32/BF16");
+  if (a.cache_policy != LD_CACHE_KEEP && a.cache_policy != LD_CACHE_STREAM)
+    return fail(LD_ERR_INVALID_ARGUMENT, "cache_policy must be LD_CACHE_KEEP or LD_CACHE_STREAM");
   if (a.num_requests == 0) return LD_OK;
   if (!a.qkv || !a.a || !a.b || !a.a_log || !a.dt_bias || !a.indices || !a.cu || !a.accepted ||
       !a.state || !a.gate || !a.norm_weight || !a.out)
@@ -388,9 +545,10 @@ extern "C" int ld_gdn_decode(const ld_gdn_decode_args* args, void* stream) {
   p.eps = a.eps;
   const bool dt_bf16 = a.dt_bias_dtype == LD_DTYPE_BF16;
   const bool w_bf16 = a.norm_weight_dtype == LD_DTYPE_BF16;
-  auto kernel = dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true> : gdn_decode_kernel<true, false>)
-                        : (w_bf16 ? gdn_decode_kernel<false, true> : gdn_decode_kernel<false, false>);
-  hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), p);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a.cache_policy == LD_CACHE_STREAM)
+    launch_decode<true>(p, dt_bf16, w_bf16, static_cast<uint32_t>(blocks), s);
+  else
+    launch_decode<false>(p, dt_bf16, w_bf16, static_cast<uint32_t>(blocks), s);
   return check_launch("ld_gdn_decode");
 }

@@ -19,6 +19,8 @@ memory on the host, so it can be captured in a HIP graph.
 
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib
@@ -38,6 +40,25 @@ SCHEMAS = {
 
 HEAD_DIM = _lib.HEAD_DIM
 QK_SCALE = HEAD_DIM**-0.5  # reference csrc/gdn_decode.cu:417
+
+# State cache policy of the decode kernel (never changes results, only where the state
+# lines live between steps): "keep" leaves them cached, which pays off when one layer's
+# working set fits the 256 MB Infinity Cache and is stepped again soon; "stream" uses
+# non-temporal loads/stores for working sets far beyond it (many layers per decode step).
+# Set with set_state_cache_policy() or the LIGHTDELTA_STATE_CACHE environment variable.
+_POLICIES = {"keep": _lib.CACHE_KEEP, "stream": _lib.CACHE_STREAM}
+_cache_policy = _POLICIES[os.environ.get("LIGHTDELTA_STATE_CACHE", "keep")]
+
+
+def set_state_cache_policy(policy: str) -> None:
+    global _cache_policy
+    if policy not in _POLICIES:
+        raise ValueError(f"state cache policy must be one of {sorted(_POLICIES)}")
+    _cache_policy = _POLICIES[policy]
+
+
+def state_cache_policy() -> str:
+    return next(name for name, code in _POLICIES.items() if code == _cache_policy)
 
 _FLOATS = (torch.float32, torch.bfloat16)
 
@@ -200,6 +221,7 @@ def _decode_impl(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, 
         hv,
         QK_SCALE,
         eps,
+        _cache_policy,
     )
     lib = _lib.load()
     with _DeviceGuard(qkv.device):
