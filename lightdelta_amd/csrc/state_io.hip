@@ -4,16 +4,16 @@
 // Semantics follow the reference's copy kernel (csrc/state_io.cu:11-27): a slot <= 0 is
 // padding; gather zero-fills rows whose slot is padding or whose `valid` flag is false,
 // scatter and copy skip padding.  Unlike the reference (one 4-byte element per thread per
-// iteration, csrc/state_io.cu:22-26), every thread here moves 128-bit vectors with eight
-// loads in flight before the first store, and each workgroup owns one 32 KiB chunk of a row.
+// iteration, csrc/state_io.cu:22-26), every thread here moves 128-bit vectors with four
+// loads in flight before the first store, and each workgroup owns one 16 KiB chunk of a row.
 #include "common.h"
 
 namespace ld {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kVecsPerThread = 8;
-constexpr int64_t kVecsPerChunk = static_cast<int64_t>(kThreads) * kVecsPerThread;  // 32 KiB
+constexpr int kVecsPerThread = 4;
+constexpr int64_t kVecsPerChunk = static_cast<int64_t>(kThreads) * kVecsPerThread;  // 16 KiB
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -29,14 +29,17 @@ struct CopyParams {
   const int32_t* dst_slots;  // copy only
   const uint8_t* valid;   // gather only; NULL = all valid
   int64_t vecs;           // 16-byte vectors per row
-  int64_t chunks;         // chunks per row
+  uint32_t chunks;        // chunks per row
 };
 
+// One workgroup moves one 16 KiB chunk of one row: 4 non-temporal 128-bit loads per thread
+// in flight, then 4 stores (the data is touched once, so it bypasses cache allocation).
+// Every branch below is uniform over the workgroup.
 template <int M>
 __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p) {
-  const int64_t block = blockIdx.x;
-  const int64_t row = block / p.chunks;
-  const int64_t chunk = block - row * p.chunks;
+  const uint32_t block = blockIdx.x;
+  const uint32_t row = block / p.chunks;
+  const uint32_t chunk = block - row * p.chunks;
 
   const u32x4* src;
   u32x4* dst;
@@ -59,13 +62,31 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
     dst = reinterpret_cast<u32x4*>(p.dst + to * p.dst_stride);
   }
 
-  const int64_t first = chunk * kVecsPerChunk + threadIdx.x;
+  const int64_t begin = static_cast<int64_t>(chunk) * kVecsPerChunk;
+  const int64_t first = begin + threadIdx.x;
+  if (!live) {  // gather of a padding / invalid row: zero fill
+#pragma unroll
+    for (int i = 0; i < kVecsPerThread; ++i) {
+      const int64_t idx = first + i * kThreads;
+      if (idx < p.vecs) __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, dst + idx);
+    }
+    return;
+  }
   u32x4 v[kVecsPerThread];
+  if (begin + kVecsPerChunk <= p.vecs) {  // whole chunk: unguarded, all loads in flight
+#pragma unroll
+    for (int i = 0; i < kVecsPerThread; ++i)
+      v[i] = __builtin_nontemporal_load(src + first + i * kThreads);
+#pragma unroll
+    for (int i = 0; i < kVecsPerThread; ++i)
+      __builtin_nontemporal_store(v[i], dst + first + i * kThreads);
+    return;
+  }
+  // tail chunk of a row
 #pragma unroll
   for (int i = 0; i < kVecsPerThread; ++i) {
     const int64_t idx = first + i * kThreads;
-    v[i] = u32x4{0u, 0u, 0u, 0u};
-    if (live && idx < p.vecs) v[i] = __builtin_nontemporal_load(src + idx);
+    v[i] = __builtin_nontemporal_load(src + (idx < p.vecs ? idx : 0));
   }
 #pragma unroll
   for (int i = 0; i < kVecsPerThread; ++i) {
@@ -83,8 +104,9 @@ int launch(const char* what, int mode, CopyParams p, int64_t rows, int64_t row_b
     return fail(LD_ERR_INVALID_ARGUMENT,
                 "state rows, strides and base pointers must be 16-byte aligned");
   p.vecs = row_bytes / 16;
-  p.chunks = (p.vecs + kVecsPerChunk - 1) / kVecsPerChunk;
-  const int64_t blocks = rows * p.chunks;
+  const int64_t chunks = (p.vecs + kVecsPerChunk - 1) / kVecsPerChunk;
+  p.chunks = static_cast<uint32_t>(chunks);
+  const int64_t blocks = rows * chunks;
   if (blocks > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "copy too large for one launch");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<uint32_t>(blocks));
