@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 2
+#define LD_ABI_VERSION 3
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -96,6 +96,48 @@ typedef struct ld_gdn_decode_args {
 /* Fused decode step; see ld_gdn_decode_args.  Replaces lightdelta::decode
  * (reference include/lightdelta/ops.h:5-9, csrc/gdn_decode.cu:360-420). */
 int ld_gdn_decode(const ld_gdn_decode_args* args, void* stream);
+
+/*
+ * Pre-conv inputs and conv-state pool of the conv-fused step (ld_gdn_decode_conv).
+ *   x       bf16 [tokens, conv_dim] pre-conv activations (conv_dim = (2*H + HV)*128, the
+ *           same column layout as the post-conv qkv), row stride x_row_stride, unit column
+ *           stride
+ *   state   bf16 conv-state pool of `state_slots` slots; element (slot, channel, column) at
+ *           slot*state_slot_stride + channel*state_dim_stride + column*state_len_stride
+ *           (vLLM's dim-first [slots, conv_dim, len] and dim-last [slots, len, conv_dim]
+ *           layouts are both covered); column state_len-1 is the most recent input
+ *   weight  bf16 [conv_dim, width] contiguous, 8-byte aligned; bias bf16 [conv_dim] or NULL
+ * Element strides.  width must be 4 and 3 <= state_len <= 8.  The conv slot of request r is
+ * indices[r, 0], the slot its SSM state lives in.
+ */
+typedef struct ld_conv_args {
+  const void* x;
+  int64_t x_row_stride;
+  void* state;
+  int64_t state_slots;
+  int64_t state_slot_stride;
+  int64_t state_dim_stride;
+  int64_t state_len_stride;
+  int32_t state_len;
+  int32_t width;
+  const void* weight;
+  int32_t weight_dtype;
+  int32_t bias_dtype;
+  const void* bias;
+} ld_conv_args;
+
+/*
+ * Conv-fused single-token decode step (args->width must be 1; args->qkv is not read).  Per
+ * request, the causal depthwise conv1d of the new token over the last 3 conv-state columns,
+ * plus bias and SiLU, is rounded to bf16 and becomes the step's q/k/v; the conv state of the
+ * slot shifts left by one column and takes the new input; then the GDN step of
+ * ld_gdn_decode runs.  Invalid requests (padding source, bad `accepted`, no tokens) leave
+ * both pools untouched.  Launches that touch the same slots must be stream-ordered (they
+ * share one ticket per (slot, k-head) in library-owned device memory; at most 2^20).
+ * No counterpart in the reference, whose conv is vLLM's causal_conv1d_update run before
+ * lightdelta::decode (python/lightdelta/integration/vllm_layer.py:199-220).
+ */
+int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_args* conv, void* stream);
 
 /*
  * Gather pool rows into a packed buffer:

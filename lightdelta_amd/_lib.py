@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must precede the CDLL load (see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("liblightdelta_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 CACHE_KEEP = 0
@@ -61,9 +61,33 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class ConvArgs(ctypes.Structure):
+    """Mirror of ld_conv_args (include/lightdelta_hip.h)."""
+
+    _fields_ = [
+        ("x", _vp),
+        ("x_row_stride", _c_i64),
+        ("state", _vp),
+        ("state_slots", _c_i64),
+        ("state_slot_stride", _c_i64),
+        ("state_dim_stride", _c_i64),
+        ("state_len_stride", _c_i64),
+        ("state_len", _c_i32),
+        ("width", _c_i32),
+        ("weight", _vp),
+        ("weight_dtype", _c_i32),
+        ("bias_dtype", _c_i32),
+        ("bias", _vp),
+    ]
+
+
 # Exported entry points and their C signatures (argtypes, restype).
 SIGNATURES = {
     "ld_gdn_decode": ([ctypes.POINTER(DecodeArgs), _vp], ctypes.c_int),
+    "ld_gdn_decode_conv": (
+        [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ConvArgs), _vp],
+        ctypes.c_int,
+    ),
     "ld_state_gather": (
         [_vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp],
         ctypes.c_int,

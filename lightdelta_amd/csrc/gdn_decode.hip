@@ -62,7 +62,23 @@ struct DecodeParams {
   int32_t group;  // num_v_heads / num_k_heads
   float scale;
   float eps;
+  // Conv-fused variant only (pre-conv activations and the conv-state pool).
+  const uint16_t* conv_x;
+  int64_t conv_x_row;
+  uint16_t* conv_state;
+  int64_t conv_slot;
+  int64_t conv_dim_stride;
+  int64_t conv_len_stride;
+  int32_t conv_len;
+  const uint16_t* conv_weight;  // [conv_dim, 4]
+  const uint16_t* conv_bias;    // [conv_dim] or NULL
 };
+
+constexpr int kConvWidth = 4;
+constexpr int kMaxConvLen = 8;
+// Tickets of the conv-fused variant, one per (conv slot, k-head); see gdn_decode_kernel.
+constexpr int kMaxConvTickets = 1 << 20;
+__device__ uint32_t g_conv_ticket[kMaxConvTickets];
 
 __device__ __forceinline__ float load_param(const void* p, int i, bool bf16) {
   return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i])
@@ -248,6 +264,59 @@ __device__ __forceinline__ void pin_sgpr(const T& x) {
   asm volatile("" ::"s"(x));
 }
 
+// silu(x) rounded to the nearest bf16 (ties to even) as if computed exactly.
+//
+// Fast path: x * rcp(1 + exp(-x)) in fp32.  Rounding x * log2(e) inside the hardware exp
+// costs a relative error of |x| * 2^-24 in exp(-x); exp, the add, rcp and the final multiply
+// add at most ~3 * 2^-23 more, so the fp32 result is within |x| + 6 fp32 ulps of the exact
+// value.  Its bf16 rounding is therefore the exact value's unless it lies within that
+// distance of a bf16 rounding midpoint (low 16 bits near 0x8000); such lanes (window
+// 64 + 4|x| ulps) and |x| > 64 recompute x / (1 + exp(-x)) in fp64 and round that to bf16
+// without double rounding.  Inlined: a call would make the callee wait for every load in
+// flight.
+__device__ __forceinline__ uint16_t silu_bf16_exact(float x) {
+  const double yd = static_cast<double>(x) / (1.0 + exp(-static_cast<double>(x)));
+  const float t = static_cast<float>(yd);
+  const uint32_t u = __float_as_uint(t);
+  if ((u & 0xffffu) == 0x8000u && static_cast<double>(t) != yd)  // fp32 rounding hit a tie
+    return static_cast<uint16_t>((u >> 16) + (fabs(yd) > fabs(static_cast<double>(t)) ? 1u : 0u));
+  return f32_to_bf16(t);
+}
+
+__device__ __forceinline__ uint16_t silu_bf16(float x) {
+  const float y = silu(x);
+  const float ax = fabsf(x);
+  const int low = static_cast<int>(__float_as_uint(y) & 0xffffu) - 0x8000;
+  if (!(ax <= 64.0f) || static_cast<float>(abs(low)) <= 64.0f + 4.0f * ax)
+    return silu_bf16_exact(x);
+  return f32_to_bf16(y);
+}
+
+// One decode-token output of the causal depthwise conv (width 4) plus SiLU, rounded to bf16:
+//   bf16(silu(bias + sum_j w[j] * [state[len-3], state[len-2], state[len-1], x][j]))
+// with the fp32 accumulation running from the oldest tap to the newest (one rounding per
+// fused multiply-add) and the SiLU correctly rounded to bf16.
+__device__ __forceinline__ uint16_t conv_output(uint16_t x, const uint16_t (&state)[kMaxConvLen],
+                                                const uint32_t (&w)[2], uint16_t bias,
+                                                bool has_bias, int len) {
+  uint16_t tap[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    // state[len - 3 + i], selected without dynamic register indexing
+    uint16_t v = state[0];
+#pragma unroll
+    for (int j = 1; j < kMaxConvLen; ++j)
+      if (j == len - 3 + i) v = state[j];
+    tap[i] = v;
+  }
+  float acc = has_bias ? bf16_to_f32(bias) : 0.0f;
+  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[0])), bf16_to_f32(tap[0]), acc);
+  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[0] >> 16)), bf16_to_f32(tap[1]), acc);
+  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[1])), bf16_to_f32(tap[2]), acc);
+  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[1] >> 16)), bf16_to_f32(x), acc);
+  return silu_bf16(acc);
+}
+
 // Waits for this wave's LDS traffic, then joins the workgroup barrier.  Global loads that
 // are still in flight stay in flight (a __syncthreads() fence would drain them).
 __device__ __forceinline__ void lds_barrier() {
@@ -259,9 +328,22 @@ __device__ __forceinline__ void lds_barrier() {
 // state loads and stores (for working sets larger than the caches).  Width: the indices
 // width W (tokens per request at most); fixing it at compile time unrolls every token loop
 // into straight-line code, which keeps the tile's per-piece load waits exact.
-template <bool DtBf16, bool WBf16, bool Stream, int Width>
+//
+// Conv: the causal depthwise conv1d (width 4, SiLU) runs first on the pre-conv activations
+// (single-token decode only).  Each workgroup convolves the 256 q/k channels of its k-head
+// and the 128 v channels of its head from the conv state of the request's slot, rounds the
+// outputs to bf16 (the dtype an unfused conv writes) and feeds them to the GDN step.  Its
+// own v channels' conv state is shifted in place.  The q/k channels are shared by the
+// HV/H workgroups of a k-head group, so their shifted state is written only after all of
+// them have read it: every workgroup counts itself in (atomic add on
+// g_conv_ticket[slot*H + kh]) after its reads; at its end, a workgroup that finds the count
+// at HV/H writes the shifted state and resets the count to 0.  The last to count in always
+// finds it, so the state is written at least once (several writers write identical bytes).
+// Nothing waits on another workgroup, and every launch leaves the counts at zero.
+template <bool DtBf16, bool WBf16, bool Stream, int Width, bool Conv>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void gdn_decode_kernel(const DecodeParams args) {
+  static_assert(!Conv || Width == 1, "the conv-fused step is single-token");
   // Every kernel argument, then all request metadata, is loaded before the first branch:
   // two dependent scalar round trips (kernel-argument segment; cu/accepted/indices) instead
   // of the compiler's default of sinking each load to its first use behind the early exits.
@@ -333,6 +415,10 @@ void gdn_decode_kernel(const DecodeParams args) {
   __shared__ float s_vt[Width][kDim];
   __shared__ float s_dbt[Width][2];
   __shared__ float s_o[Width][kDim];
+  // Conv variant: bf16 conv outputs of the 256 q/k channels and 128 v channels, and the
+  // shifted q/k conv state kept for the end-of-kernel write.
+  __shared__ uint16_t s_conv[Conv ? 3 * kDim : 2];
+  __shared__ uint16_t s_conv_new[Conv ? 2 * kDim : 1][Conv ? kMaxConvLen : 1];
 
   const int key_head = head / p.group;
   const int kq = lane & 15;
@@ -345,8 +431,46 @@ void gdn_decode_kernel(const DecodeParams args) {
   // ---- small activation loads go out before the tile, so they return first: token 0 in
   // the lane layout of the tile (q, k at 4kq.. and 64+4kq..; v of the wave's 32 rows), the
   // MTP token `wave` for the shared staging, and the epilogue inputs of token `wave` ----
-  const TokenIn in0 = load_token(p, bos, q_col, k_col, v_col + wave * kRowsPerWave + (lane & 31),
-                                 head, kq);
+  TokenIn in0;
+  // Conv variant: this thread convolves q/k channel `conv_qk` and (tid < 128) v channel
+  // `conv_v`; it loads their input, conv-state columns (clamped to the last column past
+  // conv_len, so every load is in bounds), weights and bias.
+  const int conv_qk = tid < kDim ? q_col + tid : k_col + (tid - kDim);
+  const int conv_v = v_col + (tid & (kDim - 1));
+  int64_t cs_qk_at = 0, cs_v_at = 0;
+  uint16_t cx_qk = 0, cx_v = 0, cb_qk = 0, cb_v = 0;
+  uint16_t cs_qk[kMaxConvLen], cs_v[kMaxConvLen];
+  uint32_t cw_qk[2], cw_v[2];
+  if constexpr (Conv) {
+    const uint16_t* xrow = p.conv_x + static_cast<int64_t>(bos) * p.conv_x_row;
+    cx_qk = xrow[conv_qk];
+    cx_v = xrow[conv_v];
+    const int64_t slot_at = static_cast<int64_t>(slot[0]) * p.conv_slot;
+    cs_qk_at = slot_at + conv_qk * p.conv_dim_stride;
+    cs_v_at = slot_at + conv_v * p.conv_dim_stride;
+#pragma unroll
+    for (int j = 0; j < kMaxConvLen; ++j) {
+      const int64_t col = min(j, p.conv_len - 1) * p.conv_len_stride;
+      cs_qk[j] = p.conv_state[cs_qk_at + col];
+      cs_v[j] = p.conv_state[cs_v_at + col];
+    }
+    const uint32_t* wq = reinterpret_cast<const uint32_t*>(p.conv_weight + conv_qk * kConvWidth);
+    const uint32_t* wv = reinterpret_cast<const uint32_t*>(p.conv_weight + conv_v * kConvWidth);
+    cw_qk[0] = wq[0];
+    cw_qk[1] = wq[1];
+    cw_v[0] = wv[0];
+    cw_v[1] = wv[1];
+    // Without a bias the weight array stands in as an always-valid source: the loads stay
+    // unconditional (a load under a branch makes the compiler drain every earlier load at
+    // the branch's end) and conv_output ignores the value.
+    const uint16_t* bias_src = p.conv_bias != nullptr ? p.conv_bias : p.conv_weight;
+    cb_qk = bias_src[conv_qk];
+    cb_v = bias_src[conv_v];
+    in0.a = p.a[static_cast<int64_t>(bos) * p.a_row + head];
+    in0.b = p.b[static_cast<int64_t>(bos) * p.b_row + head];
+  } else {
+    in0 = load_token(p, bos, q_col, k_col, v_col + wave * kRowsPerWave + (lane & 31), head, kq);
+  }
   const bool stages_mtp = Width > 1 && wave >= 1 && wave < num_tokens;
   const int64_t token_w = bos + min(wave, num_tokens - 1);
   TokenIn inw;
@@ -385,6 +509,43 @@ void gdn_decode_kernel(const DecodeParams args) {
   }
 
   // ---- staging, while the tile streams in ----
+  if constexpr (Conv) {
+    const int len = p.conv_len;
+    const bool has_bias = p.conv_bias != nullptr;
+    s_conv[tid] = conv_output(cx_qk, cs_qk, cw_qk, cb_qk, has_bias, len);
+    if (tid < kDim) s_conv[2 * kDim + tid] = conv_output(cx_v, cs_v, cw_v, cb_v, has_bias, len);
+    // Shifted state: columns 1..len-1, then the new input.
+#pragma unroll
+    for (int j = 0; j < kMaxConvLen; ++j) {
+      if (j < len) {
+        const uint16_t qk_new = j + 1 < len ? cs_qk[j + 1 < kMaxConvLen ? j + 1 : j] : cx_qk;
+        const uint16_t v_new = j + 1 < len ? cs_v[j + 1 < kMaxConvLen ? j + 1 : j] : cx_v;
+        if (tid < kDim) p.conv_state[cs_v_at + j * p.conv_len_stride] = v_new;  // own channels
+        if (p.group == 1)
+          p.conv_state[cs_qk_at + j * p.conv_len_stride] = qk_new;
+        else
+          s_conv_new[tid][j] = qk_new;
+      }
+    }
+    // Conv outputs visible to every wave; every q/k conv-state read of this workgroup done.
+    lds_barrier();
+    // Non-returning and relaxed: every conv-state value this workgroup read has already been
+    // consumed (the barrier above follows the conv arithmetic), so the increment cannot
+    // overtake a read; a returned value or an ordered atomic would make the compiler drain
+    // the whole tile stream of this wave here.
+    if (p.group > 1 && tid == 0)
+      __hip_atomic_fetch_add(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
+                             1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t* c32 = reinterpret_cast<const uint32_t*>(s_conv);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      in0.q[2 * e] = c32[e * 32 + 2 * kq];
+      in0.q[2 * e + 1] = c32[e * 32 + 2 * kq + 1];
+      in0.k[2 * e] = c32[64 + e * 32 + 2 * kq];
+      in0.k[2 * e + 1] = c32[64 + e * 32 + 2 * kq + 1];
+    }
+    in0.v = s_conv[2 * kDim + wave * kRowsPerWave + (lane & 31)];
+  }
   {
     const Staged x = stage_token(in0, a_log, dt_bias, p.scale);
     if (rsub == 0) {
@@ -469,36 +630,57 @@ void gdn_decode_kernel(const DecodeParams args) {
       orow[v] = f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(gate));
     }
   }
+
+  // ---- conv variant: once the whole k-head group has read the q/k conv state (the count
+  // reached HV/H), a workgroup that sees it writes the shifted copy (identical bytes if
+  // several do) and returns the count to zero; the last incrementer always sees it ----
+  if constexpr (Conv) {
+    uint32_t* const ticket = &g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head];
+    if (p.group > 1 && wave == 0 &&
+        __builtin_amdgcn_readfirstlane(__hip_atomic_load(ticket, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)) ==
+            static_cast<uint32_t>(p.group)) {
+      for (int c = lane; c < 2 * kDim; c += 64) {
+        const int ch = c < kDim ? q_col + c : k_col + (c - kDim);
+        const int64_t at = static_cast<int64_t>(slot[0]) * p.conv_slot + ch * p.conv_dim_stride;
+        for (int j = 0; j < p.conv_len; ++j) p.conv_state[at + j * p.conv_len_stride] = s_conv_new[c][j];
+      }
+      if (lane == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
-template <bool Stream, int Width>
+template <bool Stream, int Width, bool Conv>
 void launch_decode(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
                    hipStream_t stream) {
-  auto kernel = dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, Stream, Width>
-                                  : gdn_decode_kernel<true, false, Stream, Width>)
-                        : (w_bf16 ? gdn_decode_kernel<false, true, Stream, Width>
-                                  : gdn_decode_kernel<false, false, Stream, Width>);
+  auto kernel = dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, Stream, Width, Conv>
+                                  : gdn_decode_kernel<true, false, Stream, Width, Conv>)
+                        : (w_bf16 ? gdn_decode_kernel<false, true, Stream, Width, Conv>
+                                  : gdn_decode_kernel<false, false, Stream, Width, Conv>);
   hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, stream, p);
 }
 
 template <bool Stream>
-void launch_decode(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
-                   hipStream_t stream) {
+void launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
+                   uint32_t blocks, hipStream_t stream) {
+  if (conv) {
+    launch_decode<Stream, 1, true>(p, dt_bf16, w_bf16, blocks, stream);
+    return;
+  }
   switch (p.width) {
-    case 1: launch_decode<Stream, 1>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 2: launch_decode<Stream, 2>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 3: launch_decode<Stream, 3>(p, dt_bf16, w_bf16, blocks, stream); break;
-    default: launch_decode<Stream, 4>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 1: launch_decode<Stream, 1, false>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 2: launch_decode<Stream, 2, false>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 3: launch_decode<Stream, 3, false>(p, dt_bf16, w_bf16, blocks, stream); break;
+    default: launch_decode<Stream, 4, false>(p, dt_bf16, w_bf16, blocks, stream); break;
   }
 }
 
-}  // namespace
-}  // namespace ld
-
-extern "C" int ld_gdn_decode(const ld_gdn_decode_args* args, void* stream) {
-  using namespace ld;
+// Validates the step arguments and fills the kernel parameters; returns LD_OK, or an error
+// code with the message recorded.  *blocks = 0 means there is nothing to launch.
+int prepare(const ld_gdn_decode_args* args, DecodeParams& p, int64_t& blocks) {
   if (args == nullptr) return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_decode: args is NULL");
   const ld_gdn_decode_args& a = *args;
+  blocks = 0;
   if (a.num_requests < 0) return fail(LD_ERR_INVALID_ARGUMENT, "num_requests must be >= 0");
   if (a.width < 1 || a.width > LD_MAX_TOKENS)
     return fail(LD_ERR_INVALID_ARGUMENT, "decode/MTP supports 1 through 4 tokens per request");
@@ -511,15 +693,15 @@ extern "C" int ld_gdn_decode(const ld_gdn_decode_args* args, void* stream) {
   if (a.cache_policy != LD_CACHE_KEEP && a.cache_policy != LD_CACHE_STREAM)
     return fail(LD_ERR_INVALID_ARGUMENT, "cache_policy must be LD_CACHE_KEEP or LD_CACHE_STREAM");
   if (a.num_requests == 0) return LD_OK;
-  if (!a.qkv || !a.a || !a.b || !a.a_log || !a.dt_bias || !a.indices || !a.cu || !a.accepted ||
+  if (!a.a || !a.b || !a.a_log || !a.dt_bias || !a.indices || !a.cu || !a.accepted ||
       !a.state || !a.gate || !a.norm_weight || !a.out)
     return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_decode: NULL tensor pointer");
   if (!aligned16(a.state) || (a.state_slot_stride & 3) != 0)
     return fail(LD_ERR_INVALID_ARGUMENT, "state slots must be 16-byte aligned");
-  const int64_t blocks = static_cast<int64_t>(a.num_requests) * a.num_v_heads;
+  blocks = static_cast<int64_t>(a.num_requests) * a.num_v_heads;
   if (blocks > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "too many (request, head) tiles");
 
-  DecodeParams p;
+  p = DecodeParams{};
   p.qkv = static_cast<const uint16_t*>(a.qkv);
   p.qkv_row = a.qkv_row_stride;
   p.a = static_cast<const uint16_t*>(a.a);
@@ -543,12 +725,66 @@ extern "C" int ld_gdn_decode(const ld_gdn_decode_args* args, void* stream) {
   p.group = a.num_v_heads / a.num_k_heads;
   p.scale = a.scale;
   p.eps = a.eps;
+  return LD_OK;
+}
+
+int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, bool conv,
+           void* stream) {
   const bool dt_bf16 = a.dt_bias_dtype == LD_DTYPE_BF16;
   const bool w_bf16 = a.norm_weight_dtype == LD_DTYPE_BF16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (a.cache_policy == LD_CACHE_STREAM)
-    launch_decode<true>(p, dt_bf16, w_bf16, static_cast<uint32_t>(blocks), s);
+    launch_decode<true>(p, conv, dt_bf16, w_bf16, static_cast<uint32_t>(blocks), s);
   else
-    launch_decode<false>(p, dt_bf16, w_bf16, static_cast<uint32_t>(blocks), s);
-  return check_launch("ld_gdn_decode");
+    launch_decode<false>(p, conv, dt_bf16, w_bf16, static_cast<uint32_t>(blocks), s);
+  return check_launch(conv ? "ld_gdn_decode_conv" : "ld_gdn_decode");
+}
+
+}  // namespace
+}  // namespace ld
+
+extern "C" int ld_gdn_decode(const ld_gdn_decode_args* args, void* stream) {
+  using namespace ld;
+  DecodeParams p;
+  int64_t blocks = 0;
+  const int rc = prepare(args, p, blocks);
+  if (rc != LD_OK || blocks == 0) return rc;
+  if (!args->qkv) return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_decode: NULL tensor pointer");
+  return launch(*args, p, blocks, false, stream);
+}
+
+extern "C" int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_args* conv,
+                                  void* stream) {
+  using namespace ld;
+  if (args == nullptr || conv == nullptr)
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_decode_conv: args or conv is NULL");
+  if (args->width != 1)
+    return fail(LD_ERR_INVALID_ARGUMENT, "the conv-fused step supports 1 token per request");
+  if (conv->width != kConvWidth) return fail(LD_ERR_INVALID_ARGUMENT, "conv width must be 4");
+  if (conv->state_len < kConvWidth - 1 || conv->state_len > kMaxConvLen)
+    return fail(LD_ERR_INVALID_ARGUMENT, "conv state length must be 3 through 8");
+  if (conv->weight_dtype != LD_DTYPE_BF16 ||
+      (conv->bias != nullptr && conv->bias_dtype != LD_DTYPE_BF16))
+    return fail(LD_ERR_INVALID_ARGUMENT, "conv weight and bias must be BF16");
+  if (conv->state_slots < 0 ||
+      conv->state_slots * static_cast<int64_t>(args->num_k_heads) > kMaxConvTickets)
+    return fail(LD_ERR_INVALID_ARGUMENT, "conv state pool too large (slots x k-heads > 2^20)");
+  DecodeParams p;
+  int64_t blocks = 0;
+  const int rc = prepare(args, p, blocks);
+  if (rc != LD_OK || blocks == 0) return rc;
+  if (!conv->x || !conv->state || !conv->weight)
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_decode_conv: NULL tensor pointer");
+  if ((reinterpret_cast<uintptr_t>(conv->weight) & 7) != 0)
+    return fail(LD_ERR_INVALID_ARGUMENT, "conv weight must be 8-byte aligned");
+  p.conv_x = static_cast<const uint16_t*>(conv->x);
+  p.conv_x_row = conv->x_row_stride;
+  p.conv_state = static_cast<uint16_t*>(conv->state);
+  p.conv_slot = conv->state_slot_stride;
+  p.conv_dim_stride = conv->state_dim_stride;
+  p.conv_len_stride = conv->state_len_stride;
+  p.conv_len = conv->state_len;
+  p.conv_weight = static_cast<const uint16_t*>(conv->weight);
+  p.conv_bias = static_cast<const uint16_t*>(conv->bias);
+  return launch(*args, p, blocks, true, stream);
 }

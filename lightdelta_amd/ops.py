@@ -10,6 +10,12 @@ Argument validation raises RuntimeError with the reference's messages
 Additive ops (no reference counterpart):
   copy_state(pool, src, dst)            slot -> slot copy inside one pool (MTP commit,
                                         slot reuse), any dtype, padding slot <= 0 skipped
+  decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, <decode args without qkv>)
+                                        causal conv1d (width 4, SiLU, bf16 output) of the
+                                        pre-conv activations fused into the decode step;
+                                        conv_state [slots, conv_dim, state_len] (any strides,
+                                        so vLLM's transposed dim-last view works), one token
+                                        per request
   gather_slots / scatter_slots          dtype-generic gather_state / scatter_state, for the
                                         bf16 conv-state pool and any dense-inner pool
 
@@ -34,6 +40,12 @@ SCHEMAS = {
     "gather_state": "gather_state(Tensor pool, Tensor slots, Tensor valid, Tensor(o!) out) -> ()",
     "scatter_state": "scatter_state(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
     "copy_state": "copy_state(Tensor(p!) pool, Tensor src, Tensor dst) -> ()",
+    "decode_conv": (
+        "decode_conv(Tensor mixed_qkv, Tensor(c!) conv_state, Tensor conv_weight, "
+        "Tensor? conv_bias, Tensor a, Tensor b, Tensor a_log, Tensor dt_bias, Tensor indices, "
+        "Tensor cu, Tensor accepted, Tensor(s!) state, Tensor gate, Tensor weight, "
+        "Tensor(o!) out, float eps) -> ()"
+    ),
     "gather_slots": "gather_slots(Tensor pool, Tensor slots, Tensor valid, Tensor(o!) out) -> ()",
     "scatter_slots": "scatter_slots(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
 }
@@ -228,6 +240,64 @@ def _decode_impl(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, 
         _lib.check(lib.ld_gdn_decode(args, _stream(qkv.device)))
 
 
+def check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log, dt_bias,
+                      indices, cu, accepted, state, gate, weight, out, eps):
+    """Validation of decode_conv: decode's checks on the pre-conv activations, plus the conv
+    pool, weight and bias."""
+    h, hv = check_decode(mixed_qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate,
+                         weight, out, eps)
+    conv_dim = mixed_qkv.shape[1]
+    _require(indices.shape[1] == 1, "the conv-fused step supports 1 token per request")
+    _require(
+        conv_state.device == mixed_qkv.device
+        and conv_state.dtype == torch.bfloat16
+        and conv_state.dim() == 3
+        and conv_state.shape[1] == conv_dim
+        and 3 <= conv_state.shape[2] <= 8,
+        "conv_state must be CUDA BF16 [slots, conv_dim, 3..8]",
+    )
+    _require(
+        conv_weight.device == mixed_qkv.device
+        and conv_weight.dtype == torch.bfloat16
+        and tuple(conv_weight.shape) == (conv_dim, 4)
+        and conv_weight.is_contiguous()
+        and conv_weight.data_ptr() % 8 == 0,
+        "conv_weight must be contiguous CUDA BF16 [conv_dim, 4]",
+    )
+    if conv_bias is not None:
+        _require(
+            conv_bias.device == mixed_qkv.device
+            and conv_bias.dtype == torch.bfloat16
+            and conv_bias.numel() == conv_dim
+            and conv_bias.is_contiguous(),
+            "conv_bias must be contiguous CUDA BF16 [conv_dim]",
+        )
+    return h, hv
+
+
+def _decode_conv_impl(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log, dt_bias,
+                      indices, cu, accepted, state, gate, weight, out, eps):
+    h, hv = check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log,
+                              dt_bias, indices, cu, accepted, state, gate, weight, out, eps)
+    requests = indices.shape[0]
+    args = _lib.DecodeArgs(
+        0, 0, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), a_log.data_ptr(),
+        dt_bias.data_ptr(), _dtype_code(dt_bias), _dtype_code(weight), indices.data_ptr(),
+        cu.data_ptr(), accepted.data_ptr(), state.data_ptr(), state.stride(0),
+        gate.data_ptr(), gate.stride(0), weight.data_ptr(), out.data_ptr(), requests, 1, h,
+        hv, QK_SCALE, eps, _cache_policy,
+    )
+    conv = _lib.ConvArgs(
+        mixed_qkv.data_ptr(), mixed_qkv.stride(0), conv_state.data_ptr(), conv_state.shape[0],
+        conv_state.stride(0), conv_state.stride(1), conv_state.stride(2), conv_state.shape[2], 4,
+        conv_weight.data_ptr(), _lib.DTYPE_BF16, _lib.DTYPE_BF16,
+        None if conv_bias is None else conv_bias.data_ptr(),
+    )
+    lib = _lib.load()
+    with _DeviceGuard(mixed_qkv.device):
+        _lib.check(lib.ld_gdn_decode_conv(args, conv, _stream(mixed_qkv.device)))
+
+
 # ---------------------------------------------------------------------------------------
 # state-pool copies
 # ---------------------------------------------------------------------------------------
@@ -399,6 +469,7 @@ _IMPLS = {
     "gather_state": _gather_state_impl,
     "scatter_state": _scatter_state_impl,
     "copy_state": _copy_state_impl,
+    "decode_conv": _decode_conv_impl,
     "gather_slots": _gather_slots_impl,
     "scatter_slots": _scatter_slots_impl,
 }

@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import torch
 
+from . import conv as conv_oracle
 from . import gdn
 
 HEAD_DIM = 128
@@ -122,3 +123,29 @@ def packed_reference_step(qkv, a, b, a_log, dt_bias, slots, cu, accepted, pool, 
     destinations = torch.where(live & valid[:, None] & (slots > 0), slots, 0).flatten()
     keep = destinations[:, None, None, None] > 0
     pool.index_copy_(0, destinations.long(), torch.where(keep, states, pool[0]))
+
+
+def expected_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log, dt_bias,
+                         indices, cu, accepted, pool, gate, weight, out, eps, *, return_pre=False):
+    """Expected (out, pool, conv_state) after one conv-fused decode call: the conv update
+    (oracle/conv.py) of every valid single-token request on conv slot indices[r, 0], then
+    expected_decode on the post-conv activations.  Invalid requests touch neither pool.
+    Returns (out, pool[, pre], conv_state, post), post being the bf16 post-conv activation
+    matrix the GDN step consumed."""
+    mixed = mixed_qkv.cpu()
+    cstate = conv_state.cpu().clone()
+    indices_c, cu_c, accepted_c = indices.cpu().long(), cu.cpu().long(), accepted.cpu().long()
+    post = mixed.clone()
+    for r in range(indices_c.shape[0]):
+        bos, eos = int(cu_c[r]), int(cu_c[r + 1])
+        slot = int(indices_c[r, 0])
+        if eos - bos != 1 or int(accepted_c[r]) != 1 or slot <= 0:
+            continue
+        y, new_state = conv_oracle.conv_update(
+            mixed[bos:eos], cstate[slot][None], conv_weight.cpu(),
+            None if conv_bias is None else conv_bias.cpu())
+        post[bos:eos] = y
+        cstate[slot] = new_state[0]
+    result = expected_decode(post, a, b, a_log, dt_bias, indices, cu, accepted, pool, gate,
+                             weight, out, eps, return_pre=return_pre)
+    return result + (cstate, post)

@@ -22,8 +22,8 @@ def declared_functions() -> set[str]:
 
 def test_header_declares_the_entry_points():
     assert declared_functions() == {
-        "ld_gdn_decode", "ld_state_gather", "ld_state_scatter", "ld_state_copy",
-        "ld_last_error", "ld_abi_version",
+        "ld_gdn_decode", "ld_gdn_decode_conv", "ld_state_gather", "ld_state_scatter",
+        "ld_state_copy", "ld_last_error", "ld_abi_version",
     }
 
 
@@ -35,12 +35,14 @@ def test_library_exports_every_declared_symbol():
     assert lib.ld_abi_version() == _lib.ABI_VERSION
 
 
-def test_decode_args_layout_matches_header():
-    """ctypes mirror of ld_gdn_decode_args: same field names in the same order."""
+@pytest.mark.parametrize("struct,mirror", [("ld_gdn_decode_args", _lib.DecodeArgs),
+                                           ("ld_conv_args", _lib.ConvArgs)])
+def test_args_layout_matches_header(struct, mirror):
+    """ctypes mirrors of the argument structs: same field names in the same order."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    body = re.search(r"typedef struct ld_gdn_decode_args \{(.*?)\}", text, flags=re.S).group(1)
+    body = re.search(r"typedef struct " + struct + r" \{(.*?)\}", text, flags=re.S).group(1)
     fields = re.findall(r"(\w+);", body)
-    assert fields == [name for name, _ in _lib.DecodeArgs._fields_]
+    assert fields == [name for name, _ in mirror._fields_]
 
 
 @pytest.mark.parametrize("width,heads,eps,message", [
@@ -72,6 +74,29 @@ def test_empty_work_is_a_no_op():
     assert lib.ld_gdn_decode(ctypes.byref(args), None) == 0
     assert lib.ld_state_copy(None, 0, None, None, 0, 2048, None) == 0
     assert lib.ld_state_gather(None, 0, None, 1, None, None, 0, 2048, 0, None) == 0
+
+
+def test_decode_conv_rejects_multi_token_and_bad_conv_shapes():
+    lib = _lib.load()
+    args = _lib.DecodeArgs()
+    args.num_requests = 1
+    args.num_k_heads, args.num_v_heads = 16, 32
+    args.eps = 1e-6
+    conv = _lib.ConvArgs()
+    conv.width, conv.state_len, conv.weight_dtype = 4, 3, _lib.DTYPE_BF16
+    args.width = 2
+    assert lib.ld_gdn_decode_conv(ctypes.byref(args), ctypes.byref(conv), None) == 1
+    assert "1 token per request" in lib.ld_last_error().decode()
+    args.width = 1
+    conv.width = 3
+    assert lib.ld_gdn_decode_conv(ctypes.byref(args), ctypes.byref(conv), None) == 1
+    assert "conv width must be 4" in lib.ld_last_error().decode()
+    conv.width, conv.state_len = 4, 9
+    assert lib.ld_gdn_decode_conv(ctypes.byref(args), ctypes.byref(conv), None) == 1
+    assert "3 through 8" in lib.ld_last_error().decode()
+    conv.state_len, conv.state_slots = 3, (1 << 20)
+    assert lib.ld_gdn_decode_conv(ctypes.byref(args), ctypes.byref(conv), None) == 1
+    assert "too large" in lib.ld_last_error().decode()
 
 
 def test_copy_rejects_misaligned_rows():

@@ -1,0 +1,122 @@
+"""Pins the conv oracle (oracle/conv.py) definitionally: against
+torch.nn.functional.conv1d with groups = channels and against an element loop, plus the
+state shift.  No reference test or fixture covers the conv (it lives in vLLM), so the conv
+is "parity unpinned" beyond these definitional checks."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+import pytest
+import torch
+
+from oracle import conv
+
+
+def case(seed, batch=3, channels=6, length=3, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, channels, generator=g).bfloat16()
+    state = torch.randn(batch, channels, length, generator=g).bfloat16()
+    weight = (torch.randn(channels, 4, generator=g) / 2).bfloat16()
+    b = torch.randn(channels, generator=g).bfloat16() if bias else None
+    return x, state, weight, b
+
+
+@pytest.mark.parametrize("length,bias", [(3, False), (3, True), (4, False), (6, True)])
+def test_conv_matches_conv1d_groups(length, bias):
+    x, state, weight, b = case(length, length=length, bias=bias)
+    y, _ = conv.conv_update(x, state, weight, b)
+    ref = conv.conv_update_reference_form(x, state, weight, b)
+    # both round an fp32 sum of 4 products (+ bias) to bf16; summation order may differ
+    torch.testing.assert_close(y.float(), ref.float(), rtol=8e-3, atol=1e-2)
+
+
+def test_conv_element_loop_and_state_shift():
+    x, state, weight, b = case(1, batch=2, channels=4, length=5)
+    y, new_state = conv.conv_update(x, state, weight, b)
+    for r in range(2):
+        for d in range(4):
+            window = [float(state[r, d, j]) for j in range(2, 5)] + [float(x[r, d])]
+            acc = float(b[d]) + sum(float(weight[d, j]) * window[j] for j in range(4))
+            expect = acc / (1 + math.exp(-acc))
+            assert abs(float(y[r, d]) - expect) <= 0.008 * abs(expect) + 1e-3
+            assert [float(v) for v in new_state[r, d]] == [float(state[r, d, j]) for j in range(1, 5)] + [float(x[r, d])]
+
+
+def loop_check(x, state, weight, b, y):
+    """The element-loop statement of the conv, as a pass/fail predicate."""
+    length = state.shape[-1]
+    for r in range(x.shape[0]):
+        for d in range(x.shape[1]):
+            window = [float(state[r, d, j]) for j in range(length - 3, length)] + [float(x[r, d])]
+            acc = (float(b[d]) if b is not None else 0.0) + sum(
+                float(weight[d, j]) * window[j] for j in range(4))
+            expect = acc / (1 + math.exp(-acc))
+            if abs(float(y[r, d]) - expect) > 0.008 * abs(expect) + 1e-3:
+                return False
+    return True
+
+
+@pytest.mark.parametrize("mistake", ["reversed_taps", "oldest_window", "dropped_bias", "no_silu"])
+def test_planted_conv_mistakes_fail_the_loop_check(mistake):
+    x, state, weight, b = case(7, batch=2, channels=8, length=4)
+    assert loop_check(x, state, weight, b, conv.conv_update(x, state, weight, b)[0])
+    if mistake == "reversed_taps":
+        y = conv.conv_update(x, state, weight.flip(1), b)[0]
+    elif mistake == "oldest_window":  # window from the first state columns instead of the last
+        y = conv.conv_update(x, torch.cat([state[..., :3], state[..., :1]], -1), weight, b)[0]
+    elif mistake == "dropped_bias":
+        y = conv.conv_update(x, state, weight, None)[0]
+    else:
+        window = torch.cat([state[..., 1:], x[..., None]], -1).float()
+        y = ((window * weight.float()).sum(-1) + b.float()).bfloat16()
+    assert not loop_check(x, state, weight, b, y)
+
+
+def test_fma_chain_and_correct_rounding():
+    """The oracle's conv output is the float64 SiLU of an fp32 fma chain (one rounding per
+    tap, oldest first), rounded once to the nearest bf16."""
+    x, state, weight, b = case(3, batch=2, channels=5, length=3)
+    y, _ = conv.conv_update(x, state, weight, b)
+    for r in range(2):
+        for d in range(5):
+            window = [float(state[r, d, j]) for j in range(3)] + [float(x[r, d])]
+            acc = np.float32(float(b[d]))
+            for j in range(4):
+                acc = np.float32(np.float64(weight[d, j].item()) * window[j] + np.float64(acc))
+            exact = float(acc) / (1 + math.exp(-float(acc)))
+            assert float(y[r, d]) == float(nearest_bf16(exact))
+
+
+def nearest_bf16(v: float) -> float:
+    """Brute force: the bf16 nearest to v (ties to the even significand)."""
+    t = torch.tensor([v], dtype=torch.float64).float()
+    bits = int(t.view(torch.int32)) & 0xFFFFFFFF
+    lo = torch.tensor([(bits >> 16) << 16], dtype=torch.int64).to(torch.int32).view(torch.float32)
+    hi = torch.tensor([((bits >> 16) + 1) << 16], dtype=torch.int64).to(torch.int32).view(
+        torch.float32)
+    lo, hi = float(lo), float(hi)
+    dl, dh = abs(v - lo), abs(v - hi)
+    if dl != dh:
+        return lo if dl < dh else hi
+    return lo if ((bits >> 16) & 1) == 0 else hi
+
+
+def test_round_to_bf16_is_single_rounding():
+    """Against brute force, on values whose fp32 rounding lands exactly on a bf16 midpoint
+    (where rounding through fp32 would round twice) and on random values."""
+    rng = np.random.default_rng(0)
+    mids = (rng.integers(0x3C00, 0x4200, 200).astype(np.uint32) << 16) | 0x8000
+    mid_vals = mids.view(np.float32).astype(np.float64)
+    # nudge off the midpoint by less than half an fp32 ulp: fp32 rounds back onto it
+    nudged = mid_vals * (1 + rng.choice([-1.0, 1.0], 200) * rng.uniform(1e-9, 2.5e-8, 200))
+    assert (nudged.astype(np.float32) == mid_vals.astype(np.float32)).all()
+    through_fp32 = torch.from_numpy(nudged.astype(np.float32)).to(torch.bfloat16).float()
+    values = np.concatenate([nudged, mid_vals, rng.normal(0, 3, 300)])
+    got = conv.round_to_bf16(values).float().numpy()
+    want = np.array([nearest_bf16(float(v)) for v in values])
+    np.testing.assert_array_equal(got, want)
+    # the double rounding the oracle avoids would disagree on some of the nudged values
+    assert (through_fp32.numpy() != got[:200]).any()
