@@ -60,6 +60,7 @@ def parse_args():
                    help="bound on the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-cold", action="store_true")
+    p.add_argument("--no-conv", action="store_true")
     p.add_argument("--no-graph", action="store_true",
                    help="time K eager launches instead of one K-step graph replay")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -153,6 +154,37 @@ def cpu_baseline(seconds: float) -> dict:
         "sample": f"{len(times)} steps of the packed Torch reference path (index_select gather, "
                   f"unfused GDN, index_copy_ write-back) at B=32, 16/32 heads, 256-slot pool; "
                   f"median step {median * 1e3:.1f} ms; {cpu}",
+    }
+
+
+def conv_fused(case, op_args, steps, device):
+    """The same step with the causal conv1d (width 4, SiLU, conv state of 3 columns, bf16
+    pool of 256 slots x 8192 channels) fused in front: one decode_conv launch per step on the
+    pre-conv activations."""
+    import torch
+
+    conv_dim = case["qkv"].shape[1]
+    gen = torch.Generator().manual_seed(1)
+    conv_state = torch.randn(POOL, conv_dim, 3, generator=gen).bfloat16().to(device)
+    conv_weight = (torch.randn(conv_dim, 4, generator=gen) / 2).bfloat16().to(device)
+    rest = op_args[1:]
+    step = lambda: torch.ops.lightdelta.decode_conv(  # noqa: E731
+        case["qkv"], conv_state, conv_weight, None, *rest, 1e-6)
+    for _ in range(4):
+        step()
+    graph = capture(step, steps)
+    graph.replay()
+    torch.cuda.synchronize()
+    elapsed = timed_replay(graph)
+    rate = steps / elapsed
+    conv_bytes = BATCH * conv_dim * 3 * 2 * 2  # conv state columns read + written
+    return {
+        "workload": "same step with the width-4 causal conv1d + SiLU fused in front "
+                    "(bf16 conv pool 256 x 8192 x 3, no bias)",
+        "steps_per_s": round(rate, 1),
+        "us_per_step": round(elapsed * 1e6 / steps, 3),
+        "state_TBps": round(STATE_BYTES * rate / 1e12, 3),
+        "frac": round((STATE_BYTES + conv_bytes) * rate / 1e9 / HBM_PEAK_GBS, 4),
     }
 
 
@@ -287,6 +319,9 @@ def main():
             "frac": round(STATE_BYTES * cold_rate / 1e9 / HBM_PEAK_GBS, 4),
         }
         del big
+
+    if not args.no_conv:
+        result["conv_fused"] = conv_fused(case, op_args, args.steps, device)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

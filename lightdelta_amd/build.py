@@ -31,6 +31,10 @@ HIPCC_FLAGS = [
     "-Werror=return-type",
     # Packed fp32 VALU forms are kept out of the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Atomics stay as written: the optimizer's wave-aggregated form of a returning atomic
+    # consumes the result at once, which waits for every load in flight (the conv-state
+    # ticket count is issued mid-kernel and first read at the end).
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]

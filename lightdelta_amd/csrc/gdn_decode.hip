@@ -296,7 +296,8 @@ __device__ __forceinline__ uint16_t silu_bf16(float x) {
 //   bf16(silu(bias + sum_j w[j] * [state[len-3], state[len-2], state[len-1], x][j]))
 // with the fp32 accumulation running from the oldest tap to the newest (one rounding per
 // fused multiply-add) and the SiLU correctly rounded to bf16.
-__device__ __forceinline__ uint16_t conv_output(uint16_t x, const uint16_t (&state)[kMaxConvLen],
+template <int N>
+__device__ __forceinline__ uint16_t conv_output(uint16_t x, const uint16_t (&state)[N],
                                                 const uint32_t (&w)[2], uint16_t bias,
                                                 bool has_bias, int len) {
   uint16_t tap[3];
@@ -305,7 +306,7 @@ __device__ __forceinline__ uint16_t conv_output(uint16_t x, const uint16_t (&sta
     // state[len - 3 + i], selected without dynamic register indexing
     uint16_t v = state[0];
 #pragma unroll
-    for (int j = 1; j < kMaxConvLen; ++j)
+    for (int j = 1; j < N; ++j)
       if (j == len - 3 + i) v = state[j];
     tap[i] = v;
   }
@@ -335,14 +336,17 @@ __device__ __forceinline__ void lds_barrier() {
 // outputs to bf16 (the dtype an unfused conv writes) and feeds them to the GDN step.  Its
 // own v channels' conv state is shifted in place.  The q/k channels are shared by the
 // HV/H workgroups of a k-head group, so their shifted state is written only after all of
-// them have read it: every workgroup counts itself in (atomic add on
-// g_conv_ticket[slot*H + kh]) after its reads; at its end, a workgroup that finds the count
-// at HV/H writes the shifted state and resets the count to 0.  The last to count in always
-// finds it, so the state is written at least once (several writers write identical bytes).
-// Nothing waits on another workgroup, and every launch leaves the counts at zero.
-template <bool DtBf16, bool WBf16, bool Stream, int Width, bool Conv>
+// them have read it: every workgroup counts itself in (relaxed atomic add on
+// g_conv_ticket[slot*H + kh], returning the previous count) after its reads; the one that
+// receives HV/H - 1 counted in last, writes the shifted state at its end and resets the
+// count to 0.  Nothing waits on another workgroup, and every launch leaves the counts at
+// zero.  ConvCols: conv-state columns held per channel (4 for states of 3..4 columns, 8 for
+// up to 8; 0 = no conv).
+template <bool DtBf16, bool WBf16, bool Stream, int Width, int ConvCols>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void gdn_decode_kernel(const DecodeParams args) {
+  constexpr bool Conv = ConvCols > 0;
+  constexpr int kCols = Conv ? ConvCols : 1;
   static_assert(!Conv || Width == 1, "the conv-fused step is single-token");
   // Every kernel argument, then all request metadata, is loaded before the first branch:
   // two dependent scalar round trips (kernel-argument segment; cu/accepted/indices) instead
@@ -418,7 +422,8 @@ void gdn_decode_kernel(const DecodeParams args) {
   // Conv variant: bf16 conv outputs of the 256 q/k channels and 128 v channels, and the
   // shifted q/k conv state kept for the end-of-kernel write.
   __shared__ uint16_t s_conv[Conv ? 3 * kDim : 2];
-  __shared__ uint16_t s_conv_new[Conv ? 2 * kDim : 1][Conv ? kMaxConvLen : 1];
+  __shared__ uint16_t s_conv_new[Conv ? 2 * kDim : 1][kCols];
+  __shared__ uint32_t s_arrived;
 
   const int key_head = head / p.group;
   const int kq = lane & 15;
@@ -439,8 +444,9 @@ void gdn_decode_kernel(const DecodeParams args) {
   const int conv_v = v_col + (tid & (kDim - 1));
   int64_t cs_qk_at = 0, cs_v_at = 0;
   uint16_t cx_qk = 0, cx_v = 0, cb_qk = 0, cb_v = 0;
-  uint16_t cs_qk[kMaxConvLen], cs_v[kMaxConvLen];
+  uint16_t cs_qk[kCols], cs_v[kCols];
   uint32_t cw_qk[2], cw_v[2];
+  uint32_t arrived = 0;  // ticket count before this workgroup's increment (thread 0)
   if constexpr (Conv) {
     const uint16_t* xrow = p.conv_x + static_cast<int64_t>(bos) * p.conv_x_row;
     cx_qk = xrow[conv_qk];
@@ -449,7 +455,7 @@ void gdn_decode_kernel(const DecodeParams args) {
     cs_qk_at = slot_at + conv_qk * p.conv_dim_stride;
     cs_v_at = slot_at + conv_v * p.conv_dim_stride;
 #pragma unroll
-    for (int j = 0; j < kMaxConvLen; ++j) {
+    for (int j = 0; j < kCols; ++j) {
       const int64_t col = min(j, p.conv_len - 1) * p.conv_len_stride;
       cs_qk[j] = p.conv_state[cs_qk_at + col];
       cs_v[j] = p.conv_state[cs_v_at + col];
@@ -514,28 +520,28 @@ void gdn_decode_kernel(const DecodeParams args) {
     const bool has_bias = p.conv_bias != nullptr;
     s_conv[tid] = conv_output(cx_qk, cs_qk, cw_qk, cb_qk, has_bias, len);
     if (tid < kDim) s_conv[2 * kDim + tid] = conv_output(cx_v, cs_v, cw_v, cb_v, has_bias, len);
-    // Shifted state: columns 1..len-1, then the new input.
+    // Shifted state: columns 1..len-1, then the new input.  The v channels (this
+    // workgroup's alone) are shifted in place now; threads 128..255 repeat the stores of
+    // threads 0..127 with identical bytes, and columns past len-1 repeat column len-1, so
+    // the stores need no branch (a store under a branch makes later load waits conservative).
+    // The q/k channels are kept for the end-of-kernel write.
 #pragma unroll
-    for (int j = 0; j < kMaxConvLen; ++j) {
-      if (j < len) {
-        const uint16_t qk_new = j + 1 < len ? cs_qk[j + 1 < kMaxConvLen ? j + 1 : j] : cx_qk;
-        const uint16_t v_new = j + 1 < len ? cs_v[j + 1 < kMaxConvLen ? j + 1 : j] : cx_v;
-        if (tid < kDim) p.conv_state[cs_v_at + j * p.conv_len_stride] = v_new;  // own channels
-        if (p.group == 1)
-          p.conv_state[cs_qk_at + j * p.conv_len_stride] = qk_new;
-        else
-          s_conv_new[tid][j] = qk_new;
-      }
+    for (int j = 0; j < kCols; ++j) {
+      const uint16_t qk_new = j + 1 < len ? cs_qk[j + 1 < kCols ? j + 1 : j] : cx_qk;
+      const uint16_t v_new = j + 1 < len ? cs_v[j + 1 < kCols ? j + 1 : j] : cx_v;
+      p.conv_state[cs_v_at + min(j, len - 1) * p.conv_len_stride] = v_new;
+      s_conv_new[tid][j] = qk_new;
     }
     // Conv outputs visible to every wave; every q/k conv-state read of this workgroup done.
     lds_barrier();
-    // Non-returning and relaxed: every conv-state value this workgroup read has already been
-    // consumed (the barrier above follows the conv arithmetic), so the increment cannot
-    // overtake a read; a returned value or an ordered atomic would make the compiler drain
-    // the whole tile stream of this wave here.
+    // Relaxed: every conv-state value this workgroup read has already been consumed (the
+    // barrier above follows the conv arithmetic), so the increment cannot overtake a read.
+    // The returned count is first used at the kernel's end, by which time it has long
+    // arrived: no wait on the tile stream here, and no extra round trip there.
     if (p.group > 1 && tid == 0)
-      __hip_atomic_fetch_add(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
-                             1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      arrived = __hip_atomic_fetch_add(
+          &g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head], 1u,
+          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t* c32 = reinterpret_cast<const uint32_t*>(s_conv);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -608,6 +614,9 @@ void gdn_decode_kernel(const DecodeParams args) {
   LD_CHUNK(2)
   LD_CHUNK(3)
 #undef LD_CHUNK
+  if constexpr (Conv) {
+    if (tid == 0) s_arrived = arrived;
+  }
   lds_barrier();
 
   // ---- gated RMSNorm epilogue for token `wave` ----
@@ -631,47 +640,49 @@ void gdn_decode_kernel(const DecodeParams args) {
     }
   }
 
-  // ---- conv variant: once the whole k-head group has read the q/k conv state (the count
-  // reached HV/H), a workgroup that sees it writes the shifted copy (identical bytes if
-  // several do) and returns the count to zero; the last incrementer always sees it ----
+  // ---- conv variant: the only workgroup of its k-head (HV == H), or the one that counted
+  // in last (all HV/H of the k-head group had read the q/k conv state before it), writes the
+  // shifted q/k conv state and returns the count to zero for the next launch ----
   if constexpr (Conv) {
-    uint32_t* const ticket = &g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head];
-    if (p.group > 1 && wave == 0 &&
-        __builtin_amdgcn_readfirstlane(__hip_atomic_load(ticket, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT)) ==
-            static_cast<uint32_t>(p.group)) {
-      for (int c = lane; c < 2 * kDim; c += 64) {
+    if (p.group == 1 || s_arrived == static_cast<uint32_t>(p.group - 1)) {
+      const int64_t slot_at = static_cast<int64_t>(slot[0]) * p.conv_slot;
+      for (int c = tid; c < 2 * kDim; c += kThreads) {
         const int ch = c < kDim ? q_col + c : k_col + (c - kDim);
-        const int64_t at = static_cast<int64_t>(slot[0]) * p.conv_slot + ch * p.conv_dim_stride;
+        const int64_t at = slot_at + ch * p.conv_dim_stride;
         for (int j = 0; j < p.conv_len; ++j) p.conv_state[at + j * p.conv_len_stride] = s_conv_new[c][j];
       }
-      if (lane == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (p.group > 1 && tid == 0)
+        __hip_atomic_store(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
+                           0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
 
-template <bool Stream, int Width, bool Conv>
+template <bool Stream, int Width, int ConvCols>
 void launch_decode(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
                    hipStream_t stream) {
-  auto kernel = dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, Stream, Width, Conv>
-                                  : gdn_decode_kernel<true, false, Stream, Width, Conv>)
-                        : (w_bf16 ? gdn_decode_kernel<false, true, Stream, Width, Conv>
-                                  : gdn_decode_kernel<false, false, Stream, Width, Conv>);
+  auto kernel = dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, Stream, Width, ConvCols>
+                                  : gdn_decode_kernel<true, false, Stream, Width, ConvCols>)
+                        : (w_bf16 ? gdn_decode_kernel<false, true, Stream, Width, ConvCols>
+                                  : gdn_decode_kernel<false, false, Stream, Width, ConvCols>);
   hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, stream, p);
 }
 
 template <bool Stream>
 void launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
                    uint32_t blocks, hipStream_t stream) {
-  if (conv) {
-    launch_decode<Stream, 1, true>(p, dt_bf16, w_bf16, blocks, stream);
+  if (conv) {  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
+    if (p.conv_len <= 4)
+      launch_decode<Stream, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
+    else
+      launch_decode<Stream, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
     return;
   }
   switch (p.width) {
-    case 1: launch_decode<Stream, 1, false>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 2: launch_decode<Stream, 2, false>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 3: launch_decode<Stream, 3, false>(p, dt_bf16, w_bf16, blocks, stream); break;
-    default: launch_decode<Stream, 4, false>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 1: launch_decode<Stream, 1, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 2: launch_decode<Stream, 2, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 3: launch_decode<Stream, 3, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
+    default: launch_decode<Stream, 4, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
   }
 }
 
