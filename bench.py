@@ -61,6 +61,9 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-cold", action="store_true")
     p.add_argument("--no-conv", action="store_true")
+    p.add_argument("--no-stack", action="store_true",
+                   help="skip the 48-layer, 96 GiB stack measurement")
+    p.add_argument("--stack-steps", type=int, default=256)
     p.add_argument("--no-graph", action="store_true",
                    help="time K eager launches instead of one K-step graph replay")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -185,6 +188,62 @@ def conv_fused(case, op_args, steps, device):
         "us_per_step": round(elapsed * 1e6 / steps, 3),
         "state_TBps": round(STATE_BYTES * rate / 1e12, 3),
         "frac": round((STATE_BYTES + conv_bytes) * rate / 1e9 / HBM_PEAK_GBS, 4),
+    }
+
+
+def stack48(steps, device):
+    """48 GDN decode layers captured as one HIP graph, batch 128, 16 qk / 32 v heads, 1024
+    slots per layer (96 GiB fp32 state), stream cache policy; the slot ids (shared by every
+    layer) are reshuffled before every replay by a device-to-device copy from a table of
+    random distinct ids.  `steps` replays are timed end to end, reshuffles included."""
+    import torch
+
+    from lightdelta_amd import ops
+    from lightdelta_amd.workloads import stack_case, stack_layer
+
+    layers_n, batch, slots_n = 48, 128, 1024
+    case = stack_case(layers_n, batch, pool_slots=slots_n, seed=5, device=device)
+    layers = [stack_layer(case, layer) for layer in range(layers_n)]
+
+    def step():
+        for a in layers:
+            torch.ops.lightdelta.decode(*[a[k] for k in ORDER], 1e-6)
+
+    policy = ops.state_cache_policy()
+    ops.set_state_cache_policy("stream")
+    try:
+        step()
+        graph = capture(step, 1)
+    finally:
+        ops.set_state_cache_policy(policy)
+    gen = torch.Generator().manual_seed(6)
+    table = torch.stack([torch.randperm(slots_n - 1, generator=gen)[:batch] + 1
+                         for _ in range(steps)]).to(torch.int32).view(steps, batch, 1).to(device)
+    for i in range(2):  # untimed warm-up replays
+        case["slots"].copy_(table[i])
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = events()
+    start.record()
+    for i in range(steps):
+        case["slots"].copy_(table[i])
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    elapsed = start.elapsed_time(end) / 1000.0
+    step_bytes = layers_n * batch * HV * DIM * DIM * 4 * 2
+    rate = steps / elapsed
+    return {
+        "workload": "48-layer stack of decode steps in one HIP graph, batch 128, 16 qk / 32 v "
+                    "heads, 1024 slots per layer (96 GiB fp32 state), slot ids reshuffled "
+                    "before every replay, stream cache policy",
+        "steps": steps,
+        "ms_per_step": round(elapsed * 1000.0 / steps, 4),
+        "steps_per_s": round(rate, 2),
+        "tokens_per_s": round(rate * batch, 1),
+        "state_bytes_per_step": step_bytes,
+        "state_TBps": round(step_bytes * rate / 1e12, 3),
+        "frac": round(step_bytes * rate / 1e9 / HBM_PEAK_GBS, 4),
     }
 
 
@@ -322,6 +381,11 @@ def main():
 
     if not args.no_conv:
         result["conv_fused"] = conv_fused(case, op_args, args.steps, device)
+
+    if not args.no_stack:
+        case = op_args = graph = None  # noqa: F841  (release the B=32 pools first)
+        torch.cuda.empty_cache()
+        result["stack48"] = stack48(args.stack_steps, device)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -72,3 +72,44 @@ def decode_case(
         )
         case = moved
     return case
+
+
+def stack_case(layers: int, batch: int, *, num_k_heads: int = 16, num_v_heads: int = 32,
+               pool_slots: int = 1024, seed: int = 0, device="cuda") -> dict:
+    """A stack of `layers` GDN decode layers, one token per request: per-layer activations,
+    parameters and state pool (one [layers, pool_slots, HV, 128, 128] fp32 tensor), and one
+    slots/cu/accepted set shared by every layer (a request keeps its slot id in every
+    layer).  Same distributions as decode_case; generated on `device`."""
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    qkv_cols = (2 * num_k_heads + num_v_heads) * HEAD_DIM
+    gate_cols = num_v_heads * HEAD_DIM
+    qkvz = torch.randn(layers, batch, qkv_cols + gate_cols, generator=gen, device=dev).bfloat16()
+    ba = torch.randn(layers, batch, 2 * num_v_heads, generator=gen, device=dev).bfloat16()
+    pool = torch.empty(layers, pool_slots, num_v_heads, HEAD_DIM, HEAD_DIM, device=dev)
+    for layer in range(layers):
+        pool[layer].normal_(0.0, 0.02, generator=gen)
+    cpu_gen = torch.Generator().manual_seed(seed)
+    slots = (torch.randperm(pool_slots - 1, generator=cpu_gen)[:batch] + 1).to(torch.int32)
+    return dict(
+        qkv=qkvz[:, :, :qkv_cols],
+        a=ba[:, :, num_v_heads:],
+        b=ba[:, :, :num_v_heads],
+        a_log=(torch.rand(layers, num_v_heads, generator=gen, device=dev) * 2 - 1),
+        dt_bias=torch.zeros(layers, num_v_heads, device=dev),
+        slots=slots.view(batch, 1).to(dev),
+        cu=torch.arange(0, batch + 1, dtype=torch.int32, device=dev),
+        accepted=torch.ones(batch, dtype=torch.int32, device=dev),
+        pool=pool,
+        gate=qkvz[:, :, qkv_cols:].unflatten(-1, (num_v_heads, HEAD_DIM)),
+        weight=1 + 0.1 * torch.randn(layers, HEAD_DIM, generator=gen, device=dev),
+        out=torch.zeros(layers, batch, num_v_heads, HEAD_DIM, dtype=torch.bfloat16, device=dev),
+    )
+
+
+STACK_SHARED = ("slots", "cu", "accepted")
+
+
+def stack_layer(case: dict, layer: int) -> dict:
+    """Arguments of layer `layer` of a stack_case, keyed like decode_case."""
+    return {k: (v if k in STACK_SHARED else v[layer]) for k, v in case.items()}
