@@ -24,6 +24,11 @@ in the 256 MB Infinity Cache between consecutive steps.  A second, cache-cold fi
 16 disjoint slot sets through a 1024-slot (2 GiB) pool with the "stream" policy
 (non-temporal state traffic), the regime of a many-layer model.
 
+Further figures in the same line: `conv_fused` (the same step with the width-4 causal
+conv1d + SiLU fused in front) and `stack48` (48 layers captured as one HIP graph, batch
+128, 1024 slots per layer = 96 GiB of state, slot ids reshuffled before every replay, 256
+replays timed end to end; --no-stack skips it).
+
 CPU baseline: the reference's packed Torch path (index_select gather, unfused GDN,
 index_copy_ write-back; oracle/decode.py) on the host cores at the same shapes, timed for a
 bounded number of steps.
