@@ -80,6 +80,10 @@ constexpr int kMaxConvLen = 8;
 constexpr int kMaxConvTickets = 1 << 20;
 __device__ uint32_t g_conv_ticket[kMaxConvTickets];
 
+// Stream policy: destination of the state of an MTP token that has no slot to go to (past
+// the request's last token, or a padding slot): one tile that is written and never read.
+__device__ __align__(256) f32x4 g_state_sink[kDim * kDim / 4];
+
 __device__ __forceinline__ float load_param(const void* p, int i, bool bf16) {
   return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i])
               : static_cast<const float*>(p)[i];
@@ -237,7 +241,13 @@ __device__ __forceinline__ void chunk_step(f32x4 (&s)[kPieces], const Vectors& x
     s[j0 + 2][e] = fmaf(d1, x.k0[e], s[j0 + 2][e]);
     s[j0 + 3][e] = fmaf(d1, x.k1[e], s[j0 + 3][e]);
   }
-  if (dst_tile != nullptr) {
+  // Stream: unconditional (a token without a destination writes the sink tile), so the
+  // compiler's count of memory operations in flight is exact and later chunks wait for
+  // their own loads only.  Keep: skipped for a null destination; the branch makes the
+  // compiler assume the stores may not have been issued, so chunks 2 and 3 also wait for
+  // the earlier chunks' stores -- measured 1.5% faster when the state is served from the
+  // Infinity Cache, and 2% slower when it streams from HBM.
+  if (Stream || dst_tile != nullptr) {
 #pragma unroll
     for (int j = j0; j < j0 + 4; ++j) {
       f32x4* dst = reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j)));
@@ -477,7 +487,11 @@ void gdn_decode_kernel(const DecodeParams args) {
   } else {
     in0 = load_token(p, bos, q_col, k_col, v_col + wave * kRowsPerWave + (lane & 31), head, kq);
   }
-  const bool stages_mtp = Width > 1 && wave >= 1 && wave < num_tokens;
+  // Every MTP token slot t < W is staged and stepped, past the request's last token too
+  // (with a copy of that token), so the token loops have no branches; such tokens' states
+  // go to the sink tile (stream policy) or are not stored (keep), and their outputs are not
+  // written.
+  const bool stages_mtp = Width > 1 && wave >= 1 && wave < Width;
   const int64_t token_w = bos + min(wave, num_tokens - 1);
   TokenIn inw;
   uint16_t vw_hi = 0;
@@ -594,7 +608,9 @@ void gdn_decode_kernel(const DecodeParams args) {
   char* dst[Width];
 #pragma unroll
   for (int t = 0; t < Width; ++t)
-    dst[t] = slot[t] > 0 ? state_bytes + slot[t] * slot_bytes : nullptr;
+    dst[t] = (t < num_tokens && slot[t] > 0) ? state_bytes + slot[t] * slot_bytes
+             : Stream                         ? reinterpret_cast<char*>(g_state_sink)
+                                              : nullptr;
 
 #define LD_CHUNK(C)                                                                         \
   {                                                                                         \
@@ -602,11 +618,10 @@ void gdn_decode_kernel(const DecodeParams args) {
     chunk_step<C, Stream>(s, load_vectors(s_qk0[wave], kq), s_v0[wave][8 * (C) + rsub],     \
                           s_v0[wave][8 * (C) + 4 + rsub], s_o[0], s_db0[wave][0],           \
                           s_db0[wave][1], kq, r, dst[0], lane_bytes);                       \
-    if ((C) == 0 && Width > 1 && num_tokens > 1) lds_barrier();                             \
+    if ((C) == 0 && Width > 1) lds_barrier();                                               \
     _Pragma("unroll") for (int t = 1; t < Width; ++t) {                                     \
-      if (t < num_tokens)                                                                   \
-        chunk_step<C, Stream>(s, load_vectors(s_qkt[t], kq), s_vt[t][r], s_vt[t][r + 4],    \
-                              s_o[t], s_dbt[t][0], s_dbt[t][1], kq, r, dst[t], lane_bytes); \
+      chunk_step<C, Stream>(s, load_vectors(s_qkt[t], kq), s_vt[t][r], s_vt[t][r + 4],      \
+                            s_o[t], s_dbt[t][0], s_dbt[t][1], kq, r, dst[t], lane_bytes);   \
     }                                                                                       \
   }
   LD_CHUNK(0)

@@ -8,6 +8,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from lightdelta_amd import ops
 from lightdelta_amd.backend import GDNBackend
 from lightdelta_amd.config import BackendConfig
 from lightdelta_amd.workloads import decode_case
@@ -39,11 +40,21 @@ def announce(**what):
     print("case:", " ".join(f"{k}={v}" for k, v in what.items()), flush=True)
 
 
+@pytest.fixture(params=["keep", "stream"])
+def policy(request):
+    """Runs the test under each state cache policy (their store paths differ for tokens
+    without a destination slot)."""
+    saved = ops.state_cache_policy()
+    ops.set_state_cache_policy(request.param)
+    yield request.param
+    ops.set_state_cache_policy(saved)
+
+
 @pytest.mark.parametrize("heads", [(16, 48), (16, 32), (4, 8)])
 @pytest.mark.parametrize("width", [1, 2, 3, 4])
 @pytest.mark.parametrize("state_io", ["indexed", "packed"])
-def test_matches_oracle(gpu, heads, width, state_io):
-    announce(test="matches_oracle", heads=heads, width=width, state_io=state_io)
+def test_matches_oracle(gpu, heads, width, state_io, policy):
+    announce(test="matches_oracle", heads=heads, width=width, state_io=state_io, policy=policy)
     case = decode_case(4, width, num_k_heads=heads[0], num_v_heads=heads[1], pool_slots=4 * width + 2,
                        seed=width, device=gpu)
     case["accepted"][:] = torch.arange(4, device=gpu) % width + 1
@@ -100,10 +111,10 @@ def test_graph_replay_changed_state_indices(gpu, state_io):
 
 
 @pytest.mark.parametrize("state_io", ["packed", "indexed"])
-def test_ragged_verification_and_discarded_slots(gpu, state_io):
+def test_ragged_verification_and_discarded_slots(gpu, state_io, policy):
     """cu=[0,4,7,8,8], an invalid accepted and a discarded candidate slot (reference
     tests/test_gdn.py:105-122)."""
-    announce(test="ragged", state_io=state_io)
+    announce(test="ragged", state_io=state_io, policy=policy)
     case = decode_case(4, 4, pool_slots=18, seed=6, device=gpu)
     case["cu"].copy_(torch.tensor([0, 4, 7, 8, 8], device=gpu, dtype=torch.int32))
     case["accepted"][:] = torch.tensor([0, 3, 1, 2], device=gpu, dtype=torch.int32)
@@ -119,10 +130,10 @@ def test_ragged_verification_and_discarded_slots(gpu, state_io):
     assert case["out"][:4].float().abs().sum() == 0  # invalid accepted -> zero output
 
 
-def test_invalid_and_empty_requests(gpu):
+def test_invalid_and_empty_requests(gpu, policy):
     """Padding sources (0 and -1), accepted out of range, a zero-token request and an empty
     batch: zero outputs, pool untouched where nothing is valid."""
-    announce(test="invalid_and_empty")
+    announce(test="invalid_and_empty", policy=policy)
     case = decode_case(4, 2, pool_slots=12, seed=7, device=gpu)
     case["slots"][0] = torch.tensor([-1, 0], device=gpu, dtype=torch.int32)
     case["accepted"][:] = torch.tensor([1, 3, 2, 1], device=gpu, dtype=torch.int32)
