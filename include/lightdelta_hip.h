@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 3
+#define LD_ABI_VERSION 4
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -175,6 +175,18 @@ int ld_state_scatter(const void* packed, int64_t packed_row_stride_bytes,
 int ld_state_copy(void* pool, int64_t pool_slot_stride_bytes, const int32_t* src_slots,
                   const int32_t* dst_slots, int64_t pairs, int64_t slot_bytes,
                   void* stream);
+
+/*
+ * Zero-fill `count` whole slots of a pool in place:
+ *   if slots[i] > 0: pool[slots[i]] = 0   (all slot_bytes bytes)
+ * Same alignment rules as ld_state_gather (pool base, slot stride and slot_bytes multiples
+ * of 16 bytes).  No counterpart in the reference (there a reused slot is re-initialised
+ * through gather_state's zero fill of rows whose `valid` flag is false,
+ * csrc/state_io.cu:17-25, python/lightdelta/backend.py:41-44); it resets slots of the pool
+ * itself for a new sequence, with the padding convention (slot <= 0 skipped).
+ */
+int ld_state_zero(void* pool, int64_t pool_slot_stride_bytes, const int32_t* slots,
+                  int64_t count, int64_t slot_bytes, void* stream);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
 const char* ld_last_error(void);

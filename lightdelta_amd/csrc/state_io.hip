@@ -3,7 +3,7 @@
 //
 // Semantics follow the reference's copy kernel (csrc/state_io.cu:11-27): a slot <= 0 is
 // padding; gather zero-fills rows whose slot is padding or whose `valid` flag is false,
-// scatter and copy skip padding.  Unlike the reference (one 4-byte element per thread per
+// scatter and copy skip padding.  Zero resets whole slots in place (padding skipped).  Unlike the reference (one 4-byte element per thread per
 // iteration, csrc/state_io.cu:22-26), every thread here moves 128-bit vectors with four
 // loads in flight before the first store, and each workgroup owns one 16 KiB chunk of a row.
 #include "common.h"
@@ -17,14 +17,14 @@ constexpr int64_t kVecsPerChunk = static_cast<int64_t>(kThreads) * kVecsPerThrea
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-enum Mode { kGather = 0, kScatter = 1, kCopy = 2 };
+enum Mode { kGather = 0, kScatter = 1, kCopy = 2, kZero = 3 };
 
 struct CopyParams {
   const char* src;        // gather: pool; scatter: packed; copy: pool
   char* dst;              // gather: out; scatter: pool; copy: pool
   int64_t src_stride;     // bytes between consecutive src rows / slots
   int64_t dst_stride;     // bytes between consecutive dst rows / slots
-  const int32_t* slots;   // gather/scatter: slot per row; copy: source slot per pair
+  const int32_t* slots;   // gather/scatter/zero: slot per row; copy: source slot per pair
   int64_t slot_stride;    // elements between consecutive slots entries (gather/scatter)
   const int32_t* dst_slots;  // copy only
   const uint8_t* valid;   // gather only; NULL = all valid
@@ -54,17 +54,23 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
     if (slot <= 0) return;
     src = reinterpret_cast<const u32x4*>(p.src + row * p.src_stride);
     dst = reinterpret_cast<u32x4*>(p.dst + slot * p.dst_stride);
-  } else {
+  } else if (M == kCopy) {
     const int from = p.slots[row];
     const int to = p.dst_slots[row];
     if (from <= 0 || to <= 0) return;
     src = reinterpret_cast<const u32x4*>(p.src + from * p.src_stride);
     dst = reinterpret_cast<u32x4*>(p.dst + to * p.dst_stride);
+  } else {  // zero fill of a slot (reuse by a new sequence)
+    const int slot = p.slots[row];
+    if (slot <= 0) return;
+    src = nullptr;
+    dst = reinterpret_cast<u32x4*>(p.dst + slot * p.dst_stride);
+    live = false;
   }
 
   const int64_t begin = static_cast<int64_t>(chunk) * kVecsPerChunk;
   const int64_t first = begin + threadIdx.x;
-  if (!live) {  // gather of a padding / invalid row: zero fill
+  if (!live) {  // zero fill: gather of a padding / invalid row, or a slot reset
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i) {
       const int64_t idx = first + i * kThreads;
@@ -100,7 +106,7 @@ int launch(const char* what, int mode, CopyParams p, int64_t rows, int64_t row_b
   if (rows < 0 || row_bytes < 0) return fail(LD_ERR_INVALID_ARGUMENT, "negative size");
   if (rows == 0 || row_bytes == 0) return LD_OK;
   if ((row_bytes & 15) != 0 || (p.src_stride & 15) != 0 || (p.dst_stride & 15) != 0 ||
-      !aligned16(p.src) || !aligned16(p.dst))
+      (mode != kZero && !aligned16(p.src)) || !aligned16(p.dst))
     return fail(LD_ERR_INVALID_ARGUMENT,
                 "state rows, strides and base pointers must be 16-byte aligned");
   p.vecs = row_bytes / 16;
@@ -114,8 +120,10 @@ int launch(const char* what, int mode, CopyParams p, int64_t rows, int64_t row_b
     hipLaunchKernelGGL(slot_copy_kernel<kGather>, grid, dim3(kThreads), 0, s, p);
   else if (mode == kScatter)
     hipLaunchKernelGGL(slot_copy_kernel<kScatter>, grid, dim3(kThreads), 0, s, p);
-  else
+  else if (mode == kCopy)
     hipLaunchKernelGGL(slot_copy_kernel<kCopy>, grid, dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(slot_copy_kernel<kZero>, grid, dim3(kThreads), 0, s, p);
   return check_launch(what);
 }
 
@@ -171,4 +179,16 @@ extern "C" int ld_state_copy(void* pool, int64_t pool_slot_stride_bytes, const i
   p.slots = src_slots;
   p.dst_slots = dst_slots;
   return launch("ld_state_copy", kCopy, p, pairs, slot_bytes, stream);
+}
+
+extern "C" int ld_state_zero(void* pool, int64_t pool_slot_stride_bytes, const int32_t* slots,
+                             int64_t count, int64_t slot_bytes, void* stream) {
+  using namespace ld;
+  if (count > 0 && (!pool || !slots))
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_state_zero: NULL pointer");
+  CopyParams p{};
+  p.dst = static_cast<char*>(pool);
+  p.dst_stride = pool_slot_stride_bytes;
+  p.slots = slots;
+  return launch("ld_state_zero", kZero, p, count, slot_bytes, stream);
 }

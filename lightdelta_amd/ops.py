@@ -10,6 +10,8 @@ Argument validation raises RuntimeError with the reference's messages
 Additive ops (no reference counterpart):
   copy_state(pool, src, dst)            slot -> slot copy inside one pool (MTP commit,
                                         slot reuse), any dtype, padding slot <= 0 skipped
+  zero_slots(pool, slots)               zero whole slots in place (a slot reused by a new
+                                        sequence), any dtype, padding slot <= 0 skipped
   decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, <decode args without qkv>)
                                         causal conv1d (width 4, SiLU, bf16 output) of the
                                         pre-conv activations fused into the decode step;
@@ -40,6 +42,7 @@ SCHEMAS = {
     "gather_state": "gather_state(Tensor pool, Tensor slots, Tensor valid, Tensor(o!) out) -> ()",
     "scatter_state": "scatter_state(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
     "copy_state": "copy_state(Tensor(p!) pool, Tensor src, Tensor dst) -> ()",
+    "zero_slots": "zero_slots(Tensor(p!) pool, Tensor slots) -> ()",
     "decode_conv": (
         "decode_conv(Tensor mixed_qkv, Tensor(c!) conv_state, Tensor conv_weight, "
         "Tensor? conv_bias, Tensor a, Tensor b, Tensor a_log, Tensor dt_bias, Tensor indices, "
@@ -460,6 +463,36 @@ def _copy_state_impl(pool, src, dst):
         )
 
 
+def check_zero(pool, slots):
+    _require(
+        _is_gpu(pool) and pool.dim() >= 1 and _dense_inner(pool),
+        "pool must be a CUDA tensor with dense inner dimensions",
+    )
+    _require(
+        slots.device == pool.device and slots.dtype == torch.int32 and slots.dim() == 1
+        and slots.is_contiguous(),
+        "slots must be a contiguous CUDA int32 vector",
+    )
+
+
+def _zero_slots_impl(pool, slots):
+    check_zero(pool, slots)
+    if slots.numel() == 0:
+        return
+    lib = _lib.load()
+    with _DeviceGuard(pool.device):
+        _lib.check(
+            lib.ld_state_zero(
+                pool.data_ptr(),
+                pool.stride(0) * pool.element_size(),
+                slots.data_ptr(),
+                slots.numel(),
+                _row_bytes(pool),
+                _stream(pool.device),
+            )
+        )
+
+
 # ---------------------------------------------------------------------------------------
 # registration
 # ---------------------------------------------------------------------------------------
@@ -469,6 +502,7 @@ _IMPLS = {
     "gather_state": _gather_state_impl,
     "scatter_state": _scatter_state_impl,
     "copy_state": _copy_state_impl,
+    "zero_slots": _zero_slots_impl,
     "decode_conv": _decode_conv_impl,
     "gather_slots": _gather_slots_impl,
     "scatter_slots": _scatter_slots_impl,

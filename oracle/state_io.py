@@ -4,6 +4,8 @@ Semantics (reference csrc/state_io.cu:16-26; slot <= 0 is padding):
   gather   out[r] = pool[slot_r] if slot_r > 0 and valid[r] else 0
   scatter  pool[slot_r] = packed[r] for slot_r > 0; other rows skipped
   copy     pool[dst_p] = pool[src_p] when src_p > 0 and dst_p > 0 (all reads before writes)
+  zero     pool[slot_i] = 0 for slot_i > 0 (no reference counterpart: the in-place form of
+           gather's zero fill of rows that are not valid, csrc/state_io.cu:17-25)
 Arrays may have any dtype; comparisons against the HIP kernels are bit-exact.
 """
 
@@ -33,4 +35,12 @@ def copy(pool: np.ndarray, src: np.ndarray, dst: np.ndarray) -> np.ndarray:
     for s, d in zip(src, dst):
         if s > 0 and d > 0:
             result[d] = pool[s]
+    return result
+
+
+def zero(pool: np.ndarray, slots: np.ndarray) -> np.ndarray:
+    result = pool.copy()
+    for slot in slots:
+        if slot > 0:
+            result[slot] = 0
     return result

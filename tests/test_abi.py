@@ -23,7 +23,7 @@ def declared_functions() -> set[str]:
 def test_header_declares_the_entry_points():
     assert declared_functions() == {
         "ld_gdn_decode", "ld_gdn_decode_conv", "ld_state_gather", "ld_state_scatter",
-        "ld_state_copy", "ld_last_error", "ld_abi_version",
+        "ld_state_copy", "ld_state_zero", "ld_last_error", "ld_abi_version",
     }
 
 
@@ -73,6 +73,7 @@ def test_empty_work_is_a_no_op():
     args.eps = 1e-6
     assert lib.ld_gdn_decode(ctypes.byref(args), None) == 0
     assert lib.ld_state_copy(None, 0, None, None, 0, 2048, None) == 0
+    assert lib.ld_state_zero(None, 0, None, 0, 2048, None) == 0
     assert lib.ld_state_gather(None, 0, None, 1, None, None, 0, 2048, 0, None) == 0
 
 
@@ -102,4 +103,6 @@ def test_decode_conv_rejects_multi_token_and_bad_conv_shapes():
 def test_copy_rejects_misaligned_rows():
     lib = _lib.load()
     code = lib.ld_state_gather(16, 24, 32, 1, None, 48, 24, 24, 1, None)
+    assert code == 1 and "16-byte aligned" in lib.ld_last_error().decode()
+    code = lib.ld_state_zero(16, 2048, 32, 1, 24, None)
     assert code == 1 and "16-byte aligned" in lib.ld_last_error().decode()

@@ -109,3 +109,10 @@ def test_state_io_oracle_against_brute_force():
     copied = state_io.copy(pool, src, dst)
     assert np.array_equal(copied[2], pool[1]) and np.array_equal(copied[3], pool[2])
     assert np.array_equal(copied[[0, 1, 4, 5, 6]], pool[[0, 1, 4, 5, 6]])
+    zeroed = state_io.zero(pool, np.array([6, -1, 0, 2]))
+    assert not zeroed[[2, 6]].any()
+    assert np.array_equal(zeroed[[0, 1, 3, 4, 5]], pool[[0, 1, 3, 4, 5]])
+    # zeroing through gather with valid = False and scatter back is the same reset
+    via_gather = state_io.scatter(state_io.gather(pool, np.array([6, 2]), np.array([0, 0], bool)),
+                                  np.array([6, 2]), pool)
+    assert np.array_equal(via_gather, zeroed)

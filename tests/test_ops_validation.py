@@ -104,6 +104,11 @@ def test_state_io_validation_messages(meta):
         ops.check_state_layout(conv, slots, torch.empty(3, 4, 8192, device=meta), fp32_4d=False)
     with pytest.raises(RuntimeError, match="same length"):
         ops.check_copy(pool, slots, slots[:2])
+    ops.check_zero(conv, slots)
+    with pytest.raises(RuntimeError, match="slots must be a contiguous CUDA int32 vector"):
+        ops.check_zero(pool, slots.long())
+    with pytest.raises(RuntimeError, match="dense inner dimensions"):
+        ops.check_zero(torch.empty(8, 4, 128, 256, device=meta)[..., :128], slots)
 
 
 def test_cpu_tensors_are_rejected():

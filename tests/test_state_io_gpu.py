@@ -70,6 +70,11 @@ def test_gather_scatter_copy_match_numpy(gpu, dtype):
     dst = torch.tensor([2, 3, -1, 9, 10, 21], dtype=torch.int32)
     torch.ops.lightdelta.copy_state(pool, src.to(gpu), dst.to(gpu))
     assert np.array_equal(row_bytes(pool), oracle.copy(expected, src.numpy(), dst.numpy()))
+    copied = oracle.copy(expected, src.numpy(), dst.numpy())
+
+    reset = torch.tensor([4, -1, 0, 38, 11], dtype=torch.int32)
+    torch.ops.lightdelta.zero_slots(pool, reset.to(gpu))
+    assert np.array_equal(row_bytes(pool), oracle.zero(copied, reset.numpy()))
 
 
 def test_gather_into_strided_rows(gpu):
@@ -90,7 +95,8 @@ def test_gather_into_strided_rows(gpu):
 def test_workload_pool_copies(gpu):
     """1024-slot fp32 pool (32 x 128 x 128 per slot, 2 GiB) and bf16 conv pool (4 x 8192 per
     slot): gather 128 slots, scatter them back to other slots, slot-to-slot copy of 128
-    random pairs including padding -1 -- each bit-exact against the pool itself."""
+    random pairs including padding -1, reset of 128 slots -- each bit-exact against the
+    pool itself."""
     announce(test="workload_pool_copies")
     gen = torch.Generator(device="cpu").manual_seed(0)
     for shape, dtype in (((32, 128, 128), torch.float32), ((4, 8192), torch.bfloat16)):
@@ -119,5 +125,15 @@ def test_workload_pool_copies(gpu):
         untouched = torch.ones(1024, dtype=torch.bool, device=gpu)
         untouched[d] = False
         assert torch.equal(pool[untouched], before[untouched])
-        del pool, before, packed
+        # reset 128 slots for reuse (with padding ids), the rest untouched
+        reset = (torch.randperm(1023, generator=gen)[:128] + 1).to(torch.int32)
+        reset[3::29] = -1
+        after_copy = pool.clone()
+        torch.ops.lightdelta.zero_slots(pool, reset.to(gpu))
+        torch.cuda.synchronize()
+        cleared = torch.zeros(1024, dtype=torch.bool, device=gpu)
+        cleared[reset[reset > 0].long().to(gpu)] = True
+        assert pool[cleared].count_nonzero() == 0
+        assert torch.equal(pool[~cleared], after_copy[~cleared])
+        del pool, before, packed, after_copy
         torch.cuda.empty_cache()
