@@ -127,15 +127,20 @@ typedef struct ld_conv_args {
 } ld_conv_args;
 
 /*
- * Conv-fused single-token decode step (args->width must be 1; args->qkv is not read).  Per
- * request, the causal depthwise conv1d of the new token over the last 3 conv-state columns,
- * plus bias and SiLU, is rounded to bf16 and becomes the step's q/k/v; the conv state of the
- * slot shifts left by one column and takes the new input; then the GDN step of
- * ld_gdn_decode runs.  Invalid requests (padding source, bad `accepted`, no tokens) leave
- * both pools untouched.  Launches that touch the same slots must be stream-ordered (they
- * share one ticket per (slot, k-head) in library-owned device memory; at most 2^20).
+ * Conv-fused decode / speculative-verify step (args->qkv is not read; `conv->x` holds the
+ * pre-conv activations).  Per request with n tokens, the causal depthwise conv1d (width 4,
+ * plus bias, SiLU, rounded to bf16) runs over the 3 conv-state columns from accepted - 1
+ * followed by the n new inputs, and its outputs become the tokens' q/k/v; the conv state of
+ * slot indices[r, 0] becomes its columns accepted .. accepted + state_len - n - 1 followed by
+ * the n inputs (vLLM's causal_conv1d_update with num_accepted_tokens; n = 1, accepted = 1
+ * is the plain one-column shift); then the GDN step of ld_gdn_decode runs.  Requests that
+ * are invalid for the GDN step, or whose conv columns would fall outside the state
+ * (accepted - 1 + 2 > state_len - 1, or accepted > n < state_len), or whose conv slot
+ * indices[r, 0] is padding, get zero outputs and leave both pools untouched.  Launches that
+ * touch the same slots must be stream-ordered (they share one ticket per (slot, k-head) in
+ * library-owned device memory; at most 2^20).
  * No counterpart in the reference, whose conv is vLLM's causal_conv1d_update run before
- * lightdelta::decode (python/lightdelta/integration/vllm_layer.py:199-220).
+ * lightdelta::decode (python/lightdelta/integration/vllm_layer.py:150-172, 199-220).
  */
 int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_args* conv, void* stream);
 

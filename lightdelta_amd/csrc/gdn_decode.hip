@@ -179,6 +179,21 @@ __device__ __forceinline__ TokenIn load_token(const DecodeParams& p, int64_t tok
   return in;
 }
 
+// The q/k part of a token in the lane layout of load_token, from conv outputs in LDS
+// (256 bf16 q/k channels of the k-head, then the v channels).
+__device__ __forceinline__ TokenIn conv_token(const uint16_t* conv, int kq) {
+  const uint32_t* c32 = reinterpret_cast<const uint32_t*>(conv);
+  TokenIn in;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    in.q[2 * e] = c32[e * 32 + 2 * kq];
+    in.q[2 * e + 1] = c32[e * 32 + 2 * kq + 1];
+    in.k[2 * e] = c32[64 + e * 32 + 2 * kq];
+    in.k[2 * e + 1] = c32[64 + e * 32 + 2 * kq + 1];
+  }
+  return in;
+}
+
 // A token's q^ / k^ pieces of this lane (q^ scaled by `scale`), decay and beta.
 struct Staged {
   f32x4 q0, q1, k0, k1;
@@ -306,26 +321,82 @@ __device__ __forceinline__ uint16_t silu_bf16(float x) {
 //   bf16(silu(bias + sum_j w[j] * [state[len-3], state[len-2], state[len-1], x][j]))
 // with the fp32 accumulation running from the oldest tap to the newest (one rounding per
 // fused multiply-add) and the SiLU correctly rounded to bf16.
-template <int N>
-__device__ __forceinline__ uint16_t conv_output(uint16_t x, const uint16_t (&state)[N],
-                                                const uint32_t (&w)[2], uint16_t bias,
-                                                bool has_bias, int len) {
-  uint16_t tap[3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    // state[len - 3 + i], selected without dynamic register indexing
-    uint16_t v = state[0];
-#pragma unroll
-    for (int j = 1; j < N; ++j)
-      if (j == len - 3 + i) v = state[j];
-    tap[i] = v;
-  }
+// bf16(silu(bias + w0*t0 + w1*t1 + w2*t2 + w3*t3)): one causal conv output from its four
+// taps, oldest first, with the fp32 accumulation running from the oldest tap to the newest
+// (one rounding per fused multiply-add) and the SiLU correctly rounded to bf16.
+__device__ __forceinline__ uint16_t conv_dot(uint16_t t0, uint16_t t1, uint16_t t2, uint16_t t3,
+                                             const uint32_t (&w)[2], uint16_t bias, bool has_bias) {
   float acc = has_bias ? bf16_to_f32(bias) : 0.0f;
-  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[0])), bf16_to_f32(tap[0]), acc);
-  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[0] >> 16)), bf16_to_f32(tap[1]), acc);
-  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[1])), bf16_to_f32(tap[2]), acc);
-  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[1] >> 16)), bf16_to_f32(x), acc);
+  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[0])), bf16_to_f32(t0), acc);
+  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[0] >> 16)), bf16_to_f32(t1), acc);
+  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[1])), bf16_to_f32(t2), acc);
+  acc = fmaf(bf16_to_f32(static_cast<uint16_t>(w[1] >> 16)), bf16_to_f32(t3), acc);
   return silu_bf16(acc);
+}
+
+// Up to 8 bf16 values of one conv channel packed in two 64-bit registers.  Element i is
+// selected with a shift, for a runtime i too: a select chain over an array lets the compiler
+// turn it into a dynamically indexed array, which it then places in scratch or LDS memory.
+struct Packed8 {
+  uint64_t lo = 0, hi = 0;
+  __device__ __forceinline__ void set(int i, uint32_t v) {  // v < 2^16, i compile-time
+    if (i < 4)
+      lo |= static_cast<uint64_t>(v) << (16 * i);
+    else
+      hi |= static_cast<uint64_t>(v) << (16 * (i - 4));
+  }
+  __device__ __forceinline__ uint16_t get(int i) const {  // 0 <= i < 8
+    return static_cast<uint16_t>((i < 4 ? lo : hi) >> (16 * (i & 3)));
+  }
+};
+
+// One decode-token output of the causal depthwise conv (width 4) plus SiLU, rounded to bf16,
+// with the history in the first 3 state columns (vLLM's causal_conv1d_update without
+// speculative tokens reads columns 0..2 whatever the state's length):
+//   bf16(silu(bias + sum_j w[j] * [state[0], state[1], state[2], x][j]))
+__device__ __forceinline__ uint16_t conv_output(uint16_t x, const uint16_t (&state)[4],
+                                                const uint32_t (&w)[2], uint16_t bias,
+                                                bool has_bias) {
+  return conv_dot(state[0], state[1], state[2], x, w, bias, has_bias);
+}
+
+// The conv of one channel over the Width tokens of a speculative-decoding step (vLLM's
+// causal_conv1d_update with num_accepted_tokens): the history is the 3 state columns from
+// `offset` (= accepted - 1), token t's window is the 4 inputs of history ++ x ending at x_t,
+// and the new state is state[offset + 1 .. offset + len - n] followed by x_0 .. x_{n-1}
+// (n = the request's tokens, len = the state's columns).  Outputs go to out[t * 3 * kDim],
+// t < Width (tokens past n use copies of the last input and are discarded by the caller);
+// new_state[k] holds column min(k, len - 1).  Reads nothing out of bounds: every column is
+// clamped to len - 1 and every token to n - 1 when loaded.
+template <int Width, int Cols>
+__device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64_t bos, int n,
+                                                    int offset, int64_t state_at, int channel,
+                                                    bool has_bias, uint16_t* out,
+                                                    uint16_t (&new_state)[Cols]) {
+  static_assert(Cols <= 8 && Width <= 4, "packed conv registers hold 8 columns, 4 tokens");
+  Packed8 st, x;
+#pragma unroll
+  for (int j = 0; j < Cols; ++j)
+    st.set(j, p.conv_state[state_at + min(j, p.conv_len - 1) * p.conv_len_stride]);
+#pragma unroll
+  for (int t = 0; t < Width; ++t) x.set(t, p.conv_x[(bos + min(t, n - 1)) * p.conv_x_row + channel]);
+  const uint32_t* wsrc = reinterpret_cast<const uint32_t*>(p.conv_weight + channel * kConvWidth);
+  const uint32_t w[2] = {wsrc[0], wsrc[1]};
+  const uint16_t bias = (p.conv_bias != nullptr ? p.conv_bias : p.conv_weight)[channel];
+  uint16_t seq[3 + Width];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) seq[m] = st.get(offset + m);
+#pragma unroll
+  for (int t = 0; t < Width; ++t) seq[3 + t] = x.get(t);
+#pragma unroll
+  for (int t = 0; t < Width; ++t)
+    out[t * 3 * kDim] = conv_dot(seq[t], seq[t + 1], seq[t + 2], seq[t + 3], w, bias, has_bias);
+  const int kept = p.conv_len - n;  // state columns that survive (<= 0: none)
+#pragma unroll
+  for (int k = 0; k < Cols; ++k) {
+    const int col = min(k, p.conv_len - 1);
+    new_state[k] = col < kept ? st.get(offset + 1 + col) : x.get(col - kept);
+  }
 }
 
 // Waits for this wave's LDS traffic, then joins the workgroup barrier.  Global loads that
@@ -340,11 +411,12 @@ __device__ __forceinline__ void lds_barrier() {
 // width W (tokens per request at most); fixing it at compile time unrolls every token loop
 // into straight-line code, which keeps the tile's per-piece load waits exact.
 //
-// Conv: the causal depthwise conv1d (width 4, SiLU) runs first on the pre-conv activations
-// (single-token decode only).  Each workgroup convolves the 256 q/k channels of its k-head
-// and the 128 v channels of its head from the conv state of the request's slot, rounds the
-// outputs to bf16 (the dtype an unfused conv writes) and feeds them to the GDN step.  Its
-// own v channels' conv state is shifted in place.  The q/k channels are shared by the
+// Conv: the causal depthwise conv1d (width 4, SiLU) runs first on the pre-conv activations.
+// Each workgroup convolves the 256 q/k channels of its k-head and the 128 v channels of its
+// head from the conv state of the request's slot, rounds the outputs to bf16 (the dtype an
+// unfused conv writes) and feeds them to the GDN step; one token (W = 1) while the tile
+// streams in, several (speculative verify, W > 1) before the tile loads.  Its own v
+// channels' conv state is updated in place.  The q/k channels are shared by the
 // HV/H workgroups of a k-head group, so their shifted state is written only after all of
 // them have read it: every workgroup counts itself in (relaxed atomic add on
 // g_conv_ticket[slot*H + kh], returning the previous count) after its reads; the one that
@@ -357,7 +429,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
 void gdn_decode_kernel(const DecodeParams args) {
   constexpr bool Conv = ConvCols > 0;
   constexpr int kCols = Conv ? ConvCols : 1;
-  static_assert(!Conv || Width == 1, "the conv-fused step is single-token");
+  // The conv runs before the tile loads for several tokens or more than 4 state columns;
+  // one token with 3..4 columns keeps it in registers while the tile streams in.
+  constexpr bool kConvFirst = Conv && (Width > 1 || kCols > 4);
+  constexpr bool kConvLate = Conv && !kConvFirst;
+  static_assert(!kConvLate || kCols == 4, "the in-flight conv holds 4 state columns");
   // Every kernel argument, then all request metadata, is loaded before the first branch:
   // two dependent scalar round trips (kernel-argument segment; cu/accepted/indices) instead
   // of the compiler's default of sinking each load to its first use behind the early exits.
@@ -409,7 +485,13 @@ void gdn_decode_kernel(const DecodeParams args) {
 #pragma unroll
   for (int t = 0; t < Width; ++t)
     if (accepted == t + 1) source = slot[t];
-  if (source <= 0 || num_tokens > Width) {
+  // Conv variant: the conv state lives in slot indices[r, 0]; the history of token 0 is its
+  // 3 columns from accepted - 1, and the columns kept for the next step must lie in the
+  // state too (true whenever the state has 3 + W - 1 columns and accepted <= tokens).
+  const int conv_offset = accepted - 1;
+  const bool conv_ok = !Conv || (slot[0] > 0 && conv_offset + kConvWidth - 2 <= p.conv_len - 1 &&
+                                 (p.conv_len <= num_tokens || conv_offset <= num_tokens - 1));
+  if (source <= 0 || num_tokens > Width || !conv_ok) {
     // Invalid request: zero outputs, state untouched.
     for (int i = tid; i < num_tokens * kDim; i += kThreads) {
       const int64_t token = bos + (i >> 7);
@@ -429,9 +511,9 @@ void gdn_decode_kernel(const DecodeParams args) {
   __shared__ float s_vt[Width][kDim];
   __shared__ float s_dbt[Width][2];
   __shared__ float s_o[Width][kDim];
-  // Conv variant: bf16 conv outputs of the 256 q/k channels and 128 v channels, and the
-  // shifted q/k conv state kept for the end-of-kernel write.
-  __shared__ uint16_t s_conv[Conv ? 3 * kDim : 2];
+  // Conv variant: bf16 conv outputs of the 256 q/k channels and 128 v channels per token,
+  // and the shifted q/k conv state kept for the end-of-kernel write.
+  __shared__ uint16_t s_conv[Conv ? Width : 1][Conv ? 3 * kDim : 2];
   __shared__ uint16_t s_conv_new[Conv ? 2 * kDim : 1][kCols];
   __shared__ uint32_t s_arrived;
 
@@ -452,23 +534,48 @@ void gdn_decode_kernel(const DecodeParams args) {
   // conv_len, so every load is in bounds), weights and bias.
   const int conv_qk = tid < kDim ? q_col + tid : k_col + (tid - kDim);
   const int conv_v = v_col + (tid & (kDim - 1));
-  int64_t cs_qk_at = 0, cs_v_at = 0;
+  const int64_t conv_slot_at = static_cast<int64_t>(slot[0]) * p.conv_slot;
+  int64_t cs_qk_at = conv_slot_at + conv_qk * p.conv_dim_stride;
+  int64_t cs_v_at = conv_slot_at + conv_v * p.conv_dim_stride;
   uint16_t cx_qk = 0, cx_v = 0, cb_qk = 0, cb_v = 0;
-  uint16_t cs_qk[kCols], cs_v[kCols];
+  uint16_t cs_qk_raw[kConvLate ? 4 : 1], cs_v_raw[kConvLate ? 4 : 1];
   uint32_t cw_qk[2], cw_v[2];
   uint32_t arrived = 0;  // ticket count before this workgroup's increment (thread 0)
-  if constexpr (Conv) {
+  if constexpr (kConvFirst) {
+    // Several tokens (speculative verify), or a long conv state: the conv runs to
+    // completion before the tile loads, so its inputs do not compete with the tile for
+    // registers.  The v channels are
+    // this workgroup's alone and are shifted in place (threads 128..255 repeat the stores
+    // of 0..127 with identical bytes); the q/k channels are kept for the end-of-kernel write.
+    uint16_t qk_new[kCols], v_new[kCols];
+    const bool has_bias = p.conv_bias != nullptr;
+    conv_channel_tokens<Width, kCols>(p, bos, num_tokens, conv_offset, cs_qk_at, conv_qk, has_bias,
+                                      &s_conv[0][tid], qk_new);
+    conv_channel_tokens<Width, kCols>(p, bos, num_tokens, conv_offset, cs_v_at, conv_v, has_bias,
+                                      &s_conv[0][2 * kDim + (tid & (kDim - 1))], v_new);
+#pragma unroll
+    for (int k = 0; k < kCols; ++k) s_conv_new[tid][k] = qk_new[k];
+    // Every wave has consumed its conv-state reads once past the barrier, so the v channels
+    // (read by two threads each) can be overwritten.
+    lds_barrier();
+#pragma unroll
+    for (int k = 0; k < kCols; ++k)
+      p.conv_state[cs_v_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new[k];
+    if (p.group > 1 && tid == 0)
+      arrived = __hip_atomic_fetch_add(
+          &g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head], 1u,
+          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    in0.a = p.a[static_cast<int64_t>(bos) * p.a_row + head];
+    in0.b = p.b[static_cast<int64_t>(bos) * p.b_row + head];
+  } else if constexpr (kConvLate) {
     const uint16_t* xrow = p.conv_x + static_cast<int64_t>(bos) * p.conv_x_row;
     cx_qk = xrow[conv_qk];
     cx_v = xrow[conv_v];
-    const int64_t slot_at = static_cast<int64_t>(slot[0]) * p.conv_slot;
-    cs_qk_at = slot_at + conv_qk * p.conv_dim_stride;
-    cs_v_at = slot_at + conv_v * p.conv_dim_stride;
 #pragma unroll
     for (int j = 0; j < kCols; ++j) {
       const int64_t col = min(j, p.conv_len - 1) * p.conv_len_stride;
-      cs_qk[j] = p.conv_state[cs_qk_at + col];
-      cs_v[j] = p.conv_state[cs_v_at + col];
+      cs_qk_raw[j] = p.conv_state[cs_qk_at + col];
+      cs_v_raw[j] = p.conv_state[cs_v_at + col];
     }
     const uint32_t* wq = reinterpret_cast<const uint32_t*>(p.conv_weight + conv_qk * kConvWidth);
     const uint32_t* wv = reinterpret_cast<const uint32_t*>(p.conv_weight + conv_v * kConvWidth);
@@ -495,7 +602,14 @@ void gdn_decode_kernel(const DecodeParams args) {
   const int64_t token_w = bos + min(wave, num_tokens - 1);
   TokenIn inw;
   uint16_t vw_hi = 0;
-  if (Width > 1) {
+  if constexpr (Conv && Width > 1) {  // post-conv token from LDS (ready: barrier above)
+    const uint16_t* conv_w = s_conv[min(wave, num_tokens - 1)];
+    inw = conv_token(conv_w, kq);
+    inw.v = conv_w[2 * kDim + 2 * lane];
+    vw_hi = conv_w[2 * kDim + 2 * lane + 1];
+    inw.a = p.a[token_w * p.a_row + head];
+    inw.b = p.b[token_w * p.b_row + head];
+  } else if (Width > 1) {
     inw = load_token(p, token_w, q_col, k_col, v_col + 2 * lane, head, kq);
     vw_hi = p.qkv[token_w * p.qkv_row + v_col + 2 * lane + 1];
   }
@@ -529,25 +643,28 @@ void gdn_decode_kernel(const DecodeParams args) {
   }
 
   // ---- staging, while the tile streams in ----
-  if constexpr (Conv) {
+  if constexpr (kConvLate) {
     const int len = p.conv_len;
     const bool has_bias = p.conv_bias != nullptr;
-    s_conv[tid] = conv_output(cx_qk, cs_qk, cw_qk, cb_qk, has_bias, len);
-    if (tid < kDim) s_conv[2 * kDim + tid] = conv_output(cx_v, cs_v, cw_v, cb_v, has_bias, len);
-    // Shifted state: columns 1..len-1, then the new input.  The v channels (this
-    // workgroup's alone) are shifted in place now; threads 128..255 repeat the stores of
-    // threads 0..127 with identical bytes, and columns past len-1 repeat column len-1, so
-    // the stores need no branch (a store under a branch makes later load waits conservative).
-    // The q/k channels are kept for the end-of-kernel write.
+    s_conv[0][tid] = conv_output(cx_qk, cs_qk_raw, cw_qk, cb_qk, has_bias);
+    if (tid < kDim) s_conv[0][2 * kDim + tid] = conv_output(cx_v, cs_v_raw, cw_v, cb_v, has_bias);
+    // Shifted state: columns 1..len-1, then the new input.  The q/k channels are kept for
+    // the end-of-kernel write.
+    uint16_t v_new[kCols];
 #pragma unroll
     for (int j = 0; j < kCols; ++j) {
-      const uint16_t qk_new = j + 1 < len ? cs_qk[j + 1 < kCols ? j + 1 : j] : cx_qk;
-      const uint16_t v_new = j + 1 < len ? cs_v[j + 1 < kCols ? j + 1 : j] : cx_v;
-      p.conv_state[cs_v_at + min(j, len - 1) * p.conv_len_stride] = v_new;
-      s_conv_new[tid][j] = qk_new;
+      s_conv_new[tid][j] = j + 1 < len ? cs_qk_raw[j + 1 < kCols ? j + 1 : j] : cx_qk;
+      v_new[j] = j + 1 < len ? cs_v_raw[j + 1 < kCols ? j + 1 : j] : cx_v;
     }
-    // Conv outputs visible to every wave; every q/k conv-state read of this workgroup done.
+    // Conv outputs visible to every wave; every conv-state read of this workgroup consumed.
     lds_barrier();
+    // The v channels (this workgroup's alone) are shifted in place; threads 128..255 repeat
+    // the stores of threads 0..127 with identical bytes (both read the channel before the
+    // barrier), and columns past len-1 repeat column len-1, so the stores need no branch (a
+    // store under a branch makes later load waits conservative).
+#pragma unroll
+    for (int j = 0; j < kCols; ++j)
+      p.conv_state[cs_v_at + min(j, len - 1) * p.conv_len_stride] = v_new[j];
     // Relaxed: every conv-state value this workgroup read has already been consumed (the
     // barrier above follows the conv arithmetic), so the increment cannot overtake a read.
     // The returned count is first used at the kernel's end, by which time it has long
@@ -556,15 +673,15 @@ void gdn_decode_kernel(const DecodeParams args) {
       arrived = __hip_atomic_fetch_add(
           &g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head], 1u,
           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t* c32 = reinterpret_cast<const uint32_t*>(s_conv);
+  }
+  if constexpr (Conv) {  // token 0 after the conv, from LDS
+    const TokenIn c = conv_token(s_conv[0], kq);
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      in0.q[2 * e] = c32[e * 32 + 2 * kq];
-      in0.q[2 * e + 1] = c32[e * 32 + 2 * kq + 1];
-      in0.k[2 * e] = c32[64 + e * 32 + 2 * kq];
-      in0.k[2 * e + 1] = c32[64 + e * 32 + 2 * kq + 1];
+    for (int e = 0; e < 4; ++e) {
+      in0.q[e] = c.q[e];
+      in0.k[e] = c.k[e];
     }
-    in0.v = s_conv[2 * kDim + wave * kRowsPerWave + (lane & 31)];
+    in0.v = s_conv[0][2 * kDim + wave * kRowsPerWave + (lane & 31)];
   }
   {
     const Staged x = stage_token(in0, a_log, dt_bias, p.scale);
@@ -686,11 +803,18 @@ void launch_decode(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t bl
 template <bool Stream>
 void launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
                    uint32_t blocks, hipStream_t stream) {
-  if (conv) {  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
-    if (p.conv_len <= 4)
-      launch_decode<Stream, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
-    else
-      launch_decode<Stream, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
+  if (conv) {
+    switch (p.width) {
+      case 1:  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
+        if (p.conv_len <= 4)
+          launch_decode<Stream, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
+        else
+          launch_decode<Stream, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
+        break;
+      case 2: launch_decode<Stream, 2, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
+      case 3: launch_decode<Stream, 3, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
+      default: launch_decode<Stream, 4, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
+    }
     return;
   }
   switch (p.width) {
@@ -784,8 +908,6 @@ extern "C" int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_
   using namespace ld;
   if (args == nullptr || conv == nullptr)
     return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_decode_conv: args or conv is NULL");
-  if (args->width != 1)
-    return fail(LD_ERR_INVALID_ARGUMENT, "the conv-fused step supports 1 token per request");
   if (conv->width != kConvWidth) return fail(LD_ERR_INVALID_ARGUMENT, "conv width must be 4");
   if (conv->state_len < kConvWidth - 1 || conv->state_len > kMaxConvLen)
     return fail(LD_ERR_INVALID_ARGUMENT, "conv state length must be 3 through 8");

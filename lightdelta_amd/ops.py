@@ -16,8 +16,9 @@ Additive ops (no reference counterpart):
                                         causal conv1d (width 4, SiLU, bf16 output) of the
                                         pre-conv activations fused into the decode step;
                                         conv_state [slots, conv_dim, state_len] (any strides,
-                                        so vLLM's transposed dim-last view works), one token
-                                        per request
+                                        so vLLM's transposed dim-last view works); 1 to 4
+                                        tokens per request, speculative verify with vLLM's
+                                        num_accepted_tokens semantics (accepted)
   gather_slots / scatter_slots          dtype-generic gather_state / scatter_state, for the
                                         bf16 conv-state pool and any dense-inner pool
 
@@ -250,7 +251,6 @@ def check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log
     h, hv = check_decode(mixed_qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate,
                          weight, out, eps)
     conv_dim = mixed_qkv.shape[1]
-    _require(indices.shape[1] == 1, "the conv-fused step supports 1 token per request")
     _require(
         conv_state.device == mixed_qkv.device
         and conv_state.dtype == torch.bfloat16
@@ -282,12 +282,12 @@ def _decode_conv_impl(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log
                       indices, cu, accepted, state, gate, weight, out, eps):
     h, hv = check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log,
                               dt_bias, indices, cu, accepted, state, gate, weight, out, eps)
-    requests = indices.shape[0]
+    requests, width = indices.shape
     args = _lib.DecodeArgs(
         0, 0, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), a_log.data_ptr(),
         dt_bias.data_ptr(), _dtype_code(dt_bias), _dtype_code(weight), indices.data_ptr(),
         cu.data_ptr(), accepted.data_ptr(), state.data_ptr(), state.stride(0),
-        gate.data_ptr(), gate.stride(0), weight.data_ptr(), out.data_ptr(), requests, 1, h,
+        gate.data_ptr(), gate.stride(0), weight.data_ptr(), out.data_ptr(), requests, width, h,
         hv, QK_SCALE, eps, _cache_policy,
     )
     conv = _lib.ConvArgs(

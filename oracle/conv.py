@@ -1,14 +1,24 @@
-"""Causal depthwise conv1d update of one decode token -- test infrastructure.
+"""Causal depthwise conv1d update of decode tokens -- test infrastructure.
 
-The pre-GDN step of the decode layer (vLLM 0.29 `causal_conv1d_update`, called at the
-reference's python/lightdelta/integration/vllm_layer.py:199-207; vLLM is a third-party
-dependency absent here, so this restates its published algorithm for the single-token
-decode case):
+The pre-GDN step of the decode layer: vLLM 0.29 `causal_conv1d_update`, called at the
+reference's python/lightdelta/integration/vllm_layer.py:199-207 (one token per request)
+and :161-172 (MTP verify: `num_accepted_tokens`, `query_start_loc`).  vLLM is a third-party
+dependency absent here, so this restates its published algorithm.  Per request with L new
+tokens x_0 .. x_{L-1}, conv state of S columns and offset a = num_accepted_tokens - 1
+(0 without speculative decoding), per channel d:
 
-  window[d] = [state[d, L-W+1 .. L-1], x[d]]            (the last W-1 state columns, x)
-  acc[d]    = bias[d]; acc[d] = fma(weight[d, j], window[d, j], acc[d]) for j = 0 .. W-1
-  y[d]      = bf16( silu(acc[d]) )                      (fp32 accumulation, oldest tap first)
-  state[d]  = [state[d, 1 .. L-1], x[d]]                (shift left by one, append x)
+  history   h = state[d, a .. a+W-2]                    (the W-1 inputs before x_0)
+  sequence  q = h ++ [x_0, .., x_{L-1}]
+  acc_t     = bias[d]; acc_t = fma(weight[d, j], q[t + j], acc_t) for j = 0 .. W-1
+  y_t[d]    = bf16( silu(acc_t) )                       (fp32 accumulation, oldest tap first)
+  new state = [state[d, a+1 .. a+S-L], x_0, .., x_{L-1}] (S columns: the state after the
+                                                         first token of the step, then the
+                                                         step's inputs)
+
+With L = 1 and a = 0 this is the plain shift: state[d, 1 .. S-1] then x_0, with the history
+in columns 0 .. W-2 whatever S is (vLLM's non-speculative update; S = W-1 there).  The next
+step's offset selects, among the S columns, the W-1 inputs that end at its last accepted
+token.
 
 The fp32 fused multiply-add chain is emulated exactly in float64 (a product of two fp32
 values is exact in float64 and the single rounding back to fp32 is that of an fma).  The
@@ -17,11 +27,12 @@ exact value's rounding.  Any fp32 SiLU rounds to the same bf16 except within a f
 ulps of a bf16 rounding midpoint, where implementations legitimately differ; fixing the
 exact rounding makes the conv output a deterministic function of its inputs.
 
-State layout `[D, L]` per slot (dim-first); a dim-last pool is passed transposed.
+State layout `[D, S]` per slot (dim-first); a dim-last pool is passed transposed.
 
 Parity of this function is pinned only definitionally (it is checked against
-torch.nn.functional.conv1d with groups = D and against an element loop); no reference test
-or fixture covers the conv, so conv parity is "unpinned" in the reference's sense.
+torch.nn.functional.conv1d with groups = D, against an element loop, and the multi-token
+form against repeated single-token updates); no reference test or fixture covers the conv,
+so conv parity is "unpinned" in the reference's sense.
 """
 
 from __future__ import annotations
@@ -45,8 +56,10 @@ def round_to_bf16(y: np.ndarray) -> torch.Tensor:
 
 
 def conv_update(x: torch.Tensor, state: torch.Tensor, weight: torch.Tensor, bias=None):
-    """x [B, D] (bf16); state [B, D, L]; weight [D, W]; bias [D] or None.
-    Returns (y [B, D] bf16, new_state [B, D, L] in state's dtype)."""
+    """The single-token primitive on an explicit window: x [B, D] (bf16); state [B, D, L]
+    whose last W-1 columns are the inputs before x; weight [D, W]; bias [D] or None.
+    Returns (y [B, D] bf16, new_state [B, D, L]: shifted left by one, x appended).
+    conv_update_tokens applies it to the history columns vLLM selects."""
     width = weight.shape[1]
     window = torch.cat([state[..., state.shape[-1] - (width - 1):], x[..., None]], -1).float()
     acc = torch.zeros(window.shape[:-1], dtype=torch.float32)
@@ -68,3 +81,25 @@ def conv_update_reference_form(x, state, weight, bias=None):
     out = F.conv1d(window, weight.float()[:, None, :], bias=None if bias is None else bias.float(),
                    groups=weight.shape[0])
     return F.silu(out[..., 0]).to(x.dtype)
+
+
+def conv_update_tokens(x: torch.Tensor, state: torch.Tensor, weight: torch.Tensor, bias=None,
+                       offset: int = 0):
+    """One request's step: x [L, D] (bf16) new tokens, state [D, S] its conv state, offset
+    = num_accepted_tokens - 1.  Returns (y [L, D] bf16, new_state [D, S]).  Requires
+    offset + W - 2 <= S - 1 and, when S > L, offset + S - L <= S - 1."""
+    width = weight.shape[1]
+    length = x.shape[0]
+    cols = state.shape[-1]
+    assert offset + width - 2 <= cols - 1
+    assert cols <= length or offset + cols - length <= cols - 1
+    history = state[:, offset:offset + width - 1]
+    seq = torch.cat([history, x.t().to(state.dtype)], -1)  # [D, W-1+L]
+    ys = []
+    for t in range(length):
+        window = seq[:, t:t + width]  # [D, W]: W-1 inputs before token t, then token t
+        y, _ = conv_update(window[:, -1][None].to(x.dtype), window[None, :, :-1], weight, bias)
+        ys.append(y[0])
+    kept = state[:, offset + 1:offset + 1 + max(cols - length, 0)]
+    new_state = torch.cat([kept, x.t().to(state.dtype)], -1)[:, -cols:]
+    return torch.stack(ys), new_state

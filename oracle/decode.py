@@ -127,25 +127,38 @@ def packed_reference_step(qkv, a, b, a_log, dt_bias, slots, cu, accepted, pool, 
 
 def expected_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log, dt_bias,
                          indices, cu, accepted, pool, gate, weight, out, eps, *, return_pre=False):
-    """Expected (out, pool, conv_state) after one conv-fused decode call: the conv update
-    (oracle/conv.py) of every valid single-token request on conv slot indices[r, 0], then
-    expected_decode on the post-conv activations.  Invalid requests touch neither pool.
+    """Expected (out, pool, conv_state) after one conv-fused decode / verify call: the conv
+    update (oracle/conv.py, conv_update_tokens) of every request's tokens on conv slot
+    indices[r, 0] from column offset accepted[r] - 1, then expected_decode on the post-conv
+    activations.  A request is processed only if the GDN step accepts it and its conv
+    columns lie in the state (conv slot > 0, offset + 2 <= S - 1, and offset <= n - 1 unless
+    n >= S); otherwise its outputs are zero and neither pool changes.
     Returns (out, pool[, pre], conv_state, post), post being the bf16 post-conv activation
     matrix the GDN step consumed."""
     mixed = mixed_qkv.cpu()
     cstate = conv_state.cpu().clone()
     indices_c, cu_c, accepted_c = indices.cpu().long(), cu.cpu().long(), accepted.cpu().long()
+    width = indices_c.shape[1]
+    cols = cstate.shape[-1]
     post = mixed.clone()
+    gdn_accepted = accepted_c.clone()
     for r in range(indices_c.shape[0]):
         bos, eos = int(cu_c[r]), int(cu_c[r + 1])
-        slot = int(indices_c[r, 0])
-        if eos - bos != 1 or int(accepted_c[r]) != 1 or slot <= 0:
+        n = eos - bos
+        acc = int(accepted_c[r])
+        source = int(indices_c[r, acc - 1]) if 1 <= acc <= width else 0
+        conv_slot = int(indices_c[r, 0])
+        offset = acc - 1
+        if n <= 0 or source <= 0 or n > width:
+            continue  # expected_decode treats it as invalid on its own
+        if conv_slot <= 0 or offset + 2 > cols - 1 or (cols > n and offset > n - 1):
+            gdn_accepted[r] = 0  # invalid: zero outputs, no writes
             continue
-        y, new_state = conv_oracle.conv_update(
-            mixed[bos:eos], cstate[slot][None], conv_weight.cpu(),
-            None if conv_bias is None else conv_bias.cpu())
+        y, new_state = conv_oracle.conv_update_tokens(
+            mixed[bos:eos], cstate[conv_slot], conv_weight.cpu(),
+            None if conv_bias is None else conv_bias.cpu(), offset)
         post[bos:eos] = y
-        cstate[slot] = new_state[0]
-    result = expected_decode(post, a, b, a_log, dt_bias, indices, cu, accepted, pool, gate,
-                             weight, out, eps, return_pre=return_pre)
+        cstate[conv_slot] = new_state
+    result = expected_decode(post, a, b, a_log, dt_bias, indices, cu, gdn_accepted.to(torch.int32),
+                             pool, gate, weight, out, eps, return_pre=return_pre)
     return result + (cstate, post)

@@ -77,7 +77,7 @@ def test_empty_work_is_a_no_op():
     assert lib.ld_state_gather(None, 0, None, 1, None, None, 0, 2048, 0, None) == 0
 
 
-def test_decode_conv_rejects_multi_token_and_bad_conv_shapes():
+def test_decode_conv_rejects_bad_widths_and_conv_shapes():
     lib = _lib.load()
     args = _lib.DecodeArgs()
     args.num_requests = 1
@@ -85,9 +85,9 @@ def test_decode_conv_rejects_multi_token_and_bad_conv_shapes():
     args.eps = 1e-6
     conv = _lib.ConvArgs()
     conv.width, conv.state_len, conv.weight_dtype = 4, 3, _lib.DTYPE_BF16
-    args.width = 2
+    args.width = 5
     assert lib.ld_gdn_decode_conv(ctypes.byref(args), ctypes.byref(conv), None) == 1
-    assert "1 token per request" in lib.ld_last_error().decode()
+    assert "1 through 4 tokens" in lib.ld_last_error().decode()
     args.width = 1
     conv.width = 3
     assert lib.ld_gdn_decode_conv(ctypes.byref(args), ctypes.byref(conv), None) == 1

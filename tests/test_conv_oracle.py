@@ -120,3 +120,49 @@ def test_round_to_bf16_is_single_rounding():
     np.testing.assert_array_equal(got, want)
     # the double rounding the oracle avoids would disagree on some of the nudged values
     assert (through_fp32.numpy() != got[:200]).any()
+
+
+def spec_case(seed, channels=5, cols=6, length=4):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(length, channels, generator=g).bfloat16()
+    state = torch.randn(channels, cols, generator=g).bfloat16()
+    weight = (torch.randn(channels, 4, generator=g) / 2).bfloat16()
+    bias = torch.randn(channels, generator=g).bfloat16()
+    return x, state, weight, bias
+
+
+def test_single_token_step_is_the_plain_update():
+    x, state, weight, bias = spec_case(1, cols=3, length=1)
+    y, new_state = conv.conv_update_tokens(x, state, weight, bias, offset=0)
+    y1, new1 = conv.conv_update(x, state[None], weight, bias)
+    assert torch.equal(y, y1) and torch.equal(new_state, new1[0])
+
+
+@pytest.mark.parametrize("offset", [0, 1, 2, 3])
+def test_multi_token_outputs_equal_a_rolling_single_token_conv(offset):
+    """Token t's output is the single-token update applied after tokens 0..t-1, starting
+    from the W-1 history columns at the offset."""
+    x, state, weight, bias = spec_case(2 + offset)
+    y, _ = conv.conv_update_tokens(x, state, weight, bias, offset=offset)
+    rolling = state[None, :, offset:offset + 3]
+    for t in range(x.shape[0]):
+        yt, rolling = conv.conv_update(x[t][None], rolling, weight, bias)
+        assert torch.equal(y[t], yt[0])
+
+
+@pytest.mark.parametrize("offset", [0, 1, 2, 3])
+def test_next_step_history_ends_at_each_accepted_token(offset):
+    """The defining property of the speculative conv state: after a step with L tokens,
+    accepting n of them (the next step's offset n-1) selects the W-1 inputs that end at
+    x_{n-1} in the sequence history ++ x.  A plain shift by L (the non-speculative update)
+    violates it."""
+    x, state, weight, bias = spec_case(10 + offset)
+    length = x.shape[0]
+    _, new_state = conv.conv_update_tokens(x, state, weight, bias, offset=offset)
+    seq = torch.cat([state[:, offset:offset + 3], x.t()], -1)
+    for n in range(1, length + 1):
+        assert torch.equal(new_state[:, n - 1:n + 2], seq[:, n:n + 3])
+    if offset != length - 1:  # where a plain shift by L coincides with the update
+        shifted = torch.cat([state[:, length:], x.t()], -1)  # planted mistake
+        assert not all(torch.equal(shifted[:, n - 1:n + 2], seq[:, n:n + 3])
+                       for n in range(1, length + 1))

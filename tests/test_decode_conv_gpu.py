@@ -4,7 +4,9 @@ state is a pure shift of bf16 data and must match bit for bit; SSM states and ou
 the decode tolerances.  Covers the workload's first configuration (B=1, 4/8 heads,
 zero-initialised conv state), the k-head groups 1, 2 and 3 (direct write and the
 last-reader write of the shared q/k conv state), vLLM's dim-first and dim-last conv pools,
-state lengths 3 and 4, bias, padding and zero-token requests, and graph replay."""
+state lengths 3, 4 and 6, bias, padding and zero-token requests, speculative verify with 2
+to 4 tokens and random accepted counts over consecutive steps, requests the conv rejects,
+and graph replay."""
 
 from __future__ import annotations
 
@@ -27,8 +29,8 @@ def announce(**what):
 
 
 def conv_case(gpu, batch, heads, pool_slots, length=3, dim_last=False, bias=False, seed=0,
-              zero_state=False):
-    case = decode_case(batch, 1, num_k_heads=heads[0], num_v_heads=heads[1],
+              zero_state=False, width=1):
+    case = decode_case(batch, width, num_k_heads=heads[0], num_v_heads=heads[1],
                        pool_slots=pool_slots, seed=seed, device=gpu)
     conv_dim = case["qkv"].shape[1]
     g = torch.Generator().manual_seed(seed + 100)
@@ -49,7 +51,11 @@ def check_step(case, expected, label):
     """The conv output is correctly rounded on both sides, so the post-conv activations are
     bit-identical and the GDN step is held to the plain decode tolerances."""
     exp_out, exp_pool, pre, exp_conv, _ = expected
-    assert torch.equal(case["conv_state"].cpu(), exp_conv), f"{label}: conv state"
+    got_conv = case["conv_state"].cpu()
+    if not torch.equal(got_conv, exp_conv):
+        bad = (got_conv != exp_conv).nonzero()
+        raise AssertionError(f"{label}: conv state differs at {len(bad)} elements "
+                             f"(slot, channel, column) first {bad[:6].tolist()}")
     assert_bf16_outputs(case["out"], exp_out, pre, label=label)
     assert_states(case["pool"], exp_pool, label=label, **STEP_STATE)
 
@@ -132,4 +138,78 @@ def test_graph_replay_with_changed_slots(gpu):
         graph.replay()
         torch.cuda.synchronize()
         check_step(case, expected, f"replay {replay}")
+        case["pool"].copy_(expected[1].to(case["pool"].device))
+
+
+@pytest.mark.parametrize("width,heads,dim_last", [(2, (16, 32), False), (3, (16, 16), True),
+                                                  (4, (16, 32), True), (4, (16, 48), False)])
+def test_speculative_verify_steps(gpu, width, heads, dim_last):
+    """Consecutive verify steps with W tokens per request and a conv state of 3 + W - 1
+    columns; each step's accepted count (the previous step's accepted tokens) is random in
+    1..W, so the conv history starts at a different column per request."""
+    announce(test="conv_verify", width=width, heads=heads, dim_last=dim_last)
+    case = conv_case(gpu, 6, heads, pool_slots=6 * width + 2, length=3 + width - 1,
+                     dim_last=dim_last, bias=True, seed=20 + width, width=width)
+    gen = torch.Generator().manual_seed(30 + width)
+    for step in range(3):
+        case["accepted"].copy_(torch.randint(1, width + 1, (6,), generator=gen, dtype=torch.int32))
+        run_and_check(case, 1, gen, label=f"verify W={width} step {step}")
+
+
+def test_ragged_verify_and_rejected_requests(gpu):
+    """W=4 with requests of 4, 2, 1 and 3 tokens: accepted within each request's tokens, one
+    request whose accepted count exceeds its tokens (its kept conv columns would fall
+    outside the state: rejected, zero outputs), one whose conv slot indices[r, 0] is padding
+    while its source slot is valid (rejected), and a padding-free short request."""
+    announce(test="conv_ragged")
+    case = conv_case(gpu, 6, (16, 32), pool_slots=30, length=6, seed=40, width=4)
+    case["cu"].copy_(torch.tensor([0, 4, 6, 7, 10, 12, 14], device=gpu, dtype=torch.int32))
+    case["accepted"].copy_(torch.tensor([3, 2, 1, 3, 2, 2], device=gpu, dtype=torch.int32))
+    case["accepted"][3] = 3  # 3 tokens, accepted 3: valid
+    case["accepted"][4] = 2  # 2 tokens, accepted 2: valid
+    case["cu"][5] = 13
+    case["accepted"][5] = 2  # request 5 has 1 token (13..14) and accepted 2 > 1: rejected
+    case["slots"][1, 0] = 0  # request 1: conv slot padding, source slots[1, 1] valid: rejected
+    for name in ("qkv", "a", "b", "gate", "out"):
+        case[name] = case[name][:14]
+    case["out"].fill_(1.0)
+    before = case["conv_state"].clone()
+    run_and_check(case, 1, torch.Generator().manual_seed(41), label="ragged verify")
+    out = case["out"].float().cpu()
+    assert out[4:6].abs().sum() == 0 and out[13:14].abs().sum() == 0
+    for r in (1, 5):
+        s0 = int(case["slots"][r, 0])
+        if s0 > 0:
+            assert torch.equal(case["conv_state"][s0].cpu(), before[s0].cpu())
+
+
+def test_single_token_long_conv_state(gpu):
+    """One token per request with a 6-column conv state (the conv runs before the tile)."""
+    announce(test="conv_long_state")
+    case = conv_case(gpu, 8, (16, 32), pool_slots=12, length=6, bias=True, seed=50)
+    run_and_check(case, 3, torch.Generator().manual_seed(51), label="long state")
+
+
+def test_verify_graph_replay(gpu):
+    announce(test="conv_verify_graph")
+    case = conv_case(gpu, 4, (16, 32), pool_slots=20, length=6, seed=60, width=4)
+    case["accepted"].copy_(torch.tensor([1, 4, 2, 3], device=gpu, dtype=torch.int32))
+    args = lambda: (case["qkv"], case["conv_state"], case["conv_weight"], case["conv_bias"],  # noqa: E731
+                    *[case[k] for k in ORDER], 1e-6)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        torch.ops.lightdelta.decode_conv(*args())
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        torch.ops.lightdelta.decode_conv(*args())
+    gen = torch.Generator().manual_seed(61)
+    for replay in range(3):
+        case["qkv"].copy_(torch.randn(case["qkv"].shape, generator=gen).bfloat16())
+        case["accepted"].copy_(torch.randint(1, 5, (4,), generator=gen, dtype=torch.int32))
+        expected = expected_decode_conv(*args(), return_pre=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        check_step(case, expected, f"verify replay {replay}")
         case["pool"].copy_(expected[1].to(case["pool"].device))
