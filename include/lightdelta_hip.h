@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 4
+#define LD_ABI_VERSION 5
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -143,6 +143,48 @@ typedef struct ld_conv_args {
  * lightdelta::decode (python/lightdelta/integration/vllm_layer.py:150-172, 199-220).
  */
 int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_args* conv, void* stream);
+
+/*
+ * Prefill of N sequences (varlen, one token per row of qkv; sequence n covers rows
+ * cu_seqlens[n] .. cu_seqlens[n+1]-1).  Per (sequence, v-head): the state starts from
+ * state[slots[n]] when slots[n] > 0 and has_initial[n] != 0, else from zeros; every token
+ * runs the decode recurrence (same numerics as ld_gdn_decode, token by token) and writes
+ * its gated-RMSNorm output to out[row]; the state after the last token is written to
+ * state[slots[n]] when slots[n] > 0 (an empty sequence writes its initial state back).
+ * Layouts as ld_gdn_decode (qkv, a, b, gate, out row strides; state [slots, HV, 128,
+ * 128]); has_initial is one byte per sequence; cu_seqlens is trusted device metadata.
+ * Replaces the reference's prefill composition (python/lightdelta/integration/
+ * vllm_layer.py:93-135: fused_post_conv_prep, gather_state with has_initial_state,
+ * chunk_gated_delta_rule, scatter_state, gated RMSNorm) in one launch.
+ */
+typedef struct ld_gdn_prefill_args {
+  const void* qkv;
+  int64_t qkv_row_stride;
+  const void* a;
+  int64_t a_row_stride;
+  const void* b;
+  int64_t b_row_stride;
+  const float* a_log;
+  const void* dt_bias;
+  int32_t dt_bias_dtype;
+  int32_t norm_weight_dtype;
+  const int32_t* slots;
+  const uint8_t* has_initial;
+  const int32_t* cu_seqlens;
+  float* state;
+  int64_t state_slot_stride;
+  const void* gate;
+  int64_t gate_row_stride;
+  const void* norm_weight;
+  void* out;
+  int32_t num_sequences;
+  int32_t num_k_heads;
+  int32_t num_v_heads;
+  float scale;
+  float eps;
+} ld_gdn_prefill_args;
+
+int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream);
 
 /*
  * Gather pool rows into a packed buffer:

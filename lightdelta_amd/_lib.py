@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must precede the CDLL load (see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("liblightdelta_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 CACHE_KEEP = 0
@@ -81,9 +81,41 @@ class ConvArgs(ctypes.Structure):
     ]
 
 
+class PrefillArgs(ctypes.Structure):
+    """Mirror of ld_gdn_prefill_args (include/lightdelta_hip.h)."""
+
+    _fields_ = [
+        ("qkv", _vp),
+        ("qkv_row_stride", _c_i64),
+        ("a", _vp),
+        ("a_row_stride", _c_i64),
+        ("b", _vp),
+        ("b_row_stride", _c_i64),
+        ("a_log", _vp),
+        ("dt_bias", _vp),
+        ("dt_bias_dtype", _c_i32),
+        ("norm_weight_dtype", _c_i32),
+        ("slots", _vp),
+        ("has_initial", _vp),
+        ("cu_seqlens", _vp),
+        ("state", _vp),
+        ("state_slot_stride", _c_i64),
+        ("gate", _vp),
+        ("gate_row_stride", _c_i64),
+        ("norm_weight", _vp),
+        ("out", _vp),
+        ("num_sequences", _c_i32),
+        ("num_k_heads", _c_i32),
+        ("num_v_heads", _c_i32),
+        ("scale", ctypes.c_float),
+        ("eps", ctypes.c_float),
+    ]
+
+
 # Exported entry points and their C signatures (argtypes, restype).
 SIGNATURES = {
     "ld_gdn_decode": ([ctypes.POINTER(DecodeArgs), _vp], ctypes.c_int),
+    "ld_gdn_prefill": ([ctypes.POINTER(PrefillArgs), _vp], ctypes.c_int),
     "ld_gdn_decode_conv": (
         [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ConvArgs), _vp],
         ctypes.c_int,

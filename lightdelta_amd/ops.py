@@ -19,6 +19,12 @@ Additive ops (no reference counterpart):
                                         so vLLM's transposed dim-last view works); 1 to 4
                                         tokens per request, speculative verify with vLLM's
                                         num_accepted_tokens semantics (accepted)
+  prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state, gate, weight,
+          out, eps)                     the layer's prefill (post-conv activations of several
+                                        sequences, cu_seqlens rows each) in one launch: state
+                                        from slots[n] if has_initial[n] else zeros, the
+                                        decode recurrence token by token, gated RMSNorm
+                                        outputs, final state to slots[n]
   gather_slots / scatter_slots          dtype-generic gather_state / scatter_state, for the
                                         bf16 conv-state pool and any dense-inner pool
 
@@ -44,6 +50,11 @@ SCHEMAS = {
     "scatter_state": "scatter_state(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
     "copy_state": "copy_state(Tensor(p!) pool, Tensor src, Tensor dst) -> ()",
     "zero_slots": "zero_slots(Tensor(p!) pool, Tensor slots) -> ()",
+    "prefill": (
+        "prefill(Tensor qkv, Tensor a, Tensor b, Tensor a_log, Tensor dt_bias, Tensor slots, "
+        "Tensor has_initial, Tensor cu_seqlens, Tensor(s!) state, Tensor gate, Tensor weight, "
+        "Tensor(o!) out, float eps) -> ()"
+    ),
     "decode_conv": (
         "decode_conv(Tensor mixed_qkv, Tensor(c!) conv_state, Tensor conv_weight, "
         "Tensor? conv_bias, Tensor a, Tensor b, Tensor a_log, Tensor dt_bias, Tensor indices, "
@@ -198,6 +209,47 @@ def check_decode(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, 
     )
     _require(eps > 0, "norm epsilon must be positive")
     return h, hv
+
+
+def check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state, gate,
+                  weight, out, eps):
+    """Validation of prefill: decode's activation, weight and state rules, with per-sequence
+    metadata slots [N] int32, has_initial [N] bool and cu_seqlens [N+1] int32."""
+    for t in (slots, cu_seqlens):
+        _require(
+            t.device == qkv.device and t.dtype == torch.int32 and t.dim() == 1
+            and t.is_contiguous(),
+            "metadata must be contiguous CUDA int32",
+        )
+    _require(
+        has_initial.device == qkv.device and has_initial.dtype == torch.bool
+        and has_initial.dim() == 1 and has_initial.is_contiguous(),
+        "has_initial must be a contiguous CUDA bool vector",
+    )
+    _require(
+        cu_seqlens.numel() == slots.numel() + 1 and has_initial.numel() == slots.numel(),
+        "invalid sequence metadata shapes",
+    )
+    return check_decode(qkv, a, b, a_log, dt_bias, slots.view(-1, 1), cu_seqlens, slots, state,
+                        gate, weight, out, eps)
+
+
+def _prefill_impl(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state, gate,
+                  weight, out, eps):
+    h, hv = check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state,
+                          gate, weight, out, eps)
+    if slots.numel() == 0:
+        return
+    args = _lib.PrefillArgs(
+        qkv.data_ptr(), qkv.stride(0), a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+        a_log.data_ptr(), dt_bias.data_ptr(), _dtype_code(dt_bias), _dtype_code(weight),
+        slots.data_ptr(), has_initial.data_ptr(), cu_seqlens.data_ptr(), state.data_ptr(),
+        state.stride(0), gate.data_ptr(), gate.stride(0), weight.data_ptr(), out.data_ptr(),
+        slots.numel(), h, hv, QK_SCALE, eps,
+    )
+    lib = _lib.load()
+    with _DeviceGuard(qkv.device):
+        _lib.check(lib.ld_gdn_prefill(args, _stream(qkv.device)))
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -503,6 +555,7 @@ _IMPLS = {
     "scatter_state": _scatter_state_impl,
     "copy_state": _copy_state_impl,
     "zero_slots": _zero_slots_impl,
+    "prefill": _prefill_impl,
     "decode_conv": _decode_conv_impl,
     "gather_slots": _gather_slots_impl,
     "scatter_slots": _scatter_slots_impl,

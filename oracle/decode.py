@@ -11,6 +11,13 @@ pool (reference csrc/gdn_decode.cu:142-168 and 303-316, backend.py:39-47):
     the next request's indices there (csrc/gdn_decode.cu:303-304); this build bounds it.
 All sources are read before any write, as in a launch whose requests touch disjoint slots.
 
+`expected_prefill` restates the layer's prefill (reference
+python/lightdelta/integration/vllm_layer.py:93-135 with prefill_io = "fused_copy"): per
+sequence n (rows cu_seqlens[n] .. cu_seqlens[n+1]-1) the initial state is pool[slots[n]]
+when slots[n] > 0 and has_initial[n], else zeros (gather_state's zero fill); the sequence
+runs post_conv_gdn over its tokens; the final state goes to pool[slots[n]] when
+slots[n] > 0 (scatter_state skips padding).
+
 `packed_reference_step` is the reference's Torch path (backend.py:30-91 with
 compute="torch_reference"): gather with index_select, the unfused GDN, write back with
 index_copy_.  It mutates `pool` and `out` in place; bench.py times it as the CPU baseline.
@@ -80,6 +87,47 @@ def expected_decode(qkv, a, b, a_log, dt_bias, indices, cu, accepted, pool, gate
                 writes.append((dest, ckpt[0, t + 1]))
     for dest, state in writes:
         new_pool[dest] = state
+    if return_pre:
+        return new_out, new_pool, (raw_pre, y_pre)
+    return new_out, new_pool
+
+
+def expected_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, pool, gate,
+                     weight, out, eps, *, return_pre=False):
+    """Expected (out, pool) after one prefill call, as new CPU tensors; with return_pre also
+    (raw_pre, y_pre) [T, HV, 128] fp32 (zero on rows no sequence covers)."""
+    qkv, a, b, a_log, dt_bias, gate, weight = (
+        t.cpu() for t in (qkv, a, b, a_log, dt_bias, gate, weight))
+    slots, cu = slots.cpu().long(), cu_seqlens.cpu().long()
+    has_initial = has_initial.cpu()
+    new_out = out.cpu().clone()
+    new_pool = pool.cpu().clone()
+    source_pool = pool.cpu()
+    h, hv = geometry(qkv, source_pool)
+    raw_pre = torch.zeros(new_out.shape, dtype=torch.float32)
+    y_pre = torch.zeros(new_out.shape, dtype=torch.float32)
+    writes = []
+    for n in range(slots.numel()):
+        bos, eos = int(cu[n]), int(cu[n + 1])
+        slot = int(slots[n])
+        if slot > 0 and bool(has_initial[n]):
+            initial = source_pool[slot].clone()
+        else:
+            initial = torch.zeros(source_pool.shape[1:], dtype=source_pool.dtype)
+        final = initial
+        if eos > bos:
+            q, k, v, ar, br, gr = split_tokens(qkv, a, b, gate, slice(bos, eos), h, hv)
+            o, final, _, (raw, y) = gdn.run(
+                q, k, v, ar, br, a_log, dt_bias, gr, weight, initial[None],
+                torch.tensor([eos - bos]), norm_eps=eps, return_pre=True)
+            final = final[0]
+            new_out[bos:eos] = o[0]
+            raw_pre[bos:eos] = raw[0]
+            y_pre[bos:eos] = y[0]
+        if slot > 0:
+            writes.append((slot, final))
+    for slot, state in writes:
+        new_pool[slot] = state
     if return_pre:
         return new_out, new_pool, (raw_pre, y_pre)
     return new_out, new_pool

@@ -22,7 +22,8 @@ def declared_functions() -> set[str]:
 
 def test_header_declares_the_entry_points():
     assert declared_functions() == {
-        "ld_gdn_decode", "ld_gdn_decode_conv", "ld_state_gather", "ld_state_scatter",
+        "ld_gdn_decode", "ld_gdn_decode_conv", "ld_gdn_prefill", "ld_state_gather",
+        "ld_state_scatter",
         "ld_state_copy", "ld_state_zero", "ld_last_error", "ld_abi_version",
     }
 
@@ -36,7 +37,8 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.parametrize("struct,mirror", [("ld_gdn_decode_args", _lib.DecodeArgs),
-                                           ("ld_conv_args", _lib.ConvArgs)])
+                                           ("ld_conv_args", _lib.ConvArgs),
+                                           ("ld_gdn_prefill_args", _lib.PrefillArgs)])
 def test_args_layout_matches_header(struct, mirror):
     """ctypes mirrors of the argument structs: same field names in the same order."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
@@ -106,3 +108,18 @@ def test_copy_rejects_misaligned_rows():
     assert code == 1 and "16-byte aligned" in lib.ld_last_error().decode()
     code = lib.ld_state_zero(16, 2048, 32, 1, 24, None)
     assert code == 1 and "16-byte aligned" in lib.ld_last_error().decode()
+
+
+def test_prefill_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    args = _lib.PrefillArgs()
+    args.num_sequences = 1
+    args.num_k_heads, args.num_v_heads = 16, 24
+    args.eps = 1e-6
+    assert lib.ld_gdn_prefill(ctypes.byref(args), None) == 1
+    assert "multiple of num_k_heads" in lib.ld_last_error().decode()
+    args.num_v_heads = 32
+    assert lib.ld_gdn_prefill(ctypes.byref(args), None) == 1
+    assert "NULL tensor pointer" in lib.ld_last_error().decode()
+    args.num_sequences = 0
+    assert lib.ld_gdn_prefill(ctypes.byref(args), None) == 0

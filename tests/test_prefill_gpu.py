@@ -1,0 +1,142 @@
+"""Parity of the gfx950 prefill (torch.ops.lightdelta.prefill) with the oracle's restatement
+of the layer's prefill (oracle/decode.py expected_prefill), and with the decode kernel:
+a prefill of n tokens must give bit for bit the states and outputs of n single-token
+decode steps on the same slot (the per-token arithmetic is shared)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from lightdelta_amd.workloads import decode_case
+from oracle.decode import expected_prefill
+from tests.parity import assert_bf16_outputs, assert_states
+
+pytestmark = pytest.mark.gpu
+
+PREFILL = ("qkv", "a", "b", "a_log", "dt_bias", "slots", "has_initial", "cu_seqlens", "pool",
+           "gate", "weight", "out")
+
+
+def announce(**what):
+    print("case:", " ".join(f"{k}={v}" for k, v in what.items()), flush=True)
+
+
+def prefill_case(gpu, lengths, heads=(16, 32), pool_slots=None, seed=0, dt_dtype=torch.float32,
+                 w_dtype=torch.float32):
+    """Sequences of the given lengths packed row after row; one slot per sequence."""
+    total = sum(lengths)
+    n = len(lengths)
+    pool_slots = pool_slots or n + 2
+    case = decode_case(max(total, 1), 1, num_k_heads=heads[0], num_v_heads=heads[1],
+                       pool_slots=max(pool_slots, total + 1), seed=seed, device=gpu,
+                       dt_bias_dtype=dt_dtype, weight_dtype=w_dtype)
+    for name in ("qkv", "a", "b", "gate", "out"):
+        case[name] = case[name][:total]
+    gen = torch.Generator().manual_seed(seed + 1)
+    case["slots"] = (torch.randperm(case["pool"].shape[0] - 1, generator=gen)[:n] + 1).to(
+        torch.int32).to(gpu)
+    case["has_initial"] = torch.ones(n, dtype=torch.bool, device=gpu)
+    cu = torch.zeros(n + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lengths), 0)
+    case["cu_seqlens"] = cu.to(gpu)
+    return case
+
+
+def run(case, eps=1e-6):
+    torch.ops.lightdelta.prefill(*[case[k] for k in PREFILL], eps)
+
+
+@pytest.mark.parametrize("heads", [(16, 32), (4, 8), (16, 48)])
+def test_prefill_matches_oracle(gpu, heads):
+    announce(test="prefill_oracle", heads=heads)
+    case = prefill_case(gpu, [5, 0, 1, 33, 70], heads=heads, seed=heads[1])
+    case["has_initial"][3] = False  # starts from zeros
+    case["slots"][2] = 0  # padding slot: zero initial state, final state dropped
+    exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6, return_pre=True)
+    before = case["pool"].clone()
+    run(case)
+    torch.cuda.synchronize()
+    assert_bf16_outputs(case["out"], exp_out, pre)
+    assert_states(case["pool"], exp_pool)
+    assert torch.equal(case["pool"][0], before[0])
+
+
+@pytest.mark.parametrize("dt_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("w_dtype", [torch.float32, torch.bfloat16])
+def test_prefill_parameter_dtypes(gpu, dt_dtype, w_dtype):
+    announce(test="prefill_dtypes", dt=dt_dtype, w=w_dtype)
+    case = prefill_case(gpu, [9, 17], seed=2, dt_dtype=dt_dtype, w_dtype=w_dtype)
+    exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6, return_pre=True)
+    run(case)
+    torch.cuda.synchronize()
+    assert_bf16_outputs(case["out"], exp_out, pre)
+    assert_states(case["pool"], exp_pool)
+
+
+def decode_steps(case, eps=1e-6):
+    """The same sequences as single-token decode steps, one launch per token, on a copy of
+    the pool; returns (out, pool)."""
+    pool = case["pool"].clone()
+    out = torch.zeros_like(case["out"])
+    cu = case["cu_seqlens"].cpu().tolist()
+    one = torch.ones(1, dtype=torch.int32, device=pool.device)
+    for n, slot in enumerate(case["slots"].cpu().tolist()):
+        if not bool(case["has_initial"][n]):
+            pool[slot].zero_()
+        for t in range(cu[n], cu[n + 1]):
+            torch.ops.lightdelta.decode(
+                case["qkv"][t:t + 1], case["a"][t:t + 1], case["b"][t:t + 1], case["a_log"],
+                case["dt_bias"], case["slots"][n:n + 1].view(1, 1),
+                torch.tensor([0, 1], dtype=torch.int32, device=pool.device), one, pool,
+                case["gate"][t:t + 1], case["weight"], out[t:t + 1], eps)
+    return out, pool
+
+
+def test_prefill_equals_decode_steps_bit_for_bit(gpu):
+    announce(test="prefill_vs_decode")
+    case = prefill_case(gpu, [3, 40, 1, 77], seed=5)
+    case["has_initial"][1] = False
+    exp_out, exp_pool = decode_steps(case)
+    run(case)
+    torch.cuda.synchronize()
+    assert torch.equal(case["out"], exp_out)
+    assert torch.equal(case["pool"], exp_pool)
+
+
+def test_long_prompt(gpu):
+    """One 2048-token prompt at 16/32 heads: bit-exact against 2048 decode steps, and within
+    the build's tolerance of the oracle's state after 2048 recurrent steps."""
+    announce(test="prefill_long")
+    case = prefill_case(gpu, [2048], seed=6)
+    exp_out, exp_pool = decode_steps(case)
+    oracle_out, oracle_pool = expected_prefill(*[case[k] for k in PREFILL], 1e-6)
+    run(case)
+    torch.cuda.synchronize()
+    assert torch.equal(case["out"], exp_out)
+    assert torch.equal(case["pool"], exp_pool)
+    assert_states(case["pool"], oracle_pool)
+    torch.testing.assert_close(case["out"].float().cpu(), oracle_out.float(), atol=8e-3, rtol=2e-2)
+
+
+def test_prefill_graph_capture(gpu):
+    announce(test="prefill_graph")
+    case = prefill_case(gpu, [12, 30, 7], seed=8)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run(case)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(case)
+    gen = torch.Generator().manual_seed(9)
+    for replay in range(3):
+        case["slots"].copy_((torch.randperm(case["pool"].shape[0] - 1, generator=gen)[:3] + 1)
+                            .to(torch.int32))
+        exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6,
+                                                  return_pre=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bf16_outputs(case["out"], exp_out, pre, label=f"replay {replay}")
+        assert_states(case["pool"], exp_pool, label=f"replay {replay}")
