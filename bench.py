@@ -25,7 +25,7 @@ in the 256 MB Infinity Cache between consecutive steps.  A second, cache-cold fi
 (non-temporal state traffic), the regime of a many-layer model.
 
 Further figures in the same line: `conv_fused` (the same step with the width-4 causal
-conv1d + SiLU fused in front) and `stack48` (48 layers captured as one HIP graph, batch
+conv1d + SiLU fused in front), `prefill` (32 x 1024 and 1 x 4096 tokens) and `stack48` (48 layers captured as one HIP graph, batch
 128, 1024 slots per layer = 96 GiB of state, slot ids reshuffled before every replay, 256
 replays timed end to end; --no-stack skips it).
 
@@ -69,6 +69,7 @@ def parse_args():
     p.add_argument("--no-stack", action="store_true",
                    help="skip the 48-layer, 96 GiB stack measurement")
     p.add_argument("--stack-steps", type=int, default=256)
+    p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-graph", action="store_true",
                    help="time K eager launches instead of one K-step graph replay")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -194,6 +195,51 @@ def conv_fused(case, op_args, steps, device):
         "state_TBps": round(STATE_BYTES * rate / 1e12, 3),
         "frac": round((STATE_BYTES + conv_bytes) * rate / 1e9 / HBM_PEAK_GBS, 4),
     }
+
+
+def prefill(device):
+    """Prefill of 32 prompts x 1024 tokens and of one 4096-token prompt (16 qk / 32 v heads,
+    states from slots of a 64-slot pool), timed over a few eager launches each."""
+    import torch
+
+    order = ("qkv", "a", "b", "a_log", "dt_bias", "slots", "has_initial", "cu_seqlens",
+             "pool", "gate", "weight", "out")
+    gen = torch.Generator(device=device).manual_seed(7)
+    qkv_cols = (2 * H + HV) * DIM
+    result = {}
+    for label, seqs, length in (("batch_32x1024", 32, 1024), ("single_4096", 1, 4096)):
+        total = seqs * length
+        qkvz = torch.randn(total, qkv_cols + HV * DIM, generator=gen, device=device).bfloat16()
+        ba = torch.randn(total, 2 * HV, generator=gen, device=device).bfloat16()
+        case = dict(
+            qkv=qkvz[:, :qkv_cols], a=ba[:, HV:], b=ba[:, :HV],
+            a_log=torch.rand(HV, generator=gen, device=device) * 2 - 1,
+            dt_bias=torch.zeros(HV, device=device),
+            slots=torch.arange(1, seqs + 1, dtype=torch.int32, device=device),
+            has_initial=torch.ones(seqs, dtype=torch.bool, device=device),
+            cu_seqlens=torch.arange(0, total + 1, length, dtype=torch.int32, device=device),
+            pool=torch.empty(seqs + 1, HV, DIM, DIM, device=device).normal_(0.0, 0.02,
+                                                                            generator=gen),
+            gate=qkvz[:, qkv_cols:].view(total, HV, DIM),
+            weight=1 + 0.1 * torch.randn(DIM, generator=gen, device=device),
+            out=torch.empty(total, HV, DIM, dtype=torch.bfloat16, device=device),
+        )
+        run = lambda: torch.ops.lightdelta.prefill(*[case[k] for k in order], 1e-6)  # noqa: E731
+        run()
+        torch.cuda.synchronize()
+        start, end = events()
+        reps = 5
+        start.record()
+        for _ in range(reps):
+            run()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / reps
+        result[label] = {"ms": round(ms, 3), "tokens_per_s": round(total / ms * 1e3, 1)}
+        del case
+    result["workload"] = ("prefill (state from the slot, token-by-token recurrence, gated "
+                          "RMSNorm, final state to the slot), 16 qk / 32 v heads")
+    return result
 
 
 def stack48(steps, device):
@@ -386,6 +432,9 @@ def main():
 
     if not args.no_conv:
         result["conv_fused"] = conv_fused(case, op_args, args.steps, device)
+
+    if not args.no_prefill:
+        result["prefill"] = prefill(device)
 
     if not args.no_stack:
         case = op_args = graph = None  # noqa: F841  (release the B=32 pools first)
