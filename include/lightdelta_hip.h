@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 5
+#define LD_ABI_VERSION 6
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -152,7 +152,10 @@ int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_args* conv,
  * its gated-RMSNorm output to out[row]; the state after the last token is written to
  * state[slots[n]] when slots[n] > 0 (an empty sequence writes its initial state back).
  * Layouts as ld_gdn_decode (qkv, a, b, gate, out row strides; state [slots, HV, 128,
- * 128]); has_initial is one byte per sequence; cu_seqlens is trusted device metadata.
+ * 128]); has_initial is one byte per sequence; cu_seqlens is trusted device metadata
+ * (non-decreasing, sequences contiguous from cu_seqlens[0]).  When sequences x heads are
+ * too few to fill the GPU, a head's state rows are split over several workgroups and the
+ * norm runs as a second launch on the same stream (same results).
  * Replaces the reference's prefill composition (python/lightdelta/integration/
  * vllm_layer.py:93-135: fused_post_conv_prep, gather_state with has_initial_state,
  * chunk_gated_delta_rule, scatter_state, gated RMSNorm) in one launch.
@@ -177,6 +180,7 @@ typedef struct ld_gdn_prefill_args {
   int64_t gate_row_stride;
   const void* norm_weight;
   void* out;
+  int64_t num_tokens;  /* rows of qkv / out (cu_seqlens[num_sequences] <= num_tokens) */
   int32_t num_sequences;
   int32_t num_k_heads;
   int32_t num_v_heads;

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must precede the CDLL load (see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("liblightdelta_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 CACHE_KEEP = 0
@@ -104,6 +104,7 @@ class PrefillArgs(ctypes.Structure):
         ("gate_row_stride", _c_i64),
         ("norm_weight", _vp),
         ("out", _vp),
+        ("num_tokens", _c_i64),
         ("num_sequences", _c_i32),
         ("num_k_heads", _c_i32),
         ("num_v_heads", _c_i32),

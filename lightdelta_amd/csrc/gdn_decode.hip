@@ -237,8 +237,8 @@ __device__ __forceinline__ Staged stage_token(const TokenIn& in, float a_log, fl
 //   S <- decay*S ; delta = (v - S k^) * beta ; S += delta k^ ; raw = bf16(S q^)
 // The updated pieces are stored to `dst_tile` (NULL: padding slot, nothing stored) and the
 // two rows' raw outputs go to LDS (one lane per row).
-template <int C, bool Stream, bool Store = true>
-__device__ __forceinline__ void chunk_step(f32x4 (&s)[kPieces], const Vectors& x, float v0,
+template <int C, bool Stream, bool Store = true, int N = kPieces>
+__device__ __forceinline__ void chunk_step(f32x4 (&s)[N], const Vectors& x, float v0,
                                            float v1, float* o, float decay, float beta,
                                            int kq, int row0, char* dst_tile,
                                            uint32_t lane_bytes) {
@@ -792,26 +792,37 @@ void gdn_decode_kernel(const DecodeParams args) {
 }
 
 
-// Prefill: one workgroup per (sequence, v-head) runs the sequence's tokens in order with the
-// state tile in registers for the whole prompt (the state is read once, from the slot or as
-// zeros, and written once, to the slot), and writes every token's gated-RMSNorm output.  The
+// Prefill: the sequence's tokens run in order with a block of state rows in registers for
+// the whole prompt (read once, from the slot or as zeros; written once, to the slot).  The
 // per-token arithmetic is the decode kernel's (stage_token, chunk_step), so a prefill of n
-// tokens gives bit for bit the states and outputs of n single-token decode steps.  Tokens go
-// in groups of 4: each wave stages the token for itself (wave-private LDS for its v rows),
-// the raw outputs of the group collect in LDS (double-buffered), and after one barrier per
-// group wave w runs the epilogue of the group's token w.  Token inputs are prefetched one
-// token ahead.
+// tokens gives bit for bit the states and outputs of n single-token decode steps.  Rows of
+// the state evolve independently (row v needs only v[v], k, q and the gates), so a head's
+// 128 rows may be split over 4 / Chunks workgroups of 4 waves, each wave holding 8 * Chunks
+// rows: fewer rows per wave shorten the per-token chain and spread a few long prompts over
+// more of the GPU, at the price of staging q and k in every workgroup.
+//   Chunks == 4 (one workgroup per head): the raw outputs of a group of 4 tokens collect in
+//   LDS (double-buffered); after one barrier per group, wave w runs the gated-RMSNorm
+//   epilogue of the group's token w.
+//   Chunks < 4: every wave writes its rows' raw outputs (rounded to bf16, the reference's
+//   rounding point before the norm) to `out`; prefill_norm_kernel applies the gated RMSNorm
+//   in place afterwards, with the epilogue's arithmetic.
+// The next token's inputs are prefetched.  Three to four waves per SIMD: the token loop
+// keeps them in flight on top of the tile, which does not fit 128 VGPRs without spills.
 constexpr int kPrefillGroup = 4;
 
-// Three to four waves per SIMD: the token loop keeps the next token's inputs in flight on
-// top of the 64-register tile, which does not fit 128 VGPRs without spills.
-template <bool DtBf16, bool WBf16>
+template <bool DtBf16, bool WBf16, int Chunks>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4)))
 void gdn_prefill_kernel(const DecodeParams args) {
+  static_assert(Chunks == 1 || Chunks == 2 || Chunks == 4, "8, 16 or 32 rows per wave");
+  constexpr int kBlocks = 4 / Chunks;         // workgroups per (sequence, head)
+  constexpr int kWaveRows = 8 * Chunks;       // state rows per wave
+  constexpr int kTilePieces = 4 * Chunks;     // 16-byte pieces per lane
   const DecodeParams& p = args;
   const int tile = blockIdx.x;
-  const int sequence = tile / p.num_v_heads;
-  const int head = tile - sequence * p.num_v_heads;
+  const int sequence = tile / (p.num_v_heads * kBlocks);
+  const int rest = tile - sequence * p.num_v_heads * kBlocks;
+  const int head = rest / kBlocks;
+  const int block = rest - head * kBlocks;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -823,84 +834,100 @@ void gdn_prefill_kernel(const DecodeParams args) {
   const int key_head = head / p.group;
   const int kq = lane & 15;
   const int rsub = lane >> 4;
-  const int row_base = wave * kRowsPerWave + rsub;
+  const int wave_row0 = block * kWaves * kWaveRows + wave * kWaveRows;  // first row of the wave
+  const int row_base = wave_row0 + rsub;
   const int q_col = key_head * kDim;
   const int k_col = (p.num_k_heads + key_head) * kDim;
   const int v_col = (2 * p.num_k_heads + head) * kDim;
-  const int v_lane = v_col + wave * kRowsPerWave + (lane & 31);
+  const int v_lane = v_col + wave_row0 + (lane & (kWaveRows - 1));
 
-  __shared__ float s_v[kWaves][kRowsPerWave];
-  __shared__ float s_o[2][kPrefillGroup][kDim];
+  __shared__ float s_v[kWaves][kWaveRows];
+  __shared__ float s_o[Chunks == 4 ? 2 : 1][Chunks == 4 ? kPrefillGroup : kWaves]
+                      [Chunks == 4 ? kDim : kWaveRows];
 
   const float dt_bias = load_param(p.dt_bias, head, DtBf16);
   const float a_log = p.a_log[head];
   float w[2];
 #pragma unroll
-  for (int e = 0; e < 2; ++e) w[e] = load_param(p.norm_weight, 2 * lane + e, WBf16);
+  for (int e = 0; e < 2; ++e) w[e] = Chunks == 4 ? load_param(p.norm_weight, 2 * lane + e, WBf16) : 0.0f;
 
   const int64_t head_offset = static_cast<int64_t>(head) * kDim * kDim;
   const uint32_t lane_bytes = static_cast<uint32_t>(row_base * kDim + kq * 4) * 4u;
-  f32x4 s[kPieces];
+  f32x4 s[kTilePieces];
   if (from_slot) {
     const char* src_tile = reinterpret_cast<const char*>(
         p.state + static_cast<int64_t>(slot) * p.state_slot + head_offset);
 #pragma unroll
-    for (int j = 0; j < kPieces; ++j)
+    for (int j = 0; j < kTilePieces; ++j)
       s[j] = *reinterpret_cast<const f32x4*>(src_tile + (lane_bytes + tile_piece_bytes(j)));
   } else {
 #pragma unroll
-    for (int j = 0; j < kPieces; ++j) s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < kTilePieces; ++j) s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   TokenIn next;  // inputs of the next token
   if (bos < eos) next = load_token(p, bos, q_col, k_col, v_lane, head, kq);
   int buf = 0;
   for (int g0 = bos; g0 < eos; g0 += kPrefillGroup, buf ^= 1) {
-    // gate of the token whose epilogue this wave runs after the group
-    const int64_t etoken = min(g0 + wave, eos - 1);
-    uint16_t gh[2];
+    // gate of the token whose epilogue this wave runs after the group (one workgroup per head)
+    uint16_t gh[2] = {0, 0};
+    if constexpr (Chunks == 4) {
+      const int64_t etoken = min(g0 + wave, eos - 1);
 #pragma unroll
-    for (int e = 0; e < 2; ++e) gh[e] = p.gate[etoken * p.gate_row + head * kDim + 2 * lane + e];
+      for (int e = 0; e < 2; ++e) gh[e] = p.gate[etoken * p.gate_row + head * kDim + 2 * lane + e];
+    }
     for (int i = 0; i < kPrefillGroup && g0 + i < eos; ++i) {
       const int t = g0 + i;
       const TokenIn in = next;
       if (t + 1 < eos) next = load_token(p, t + 1, q_col, k_col, v_lane, head, kq);
       const Staged x = stage_token(in, a_log, dt_bias, p.scale);
-      if (lane < kRowsPerWave) s_v[wave][lane] = bf16_to_f32(in.v);
-      // s_v is read back by other lanes of this wave: a wave's LDS operations run in program
-      // order, so only the compiler must not move the reads above the writes.
+      if (lane < kWaveRows) s_v[wave][lane] = bf16_to_f32(in.v);
+      // s_v (and s_o below) are read back by other lanes of this wave: a wave's LDS
+      // operations run in program order, so only the compiler must not reorder them.
       asm volatile("" ::: "memory");
       Vectors vec;
       vec.q0 = x.q0;
       vec.q1 = x.q1;
       vec.k0 = x.k0;
       vec.k1 = x.k1;
-      float* o = s_o[buf][i];
-      chunk_step<0, false, false>(s, vec, s_v[wave][rsub], s_v[wave][4 + rsub], o, x.decay,
-                                  x.beta, kq, row_base, nullptr, lane_bytes);
-      chunk_step<1, false, false>(s, vec, s_v[wave][8 + rsub], s_v[wave][12 + rsub], o, x.decay,
-                                  x.beta, kq, row_base + 8, nullptr, lane_bytes);
-      chunk_step<2, false, false>(s, vec, s_v[wave][16 + rsub], s_v[wave][20 + rsub], o,
-                                  x.decay, x.beta, kq, row_base + 16, nullptr, lane_bytes);
-      chunk_step<3, false, false>(s, vec, s_v[wave][24 + rsub], s_v[wave][28 + rsub], o,
-                                  x.decay, x.beta, kq, row_base + 24, nullptr, lane_bytes);
+      // output rows: absolute in the per-group buffer, wave-relative in the per-wave one
+      float* o = Chunks == 4 ? s_o[buf][i] : s_o[0][wave];
+      const int orow = Chunks == 4 ? row_base : rsub;
+#define LD_PREFILL_CHUNK(C)                                                                    \
+  if constexpr ((C) < Chunks)                                                                  \
+    chunk_step<C, false, false, kTilePieces>(s, vec, s_v[wave][8 * (C) + rsub],                \
+                                             s_v[wave][8 * (C) + 4 + rsub], o, x.decay,        \
+                                             x.beta, kq, orow + 8 * (C), nullptr, lane_bytes);
+      LD_PREFILL_CHUNK(0)
+      LD_PREFILL_CHUNK(1)
+      LD_PREFILL_CHUNK(2)
+      LD_PREFILL_CHUNK(3)
+#undef LD_PREFILL_CHUNK
       asm volatile("" ::: "memory");
-    }
-    lds_barrier();  // the group's raw outputs are complete
-    if (g0 + wave < eos) {  // gated RMSNorm epilogue of the group's token `wave`
-      float raw[2];
-      float ss = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        raw[e] = s_o[buf][wave][2 * lane + e];
-        ss = fmaf(raw[e], raw[e], ss);
+      if constexpr (Chunks < 4) {  // raw outputs of the wave's rows (bf16-exact values)
+        if (lane < kWaveRows)
+          p.out[(static_cast<int64_t>(t) * p.num_v_heads + head) * kDim + wave_row0 + lane] =
+              f32_to_bf16(s_o[0][wave][lane]);
       }
-      ss = wave_sum(ss);
-      const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
-      uint16_t* orow = p.out + (static_cast<int64_t>(g0 + wave) * p.num_v_heads + head) * kDim;
+    }
+    if constexpr (Chunks == 4) {
+      lds_barrier();  // the group's raw outputs are complete
+      if (g0 + wave < eos) {  // gated RMSNorm epilogue of the group's token `wave`
+        float raw[2];
+        float ss = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 2; ++e)
-        orow[2 * lane + e] = f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(bf16_to_f32(gh[e])));
+        for (int e = 0; e < 2; ++e) {
+          raw[e] = s_o[buf][wave][2 * lane + e];
+          ss = fmaf(raw[e], raw[e], ss);
+        }
+        ss = wave_sum(ss);
+        const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
+        uint16_t* orow_ptr = p.out + (static_cast<int64_t>(g0 + wave) * p.num_v_heads + head) * kDim;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          orow_ptr[2 * lane + e] =
+              f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(bf16_to_f32(gh[e])));
+      }
     }
   }
 
@@ -908,8 +935,161 @@ void gdn_prefill_kernel(const DecodeParams args) {
     char* dst_tile = reinterpret_cast<char*>(p.state + static_cast<int64_t>(slot) * p.state_slot +
                                              head_offset);
 #pragma unroll
-    for (int j = 0; j < kPieces; ++j)
+    for (int j = 0; j < kTilePieces; ++j)
       *reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j))) = s[j];
+  }
+}
+
+// Prefill with a head's rows split over 4 / Chunks workgroups (Chunks = 1 or 2): for a few
+// prompts, where one workgroup per (sequence, head) leaves most of the GPU idle and every
+// token's latency chain is exposed.  Same arithmetic as gdn_prefill_kernel; the loop is
+// arranged for latency: token inputs are prefetched kDepth tokens ahead, token t + 1 is
+// staged (norms, gates) while token t's rows update, and every lane loads the v values of
+// its own rows directly.  Raw outputs go to `out` for prefill_norm_kernel.
+template <bool DtBf16, bool WBf16, int Chunks>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4)))
+void gdn_prefill_rows_kernel(const DecodeParams args) {
+  static_assert(Chunks == 1 || Chunks == 2, "8 or 16 rows per wave");
+  constexpr int kBlocks = 4 / Chunks;
+  constexpr int kWaveRows = 8 * Chunks;
+  constexpr int kTilePieces = 4 * Chunks;
+  constexpr int kDepth = 3;  // tokens in flight ahead of the one being stepped
+  const DecodeParams& p = args;
+  const int tile = blockIdx.x;
+  const int sequence = tile / (p.num_v_heads * kBlocks);
+  const int rest = tile - sequence * p.num_v_heads * kBlocks;
+  const int head = rest / kBlocks;
+  const int block = rest - head * kBlocks;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int bos = p.cu[sequence];
+  const int eos = p.cu[sequence + 1];
+  const int slot = p.indices[sequence];
+  const bool from_slot = slot > 0 && p.has_initial[sequence] != 0;
+
+  const int key_head = head / p.group;
+  const int kq = lane & 15;
+  const int rsub = lane >> 4;
+  const int wave_row0 = block * kWaves * kWaveRows + wave * kWaveRows;
+  const int row_base = wave_row0 + rsub;
+  const int q_col = key_head * kDim;
+  const int k_col = (p.num_k_heads + key_head) * kDim;
+  const int v_col = (2 * p.num_k_heads + head) * kDim;
+
+  __shared__ float s_o[kWaves][kWaveRows];
+
+  const float dt_bias = load_param(p.dt_bias, head, DtBf16);
+  const float a_log = p.a_log[head];
+  const int64_t head_offset = static_cast<int64_t>(head) * kDim * kDim;
+  const uint32_t lane_bytes = static_cast<uint32_t>(row_base * kDim + kq * 4) * 4u;
+  f32x4 s[kTilePieces];
+  if (from_slot) {
+    const char* src_tile = reinterpret_cast<const char*>(
+        p.state + static_cast<int64_t>(slot) * p.state_slot + head_offset);
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j)
+      s[j] = *reinterpret_cast<const f32x4*>(src_tile + (lane_bytes + tile_piece_bytes(j)));
+  } else {
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j) s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  // A token's inputs: q/k/a/b as load_token lays them out, and v of the lane's 2 * Chunks rows
+  // (rows row_base + 4 i, i < 2 * Chunks).  Tokens past the sequence's end load its last one.
+  struct Pending {
+    TokenIn in;
+    uint16_t v[2 * Chunks];
+  };
+  auto fetch = [&](int t) {
+    Pending f;
+    const int64_t token = min(t, eos - 1);
+    f.in = load_token(p, token, q_col, k_col, v_col + row_base, head, kq);
+    const uint16_t* vrow = p.qkv + token * p.qkv_row + v_col + row_base;
+#pragma unroll
+    for (int i = 0; i < 2 * Chunks; ++i) f.v[i] = vrow[4 * i];
+    return f;
+  };
+  if (bos >= eos) {  // empty sequence: the initial state goes back to the slot
+    if (slot > 0) {
+      char* dst_tile = reinterpret_cast<char*>(p.state + static_cast<int64_t>(slot) * p.state_slot +
+                                               head_offset);
+#pragma unroll
+      for (int j = 0; j < kTilePieces; ++j)
+        *reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j))) = s[j];
+    }
+    return;
+  }
+  Pending pf[kDepth];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) pf[d] = fetch(bos + 1 + d);
+  Pending cur = fetch(bos);
+  Staged x = stage_token(cur.in, a_log, dt_bias, p.scale);
+  for (int t = bos; t < eos; ++t) {
+    float vv[2 * Chunks];
+#pragma unroll
+    for (int i = 0; i < 2 * Chunks; ++i) vv[i] = bf16_to_f32(cur.v[i]);
+    const Staged now = x;
+    // next token: stage it now (its inputs arrived kDepth tokens ago) and refill the queue
+    cur = pf[0];
+#pragma unroll
+    for (int d = 0; d + 1 < kDepth; ++d) pf[d] = pf[d + 1];
+    pf[kDepth - 1] = fetch(t + 1 + kDepth);
+    x = stage_token(cur.in, a_log, dt_bias, p.scale);
+    Vectors vec;
+    vec.q0 = now.q0;
+    vec.q1 = now.q1;
+    vec.k0 = now.k0;
+    vec.k1 = now.k1;
+    float* o = s_o[wave];
+    chunk_step<0, false, false, kTilePieces>(s, vec, vv[0], vv[1], o, now.decay, now.beta, kq,
+                                             rsub, nullptr, lane_bytes);
+    if constexpr (Chunks == 2)
+      chunk_step<1, false, false, kTilePieces>(s, vec, vv[2], vv[3], o, now.decay, now.beta, kq,
+                                               rsub + 8, nullptr, lane_bytes);
+    // s_o is read back by other lanes of this wave: a wave's LDS operations run in program
+    // order, so only the compiler must not reorder them.
+    asm volatile("" ::: "memory");
+    if (lane < kWaveRows)
+      p.out[(static_cast<int64_t>(t) * p.num_v_heads + head) * kDim + wave_row0 + lane] =
+          f32_to_bf16(s_o[wave][lane]);
+    asm volatile("" ::: "memory");
+  }
+  if (slot > 0) {
+    char* dst_tile = reinterpret_cast<char*>(p.state + static_cast<int64_t>(slot) * p.state_slot +
+                                             head_offset);
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j)
+      *reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j))) = s[j];
+  }
+}
+
+// The gated RMSNorm of prefill rows whose raw outputs (bf16) are already in `out`, in place:
+// one wave per (token, head) over rows cu[0] .. cu[num_sequences] - 1, with the arithmetic
+// of gdn_prefill_kernel's epilogue.
+template <bool WBf16>
+__global__ __launch_bounds__(kThreads) void prefill_norm_kernel(const DecodeParams p,
+                                                                int num_sequences) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int64_t token = item / p.num_v_heads;
+  const int head = static_cast<int>(item - token * p.num_v_heads);
+  if (token < p.cu[0] || token >= p.cu[num_sequences]) return;
+  uint16_t* row = p.out + (token * p.num_v_heads + head) * kDim;
+  const uint16_t* grow = p.gate + token * p.gate_row + head * kDim;
+  float raw[2];
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    raw[e] = bf16_to_f32(row[2 * lane + e]);
+    ss = fmaf(raw[e], raw[e], ss);
+  }
+  ss = wave_sum(ss);
+  const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const float w = load_param(p.norm_weight, 2 * lane + e, WBf16);
+    row[2 * lane + e] = f32_to_bf16(((raw[e] * rstd) * w) * silu(bf16_to_f32(grow[2 * lane + e])));
   }
 }
 
@@ -1077,8 +1257,10 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
     return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_prefill: NULL tensor pointer");
   if (!aligned16(a.state) || (a.state_slot_stride & 3) != 0)
     return fail(LD_ERR_INVALID_ARGUMENT, "state slots must be 16-byte aligned");
+  if (a.num_tokens < 0) return fail(LD_ERR_INVALID_ARGUMENT, "num_tokens must be >= 0");
   const int64_t blocks = static_cast<int64_t>(a.num_sequences) * a.num_v_heads;
-  if (blocks > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "too many (sequence, head) tiles");
+  if (blocks * 4 > 0x7fffffff || a.num_tokens * static_cast<int64_t>(a.num_v_heads) > 0x1ffffffffLL)
+    return fail(LD_ERR_INVALID_ARGUMENT, "too many (sequence, head) tiles");
   DecodeParams p{};
   p.qkv = static_cast<const uint16_t*>(a.qkv);
   p.qkv_row = a.qkv_row_stride;
@@ -1105,9 +1287,44 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
   p.eps = a.eps;
   const bool dt_bf16 = a.dt_bias_dtype == LD_DTYPE_BF16;
   const bool w_bf16 = a.norm_weight_dtype == LD_DTYPE_BF16;
-  auto kernel = dt_bf16 ? (w_bf16 ? gdn_prefill_kernel<true, true> : gdn_prefill_kernel<true, false>)
-                        : (w_bf16 ? gdn_prefill_kernel<false, true> : gdn_prefill_kernel<false, false>);
-  hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), p);
+  // Split a head's rows over more workgroups when (sequence, head) tiles alone would leave
+  // the GPU short of work (1024 tiles fill 256 CUs at 4 per CU).
+  const int64_t tiles = blocks;
+  const int chunks = tiles >= 256 ? 4 : (tiles >= 128 ? 2 : 1);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t grid = static_cast<uint32_t>(tiles * (4 / chunks));
+#define LD_PREFILL_LAUNCH(C)                                                                 \
+  hipLaunchKernelGGL(dt_bf16 ? (w_bf16 ? gdn_prefill_kernel<true, true, C>                   \
+                                       : gdn_prefill_kernel<true, false, C>)                 \
+                             : (w_bf16 ? gdn_prefill_kernel<false, true, C>                  \
+                                       : gdn_prefill_kernel<false, false, C>),               \
+                     dim3(grid), dim3(kThreads), 0, s, p)
+#define LD_PREFILL_ROWS_LAUNCH(C)                                                            \
+  hipLaunchKernelGGL(dt_bf16 ? (w_bf16 ? gdn_prefill_rows_kernel<true, true, C>              \
+                                       : gdn_prefill_rows_kernel<true, false, C>)            \
+                             : (w_bf16 ? gdn_prefill_rows_kernel<false, true, C>             \
+                                       : gdn_prefill_rows_kernel<false, false, C>),          \
+                     dim3(grid), dim3(kThreads), 0, s, p)
+  if (chunks == 4) {
+    LD_PREFILL_LAUNCH(4);
+  } else {
+    if (chunks == 2)
+      LD_PREFILL_ROWS_LAUNCH(2);
+    else
+      LD_PREFILL_ROWS_LAUNCH(1);
+    if (check_launch("ld_gdn_prefill") != LD_OK) return LD_ERR_LAUNCH;
+    const int64_t items = a.num_tokens * static_cast<int64_t>(a.num_v_heads);
+    if (items > 0) {
+      const uint32_t norm_grid = static_cast<uint32_t>((items + kWaves - 1) / kWaves);
+      if (w_bf16)
+        hipLaunchKernelGGL(prefill_norm_kernel<true>, dim3(norm_grid), dim3(kThreads), 0, s, p,
+                           a.num_sequences);
+      else
+        hipLaunchKernelGGL(prefill_norm_kernel<false>, dim3(norm_grid), dim3(kThreads), 0, s, p,
+                           a.num_sequences);
+    }
+  }
+#undef LD_PREFILL_LAUNCH
+#undef LD_PREFILL_ROWS_LAUNCH
   return check_launch("ld_gdn_prefill");
 }

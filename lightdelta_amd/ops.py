@@ -245,7 +245,7 @@ def _prefill_impl(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, sta
         a_log.data_ptr(), dt_bias.data_ptr(), _dtype_code(dt_bias), _dtype_code(weight),
         slots.data_ptr(), has_initial.data_ptr(), cu_seqlens.data_ptr(), state.data_ptr(),
         state.stride(0), gate.data_ptr(), gate.stride(0), weight.data_ptr(), out.data_ptr(),
-        slots.numel(), h, hv, QK_SCALE, eps,
+        qkv.shape[0], slots.numel(), h, hv, QK_SCALE, eps,
     )
     lib = _lib.load()
     with _DeviceGuard(qkv.device):

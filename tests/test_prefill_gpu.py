@@ -140,3 +140,34 @@ def test_prefill_graph_capture(gpu):
         torch.cuda.synchronize()
         assert_bf16_outputs(case["out"], exp_out, pre, label=f"replay {replay}")
         assert_states(case["pool"], exp_pool, label=f"replay {replay}")
+
+
+@pytest.mark.parametrize("sequences", [16, 32])
+def test_split_and_fused_paths_agree(gpu, sequences):
+    """32 sequences x 32 heads fill the GPU (one workgroup per head, fused norm); 16 split each
+    head's rows in two; one sequence alone splits them in four with the norm as a second
+    launch.  All must give the same bits, and match the oracle."""
+    announce(test="prefill_paths", sequences=sequences)
+    gen = torch.Generator().manual_seed(sequences)
+    lengths = torch.randint(0, 24, (sequences,), generator=gen).tolist()
+    case = prefill_case(gpu, lengths, seed=sequences, pool_slots=sequences + 2)
+    case["has_initial"][::3] = False
+    exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6, return_pre=True)
+    pool0 = case["pool"].clone()
+    run(case)
+    torch.cuda.synchronize()
+    assert_bf16_outputs(case["out"], exp_out, pre)
+    assert_states(case["pool"], exp_pool)
+    batch_out, batch_pool = case["out"].clone(), case["pool"].clone()
+    case["pool"].copy_(pool0)
+    case["out"].zero_()
+    cu = case["cu_seqlens"]
+    for n in range(sequences):
+        one = dict(case)
+        one["slots"] = case["slots"][n:n + 1]
+        one["has_initial"] = case["has_initial"][n:n + 1]
+        one["cu_seqlens"] = cu[n:n + 2]
+        run(one)
+    torch.cuda.synchronize()
+    assert torch.equal(case["out"], batch_out)
+    assert torch.equal(case["pool"], batch_pool)
