@@ -81,8 +81,8 @@ constexpr int kMaxConvLen = 8;
 constexpr int kMaxConvTickets = 1 << 20;
 __device__ uint32_t g_conv_ticket[kMaxConvTickets];
 
-// Stream policy: destination of the state of an MTP token that has no slot to go to (past
-// the request's last token, or a padding slot): one tile that is written and never read.
+// Destination of the state of an MTP token that has no slot to go to (past the request's last
+// token, or a padding slot) under non-temporal stores: one tile, written and never read.
 __device__ __align__(256) f32x4 g_state_sink[kDim * kDim / 4];
 
 __device__ __forceinline__ float load_param(const void* p, int i, bool bf16) {
@@ -430,6 +430,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))
 void gdn_decode_kernel(const DecodeParams args) {
   constexpr bool Conv = ConvCols > 0;
   constexpr int kCols = Conv ? ConvCols : 1;
+  // Cache hints of the state traffic.  One token: the policy's (plain loads and stores keep
+  // a layer's state in the Infinity Cache between steps; non-temporal ones stream it).
+  // Several tokens (verify): the writes are 4 times the reads, and plain loads with
+  // non-temporal stores measured fastest under either policy (B=64, T=4: 103 us against
+  // 134-139 us with both hints alike), the stores being unconditional (sink tile) so that
+  // load waits stay exact.
+  constexpr bool kLoadNT = Stream && Width == 1;
+  constexpr bool kStoreNT = Stream || Width > 1;
   // The conv runs before the tile loads for several tokens or more than 4 state columns;
   // one token with 3..4 columns keeps it in registers while the tile streams in.
   constexpr bool kConvFirst = Conv && (Width > 1 || kCols > 4);
@@ -597,7 +605,7 @@ void gdn_decode_kernel(const DecodeParams args) {
   }
   // Every MTP token slot t < W is staged and stepped, past the request's last token too
   // (with a copy of that token), so the token loops have no branches; such tokens' states
-  // go to the sink tile (stream policy) or are not stored (keep), and their outputs are not
+  // go to the sink tile (non-temporal stores) or are not stored, and their outputs are not
   // written.
   const bool stages_mtp = Width > 1 && wave >= 1 && wave < Width;
   const int64_t token_w = bos + min(wave, num_tokens - 1);
@@ -639,7 +647,7 @@ void gdn_decode_kernel(const DecodeParams args) {
   for (int j = 0; j < kPieces; ++j) {
     const f32x4* src =
         reinterpret_cast<const f32x4*>(src_tile + (lane_bytes + tile_piece_bytes(j)));
-    s[j] = Stream ? __builtin_nontemporal_load(src) : *src;
+    s[j] = kLoadNT ? __builtin_nontemporal_load(src) : *src;
     __builtin_amdgcn_sched_barrier(0);  // keep program order: chunk c's loads issue first
   }
 
@@ -727,18 +735,18 @@ void gdn_decode_kernel(const DecodeParams args) {
 #pragma unroll
   for (int t = 0; t < Width; ++t)
     dst[t] = (t < num_tokens && slot[t] > 0) ? state_bytes + slot[t] * slot_bytes
-             : Stream                         ? reinterpret_cast<char*>(g_state_sink)
+             : kStoreNT                       ? reinterpret_cast<char*>(g_state_sink)
                                               : nullptr;
 
 #define LD_CHUNK(C)                                                                         \
   {                                                                                         \
     const int r = row_base + 8 * (C);                                                       \
-    chunk_step<C, Stream>(s, load_vectors(s_qk0[wave], kq), s_v0[wave][8 * (C) + rsub],     \
+    chunk_step<C, kStoreNT>(s, load_vectors(s_qk0[wave], kq), s_v0[wave][8 * (C) + rsub],     \
                           s_v0[wave][8 * (C) + 4 + rsub], s_o[0], s_db0[wave][0],           \
                           s_db0[wave][1], kq, r, dst[0], lane_bytes);                       \
     if ((C) == 0 && Width > 1) lds_barrier();                                               \
     _Pragma("unroll") for (int t = 1; t < Width; ++t) {                                     \
-      chunk_step<C, Stream>(s, load_vectors(s_qkt[t], kq), s_vt[t][r], s_vt[t][r + 4],      \
+      chunk_step<C, kStoreNT>(s, load_vectors(s_qkt[t], kq), s_vt[t][r], s_vt[t][r + 4],      \
                             s_o[t], s_dbt[t][0], s_dbt[t][1], kq, r, dst[t], lane_bytes);   \
     }                                                                                       \
   }
