@@ -32,9 +32,28 @@ struct CopyParams {
   uint32_t chunks;        // chunks per row
 };
 
-// One workgroup moves one 16 KiB chunk of one row: 4 non-temporal 128-bit loads per thread
-// in flight, then 4 stores (the data is touched once, so it bypasses cache allocation).
-// Every branch below is uniform over the workgroup.
+// Cache hints: the pool side (rows at random slots, touched once) is non-temporal; the
+// packed side of gather / scatter is a buffer the next kernel reads or the previous one
+// wrote, so it stays cacheable.  Slot-to-slot copies read plainly and write non-temporally.
+// Measured on 128 rows of 2 MiB against non-temporal on both sides: gather 86 -> 78 us,
+// scatter 92-94 -> 77 us, copy 92 -> 76 us with the same pairs repeated (95 us when they
+// rotate through the pool, as before).
+template <int M>
+__device__ __forceinline__ u32x4 load_row(const u32x4* src) {
+  if constexpr (M == kGather) return __builtin_nontemporal_load(src);
+  return *src;
+}
+
+template <int M>
+__device__ __forceinline__ void store_row(u32x4 v, u32x4* dst) {
+  if constexpr (M == kGather)
+    *dst = v;
+  else
+    __builtin_nontemporal_store(v, dst);
+}
+
+// One workgroup moves one 16 KiB chunk of one row: 4 128-bit loads per thread in flight,
+// then 4 stores.  Every branch below is uniform over the workgroup.
 template <int M>
 __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p) {
   const uint32_t block = blockIdx.x;
@@ -74,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i) {
       const int64_t idx = first + i * kThreads;
-      if (idx < p.vecs) __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, dst + idx);
+      if (idx < p.vecs) store_row<M>(u32x4{0u, 0u, 0u, 0u}, dst + idx);
     }
     return;
   }
@@ -82,22 +101,22 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
   if (begin + kVecsPerChunk <= p.vecs) {  // whole chunk: unguarded, all loads in flight
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i)
-      v[i] = __builtin_nontemporal_load(src + first + i * kThreads);
+      v[i] = load_row<M>(src + first + i * kThreads);
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i)
-      __builtin_nontemporal_store(v[i], dst + first + i * kThreads);
+      store_row<M>(v[i], dst + first + i * kThreads);
     return;
   }
   // tail chunk of a row
 #pragma unroll
   for (int i = 0; i < kVecsPerThread; ++i) {
     const int64_t idx = first + i * kThreads;
-    v[i] = __builtin_nontemporal_load(src + (idx < p.vecs ? idx : 0));
+    v[i] = load_row<M>(src + (idx < p.vecs ? idx : 0));
   }
 #pragma unroll
   for (int i = 0; i < kVecsPerThread; ++i) {
     const int64_t idx = first + i * kThreads;
-    if (idx < p.vecs) __builtin_nontemporal_store(v[i], dst + idx);
+    if (idx < p.vecs) store_row<M>(v[i], dst + idx);
   }
 }
 
