@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 6
+#define LD_ABI_VERSION 7
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -153,9 +153,12 @@ int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_args* conv,
  * state[slots[n]] when slots[n] > 0 (an empty sequence writes its initial state back).
  * Layouts as ld_gdn_decode (qkv, a, b, gate, out row strides; state [slots, HV, 128,
  * 128]); has_initial is one byte per sequence; cu_seqlens is trusted device metadata
- * (non-decreasing, sequences contiguous from cu_seqlens[0]).  When sequences x heads are
- * too few to fill the GPU, a head's state rows are split over several workgroups and the
- * norm runs as a second launch on the same stream (same results).
+ * (non-decreasing, sequences contiguous from cu_seqlens[0]).  Two algorithms with the same
+ * contract: token-serial (the decode's arithmetic, token by token; a head's state rows are
+ * split over several workgroups when sequences x heads are too few to fill the GPU) and
+ * chunked (64-token chunks in the WY form; faster for few long prompts; results within
+ * rounding of the token-serial ones).  Either may run the norm as a second launch on the
+ * same stream.
  * Replaces the reference's prefill composition (python/lightdelta/integration/
  * vllm_layer.py:93-135: fused_post_conv_prep, gather_state with has_initial_state,
  * chunk_gated_delta_rule, scatter_state, gated RMSNorm) in one launch.
@@ -186,9 +189,24 @@ typedef struct ld_gdn_prefill_args {
   int32_t num_v_heads;
   float scale;
   float eps;
+  int32_t algorithm;       /* LD_PREFILL_AUTO / _TOKEN_SERIAL / _CHUNKED */
+  void* workspace;         /* device memory for the chunked form (NULL: not used) */
+  int64_t workspace_bytes;
 } ld_gdn_prefill_args;
 
+#define LD_PREFILL_AUTO 0         /* chunked when sequences x heads < 256 and the workspace fits */
+#define LD_PREFILL_TOKEN_SERIAL 1 /* the decode recurrence token by token */
+#define LD_PREFILL_CHUNKED 2      /* chunks of 64 tokens in the WY form (needs the workspace) */
+
 int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream);
+
+/*
+ * Workspace bytes the chunked prefill needs for num_tokens rows in num_sequences sequences
+ * and num_v_heads heads (240 KiB per chunk of 64 tokens and head, chunks bounded by
+ * num_tokens / 64 + num_sequences).
+ */
+int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t num_sequences,
+                                       int32_t num_v_heads);
 
 /*
  * Gather pool rows into a packed buffer:

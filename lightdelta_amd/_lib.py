@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must precede the CDLL load (see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("liblightdelta_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 CACHE_KEEP = 0
@@ -110,13 +110,20 @@ class PrefillArgs(ctypes.Structure):
         ("num_v_heads", _c_i32),
         ("scale", ctypes.c_float),
         ("eps", ctypes.c_float),
+        ("algorithm", _c_i32),
+        ("workspace", _vp),
+        ("workspace_bytes", _c_i64),
     ]
+
+
+PREFILL_AUTO, PREFILL_TOKEN_SERIAL, PREFILL_CHUNKED = 0, 1, 2
 
 
 # Exported entry points and their C signatures (argtypes, restype).
 SIGNATURES = {
     "ld_gdn_decode": ([ctypes.POINTER(DecodeArgs), _vp], ctypes.c_int),
     "ld_gdn_prefill": ([ctypes.POINTER(PrefillArgs), _vp], ctypes.c_int),
+    "ld_gdn_prefill_workspace_bytes": ([_c_i64, _c_i32, _c_i32], _c_i64),
     "ld_gdn_decode_conv": (
         [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ConvArgs), _vp],
         ctypes.c_int,

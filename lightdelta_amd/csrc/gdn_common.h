@@ -1,0 +1,89 @@
+// Device-side definitions shared by the decode / verify / prefill kernels (gdn_decode.hip)
+// and the chunked prefill (prefill_chunked.hip): the tile geometry, the kernel parameters,
+// and the per-token scalar math.
+#pragma once
+
+#include "common.h"
+
+namespace ld {
+
+constexpr int kDim = LD_HEAD_DIM;
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kRowsPerWave = 32;
+constexpr int kPieces = 16;        // 16-byte pieces of the tile per lane
+constexpr int kMaxTokens = LD_MAX_TOKENS;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct DecodeParams {
+  const uint16_t* qkv;
+  int64_t qkv_row;
+  const uint16_t* a;
+  int64_t a_row;
+  const uint16_t* b;
+  int64_t b_row;
+  const float* a_log;
+  const void* dt_bias;
+  const int32_t* indices;
+  const int32_t* cu;
+  const int32_t* accepted;
+  const uint8_t* has_initial;  // prefill only: per sequence, 0 = start from a zero state
+  float* state;
+  int64_t state_slot;
+  const uint16_t* gate;
+  int64_t gate_row;
+  const void* norm_weight;
+  uint16_t* out;
+  int32_t width;
+  int32_t num_k_heads;
+  int32_t num_v_heads;
+  int32_t group;  // num_v_heads / num_k_heads
+  float scale;
+  float eps;
+  // Conv-fused variant only (pre-conv activations and the conv-state pool).
+  const uint16_t* conv_x;
+  int64_t conv_x_row;
+  uint16_t* conv_state;
+  int64_t conv_slot;
+  int64_t conv_dim_stride;
+  int64_t conv_len_stride;
+  int32_t conv_len;
+  const uint16_t* conv_weight;  // [conv_dim, 4]
+  const uint16_t* conv_bias;    // [conv_dim] or NULL
+};
+
+__device__ __forceinline__ float load_param(const void* p, int i, bool bf16) {
+  return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i])
+              : static_cast<const float*>(p)[i];
+}
+
+// The per-token scalars and norms below use the hardware approximations (v_exp_f32,
+// v_log_f32, v_rcp_f32, v_rsq_f32; about 1 ulp): they sit between the arrival of the data
+// and the first state update of every wave, where exactly rounded sequences cost ~1 us per
+// step, and their error (~1e-7 relative) is four orders of magnitude below the bf16 output
+// resolution.
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
+
+__device__ __forceinline__ float sigmoid(float x) { return fast_rcp(1.0f + __expf(-x)); }
+
+__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
+
+// softplus with the threshold torch's F.softplus uses (beta=1, threshold=20); log1p(y) for
+// small y = e^x by its series, where log(1 + y) would lose y to the rounding of 1 + y.
+__device__ __forceinline__ float softplus(float x) {
+  if (x > 20.0f) return x;
+  const float y = __expf(x);
+  return y < 1e-4f ? y * (1.0f - 0.5f * y) : __logf(1.0f + y);
+}
+
+// Chunked prefill (prefill_chunked.hip): workspace bytes for num_tokens rows in
+// num_sequences sequences and num_v_heads heads, and the launch of its three phases; the
+// raw outputs go to p.out for prefill_norm_kernel.
+int64_t prefill_chunked_workspace_bytes(int64_t num_tokens, int64_t num_sequences,
+                                        int64_t num_v_heads);
+int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num_tokens,
+                           bool dt_bf16, void* workspace, hipStream_t stream);
+
+}  // namespace ld

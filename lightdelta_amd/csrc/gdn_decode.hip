@@ -24,56 +24,10 @@
 //     over the 16-lane row (quad_perm, row_half_mirror, row_mirror); every lane ends with
 //     the full sums, so no LDS round trip and no broadcast step is needed.
 //   * T <= 4 tokens (MTP verify) reuse the registers: 1 tile read, T tile writes.
-#include "common.h"
+#include "gdn_common.h"
 
 namespace ld {
 namespace {
-
-constexpr int kDim = LD_HEAD_DIM;
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
-constexpr int kRowsPerWave = 32;
-constexpr int kPieces = 16;        // 16-byte pieces of the tile per lane
-constexpr int kMaxTokens = LD_MAX_TOKENS;
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-struct DecodeParams {
-  const uint16_t* qkv;
-  int64_t qkv_row;
-  const uint16_t* a;
-  int64_t a_row;
-  const uint16_t* b;
-  int64_t b_row;
-  const float* a_log;
-  const void* dt_bias;
-  const int32_t* indices;
-  const int32_t* cu;
-  const int32_t* accepted;
-  const uint8_t* has_initial;  // prefill only: per sequence, 0 = start from a zero state
-  float* state;
-  int64_t state_slot;
-  const uint16_t* gate;
-  int64_t gate_row;
-  const void* norm_weight;
-  uint16_t* out;
-  int32_t width;
-  int32_t num_k_heads;
-  int32_t num_v_heads;
-  int32_t group;  // num_v_heads / num_k_heads
-  float scale;
-  float eps;
-  // Conv-fused variant only (pre-conv activations and the conv-state pool).
-  const uint16_t* conv_x;
-  int64_t conv_x_row;
-  uint16_t* conv_state;
-  int64_t conv_slot;
-  int64_t conv_dim_stride;
-  int64_t conv_len_stride;
-  int32_t conv_len;
-  const uint16_t* conv_weight;  // [conv_dim, 4]
-  const uint16_t* conv_bias;    // [conv_dim] or NULL
-};
 
 constexpr int kConvWidth = 4;
 constexpr int kMaxConvLen = 8;
@@ -84,31 +38,6 @@ __device__ uint32_t g_conv_ticket[kMaxConvTickets];
 // Destination of the state of an MTP token that has no slot to go to (past the request's last
 // token, or a padding slot) under non-temporal stores: one tile, written and never read.
 __device__ __align__(256) f32x4 g_state_sink[kDim * kDim / 4];
-
-__device__ __forceinline__ float load_param(const void* p, int i, bool bf16) {
-  return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i])
-              : static_cast<const float*>(p)[i];
-}
-
-// The per-token scalars and norms below use the hardware approximations (v_exp_f32,
-// v_log_f32, v_rcp_f32, v_rsq_f32; about 1 ulp): they sit between the arrival of the data
-// and the first state update of every wave, where exactly rounded sequences cost ~1 us per
-// step, and their error (~1e-7 relative) is four orders of magnitude below the bf16 output
-// resolution.
-__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
-__device__ __forceinline__ float fast_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
-
-__device__ __forceinline__ float sigmoid(float x) { return fast_rcp(1.0f + __expf(-x)); }
-
-__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
-
-// softplus with the threshold torch's F.softplus uses (beta=1, threshold=20); log1p(y) for
-// small y = e^x by its series, where log(1 + y) would lose y to the rounding of 1 + y.
-__device__ __forceinline__ float softplus(float x) {
-  if (x > 20.0f) return x;
-  const float y = __expf(x);
-  return y < 1e-4f ? y * (1.0f - 0.5f * y) : __logf(1.0f + y);
-}
 
 // Sums over the 16 lanes of a DPP row; every lane of the row receives the totals.
 __device__ __forceinline__ void row_sum2(float& x, float& y) {
@@ -1253,6 +1182,8 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
   if (args == nullptr) return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_prefill: args is NULL");
   const ld_gdn_prefill_args& a = *args;
   if (a.num_sequences < 0) return fail(LD_ERR_INVALID_ARGUMENT, "num_sequences must be >= 0");
+  if (a.algorithm < LD_PREFILL_AUTO || a.algorithm > LD_PREFILL_CHUNKED)
+    return fail(LD_ERR_INVALID_ARGUMENT, "unknown prefill algorithm");
   if (a.num_k_heads <= 0 || a.num_v_heads <= 0 || a.num_v_heads % a.num_k_heads != 0)
     return fail(LD_ERR_INVALID_ARGUMENT, "num_v_heads must be a positive multiple of num_k_heads");
   if (!(a.eps > 0.0f)) return fail(LD_ERR_INVALID_ARGUMENT, "norm epsilon must be positive");
@@ -1295,12 +1226,24 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
   p.eps = a.eps;
   const bool dt_bf16 = a.dt_bias_dtype == LD_DTYPE_BF16;
   const bool w_bf16 = a.norm_weight_dtype == LD_DTYPE_BF16;
-  // Split a head's rows over more workgroups when (sequence, head) tiles alone would leave
-  // the GPU short of work (1024 tiles fill 256 CUs at 4 per CU).
-  const int64_t tiles = blocks;
-  const int chunks = tiles >= 256 ? 4 : (tiles >= 128 ? 2 : 1);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const uint32_t grid = static_cast<uint32_t>(tiles * (4 / chunks));
+  const int64_t tiles = blocks;
+  const int64_t ws_need = prefill_chunked_workspace_bytes(a.num_tokens, a.num_sequences,
+                                                          a.num_v_heads);
+  const bool ws_fits = a.workspace != nullptr && a.workspace_bytes >= ws_need;
+  if (a.algorithm == LD_PREFILL_CHUNKED && !ws_fits)
+    return fail(LD_ERR_INVALID_ARGUMENT, "chunked prefill: workspace missing or too small");
+  const bool chunked = a.algorithm == LD_PREFILL_CHUNKED ||
+                       (a.algorithm == LD_PREFILL_AUTO && tiles < 256 && ws_fits);
+  if (chunked) {
+    const int rc = launch_prefill_chunked(p, a.num_sequences, a.num_tokens, dt_bf16,
+                                          a.workspace, s);
+    if (rc != LD_OK) return rc;
+  }
+  // Token-serial: split a head's rows over more workgroups when (sequence, head) tiles alone
+  // would leave the GPU short of work (1024 tiles fill 256 CUs at 4 per CU).
+  const int chunks = chunked ? 0 : (tiles >= 256 ? 4 : (tiles >= 128 ? 2 : 1));
+  const uint32_t grid = chunks > 0 ? static_cast<uint32_t>(tiles * (4 / chunks)) : 0u;
 #define LD_PREFILL_LAUNCH(C)                                                                 \
   hipLaunchKernelGGL(dt_bf16 ? (w_bf16 ? gdn_prefill_kernel<true, true, C>                   \
                                        : gdn_prefill_kernel<true, false, C>)                 \
@@ -1318,7 +1261,7 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
   } else {
     if (chunks == 2)
       LD_PREFILL_ROWS_LAUNCH(2);
-    else
+    else if (chunks == 1)
       LD_PREFILL_ROWS_LAUNCH(1);
     if (check_launch("ld_gdn_prefill") != LD_OK) return LD_ERR_LAUNCH;
     const int64_t items = a.num_tokens * static_cast<int64_t>(a.num_v_heads);
@@ -1335,4 +1278,10 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
 #undef LD_PREFILL_LAUNCH
 #undef LD_PREFILL_ROWS_LAUNCH
   return check_launch("ld_gdn_prefill");
+}
+
+extern "C" int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t num_sequences,
+                                                  int32_t num_v_heads) {
+  if (num_tokens < 0 || num_sequences < 0 || num_v_heads < 0) return 0;
+  return ld::prefill_chunked_workspace_bytes(num_tokens, num_sequences, num_v_heads);
 }

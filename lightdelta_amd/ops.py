@@ -234,20 +234,49 @@ def check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, sta
                         gate, weight, out, eps)
 
 
+# Prefill algorithm: "auto" runs 64-token chunks in the WY form when sequences x heads are
+# too few to fill the GPU (< 256), else the token-serial recurrence; "token_serial" and
+# "chunked" force one.  Results agree within rounding; the token-serial form reproduces the
+# decode kernel bit for bit.
+_PREFILL_ALGORITHMS = {"auto": _lib.PREFILL_AUTO, "token_serial": _lib.PREFILL_TOKEN_SERIAL,
+                       "chunked": _lib.PREFILL_CHUNKED}
+_prefill_algorithm = _lib.PREFILL_AUTO
+
+
+def set_prefill_algorithm(name: str) -> None:
+    global _prefill_algorithm
+    if name not in _PREFILL_ALGORITHMS:
+        raise ValueError(f"prefill algorithm must be one of {sorted(_PREFILL_ALGORITHMS)}")
+    _prefill_algorithm = _PREFILL_ALGORITHMS[name]
+
+
+def prefill_algorithm() -> str:
+    return next(k for k, v in _PREFILL_ALGORITHMS.items() if v == _prefill_algorithm)
+
+
 def _prefill_impl(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state, gate,
                   weight, out, eps):
     h, hv = check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state,
                           gate, weight, out, eps)
     if slots.numel() == 0:
         return
+    lib = _lib.load()
+    algorithm = _prefill_algorithm
+    chunked = algorithm == _lib.PREFILL_CHUNKED or (
+        algorithm == _lib.PREFILL_AUTO and slots.numel() * hv < 256)
+    workspace = None
+    if chunked:  # from the caching allocator (graph-capturable)
+        nbytes = lib.ld_gdn_prefill_workspace_bytes(qkv.shape[0], slots.numel(), hv)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=qkv.device)
     args = _lib.PrefillArgs(
         qkv.data_ptr(), qkv.stride(0), a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
         a_log.data_ptr(), dt_bias.data_ptr(), _dtype_code(dt_bias), _dtype_code(weight),
         slots.data_ptr(), has_initial.data_ptr(), cu_seqlens.data_ptr(), state.data_ptr(),
         state.stride(0), gate.data_ptr(), gate.stride(0), weight.data_ptr(), out.data_ptr(),
-        qkv.shape[0], slots.numel(), h, hv, QK_SCALE, eps,
+        qkv.shape[0], slots.numel(), h, hv, QK_SCALE, eps, algorithm,
+        0 if workspace is None else workspace.data_ptr(),
+        0 if workspace is None else workspace.numel(),
     )
-    lib = _lib.load()
     with _DeviceGuard(qkv.device):
         _lib.check(lib.ld_gdn_prefill(args, _stream(qkv.device)))
 

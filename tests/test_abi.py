@@ -22,7 +22,8 @@ def declared_functions() -> set[str]:
 
 def test_header_declares_the_entry_points():
     assert declared_functions() == {
-        "ld_gdn_decode", "ld_gdn_decode_conv", "ld_gdn_prefill", "ld_state_gather",
+        "ld_gdn_decode", "ld_gdn_decode_conv", "ld_gdn_prefill", "ld_gdn_prefill_workspace_bytes",
+        "ld_state_gather",
         "ld_state_scatter",
         "ld_state_copy", "ld_state_zero", "ld_last_error", "ld_abi_version",
     }
@@ -123,3 +124,17 @@ def test_prefill_rejects_bad_arguments_without_launching():
     assert "NULL tensor pointer" in lib.ld_last_error().decode()
     args.num_sequences = 0
     assert lib.ld_gdn_prefill(ctypes.byref(args), None) == 0
+
+
+def test_prefill_workspace_query_and_chunked_without_workspace():
+    lib = _lib.load()
+    one = lib.ld_gdn_prefill_workspace_bytes(4096, 1, 32)
+    assert one == (4096 // 64 + 1) * 32 * 61504 * 4
+    assert lib.ld_gdn_prefill_workspace_bytes(-1, 1, 32) == 0
+    args = _lib.PrefillArgs()
+    args.num_sequences, args.num_tokens = 1, 64
+    args.num_k_heads, args.num_v_heads = 16, 32
+    args.eps = 1e-6
+    args.algorithm = 7
+    assert lib.ld_gdn_prefill(ctypes.byref(args), None) == 1
+    assert "unknown prefill algorithm" in lib.ld_last_error().decode()

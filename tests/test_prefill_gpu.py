@@ -1,13 +1,15 @@
 """Parity of the gfx950 prefill (torch.ops.lightdelta.prefill) with the oracle's restatement
-of the layer's prefill (oracle/decode.py expected_prefill), and with the decode kernel:
-a prefill of n tokens must give bit for bit the states and outputs of n single-token
-decode steps on the same slot (the per-token arithmetic is shared)."""
+of the layer's prefill (oracle/decode.py expected_prefill), under both algorithms
+(token-serial, and 64-token chunks in the WY form); and, for the token-serial one, with the
+decode kernel: a prefill of n tokens must give bit for bit the states and outputs of n
+single-token decode steps on the same slot (the per-token arithmetic is shared)."""
 
 from __future__ import annotations
 
 import pytest
 import torch
 
+from lightdelta_amd import ops
 from lightdelta_amd.workloads import decode_case
 from oracle.decode import expected_prefill
 from tests.parity import assert_bf16_outputs, assert_states
@@ -47,9 +49,25 @@ def run(case, eps=1e-6):
     torch.ops.lightdelta.prefill(*[case[k] for k in PREFILL], eps)
 
 
+@pytest.fixture(params=["token_serial", "chunked"])
+def algorithm(request):
+    saved = ops.prefill_algorithm()
+    ops.set_prefill_algorithm(request.param)
+    yield request.param
+    ops.set_prefill_algorithm(saved)
+
+
+@pytest.fixture
+def token_serial():
+    saved = ops.prefill_algorithm()
+    ops.set_prefill_algorithm("token_serial")
+    yield
+    ops.set_prefill_algorithm(saved)
+
+
 @pytest.mark.parametrize("heads", [(16, 32), (4, 8), (16, 48)])
-def test_prefill_matches_oracle(gpu, heads):
-    announce(test="prefill_oracle", heads=heads)
+def test_prefill_matches_oracle(gpu, heads, algorithm):
+    announce(test="prefill_oracle", heads=heads, algorithm=algorithm)
     case = prefill_case(gpu, [5, 0, 1, 33, 70], heads=heads, seed=heads[1])
     case["has_initial"][3] = False  # starts from zeros
     case["slots"][2] = 0  # padding slot: zero initial state, final state dropped
@@ -64,8 +82,8 @@ def test_prefill_matches_oracle(gpu, heads):
 
 @pytest.mark.parametrize("dt_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("w_dtype", [torch.float32, torch.bfloat16])
-def test_prefill_parameter_dtypes(gpu, dt_dtype, w_dtype):
-    announce(test="prefill_dtypes", dt=dt_dtype, w=w_dtype)
+def test_prefill_parameter_dtypes(gpu, dt_dtype, w_dtype, algorithm):
+    announce(test="prefill_dtypes", dt=dt_dtype, w=w_dtype, algorithm=algorithm)
     case = prefill_case(gpu, [9, 17], seed=2, dt_dtype=dt_dtype, w_dtype=w_dtype)
     exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6, return_pre=True)
     run(case)
@@ -93,7 +111,7 @@ def decode_steps(case, eps=1e-6):
     return out, pool
 
 
-def test_prefill_equals_decode_steps_bit_for_bit(gpu):
+def test_prefill_equals_decode_steps_bit_for_bit(gpu, token_serial):
     announce(test="prefill_vs_decode")
     case = prefill_case(gpu, [3, 40, 1, 77], seed=5)
     case["has_initial"][1] = False
@@ -104,7 +122,7 @@ def test_prefill_equals_decode_steps_bit_for_bit(gpu):
     assert torch.equal(case["pool"], exp_pool)
 
 
-def test_long_prompt(gpu):
+def test_long_prompt(gpu, token_serial):
     """One 2048-token prompt at 16/32 heads: bit-exact against 2048 decode steps, and within
     the build's tolerance of the oracle's state after 2048 recurrent steps."""
     announce(test="prefill_long")
@@ -119,8 +137,8 @@ def test_long_prompt(gpu):
     torch.testing.assert_close(case["out"].float().cpu(), oracle_out.float(), atol=8e-3, rtol=2e-2)
 
 
-def test_prefill_graph_capture(gpu):
-    announce(test="prefill_graph")
+def test_prefill_graph_capture(gpu, algorithm):
+    announce(test="prefill_graph", algorithm=algorithm)
     case = prefill_case(gpu, [12, 30, 7], seed=8)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -143,7 +161,7 @@ def test_prefill_graph_capture(gpu):
 
 
 @pytest.mark.parametrize("sequences", [16, 32])
-def test_split_and_fused_paths_agree(gpu, sequences):
+def test_split_and_fused_paths_agree(gpu, sequences, token_serial):
     """32 sequences x 32 heads fill the GPU (one workgroup per head, fused norm); 16 split each
     head's rows in two; one sequence alone splits them in four with the norm as a second
     launch.  All must give the same bits, and match the oracle."""
@@ -171,3 +189,29 @@ def test_split_and_fused_paths_agree(gpu, sequences):
     torch.cuda.synchronize()
     assert torch.equal(case["out"], batch_out)
     assert torch.equal(case["pool"], batch_pool)
+
+
+def test_chunked_long_prompts_match_the_token_serial_form(gpu):
+    """Two prompts of 1000 and 3000 tokens (partial last chunks) under the chunked form:
+    within the build's tolerance of the token-serial results after thousands of steps."""
+    announce(test="prefill_chunked_long")
+    case = prefill_case(gpu, [1000, 3000], seed=11)
+    case["has_initial"][0] = False
+    pool0 = case["pool"].clone()
+    saved = ops.prefill_algorithm()
+    try:
+        ops.set_prefill_algorithm("token_serial")
+        run(case)
+        torch.cuda.synchronize()
+        ref_out, ref_pool = case["out"].clone(), case["pool"].clone()
+        case["pool"].copy_(pool0)
+        case["out"].zero_()
+        ops.set_prefill_algorithm("chunked")
+        run(case)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_prefill_algorithm(saved)
+    assert_states(case["pool"], ref_pool)
+    torch.testing.assert_close(case["out"].float(), ref_out.float(), atol=8e-3, rtol=2e-2)
+    close = ((case["out"].float() - ref_out.float()).abs() <= 2e-3 + 2e-3 * ref_out.float().abs())
+    assert close.float().mean() > 0.999
