@@ -1,5 +1,6 @@
-// Chunked prefill for gfx950: the delta rule over chunks of 64 tokens in the WY form, for
-// prompts too few to fill the GPU with one token-serial workgroup per (sequence, head).
+// Chunked prefill for gfx950: the delta rule over chunks of 64 tokens in the WY form, with
+// every product on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 operands, fp32
+// accumulation, so the arithmetic is the vector ALUs' up to summation order).
 //
 // Per chunk (tokens i = 0 .. n-1, n <= 64), with g_i the log decay, G_i = g_0 + .. + g_i,
 // Gam_ij = exp(G_i - G_j), beta_i, normalised q^_i (scaled) and k^_i, and S the state at
@@ -10,18 +11,22 @@
 //   O     = (q^_i exp(G_i)) S^T + P V_new,  P_ij = Gam_ij (q^_i . k^_j) for j <= i
 //   S'    = exp(G_{n-1}) S + V_new^T (k^_j exp(G_{n-1} - G_j))
 // which equals the token-by-token recurrence of the decode kernel (checked against it in
-// float64: 7e-8 relative on the state).  Three launches:
+// float64: 7e-8 relative on the state).  Two launches:
 //   chunk_prep_kernel  one workgroup per (chunk, v-head), all chunks in parallel: norms,
-//                      gates, A, the forward substitution for W and U, P, and the scaled
-//                      q and k; everything to a workspace record.
+//                      gates, A and P, the blocked forward substitution for W and U, and
+//                      the decayed q and k; everything to a workspace record.
 //   chunk_scan_kernel  one workgroup per (sequence, v-head, block of 16 state rows), the only
-//                      sequential part: chunk by chunk, V_new and the state update, saving
-//                      the state at each chunk's start; rows evolve independently, so a
+//                      sequential part: chunk by chunk, V_new, the raw outputs of its 16
+//                      columns (rounded to bf16 into `out`, the reference's rounding point
+//                      before the gated RMSNorm, which prefill_norm_kernel applies
+//                      afterwards) and the state update.  Rows evolve independently, so a
 //                      head's 128 rows spread over 8 workgroups.
-//   chunk_out_kernel   one workgroup per (chunk, v-head), in parallel: the raw outputs,
-//                      rounded to bf16 into `out` (the reference's rounding point before the
-//                      gated RMSNorm, which prefill_norm_kernel applies afterwards).
-// All arithmetic is fp32 on the vector ALUs, with operands staged in LDS.
+//
+// MFMA fragments (16 x 16 x 4, wave64): for lane l, li = l % 16 and lg = l / 16.  One
+// instruction takes a = A[li][kk = lg] and b = B[kk = lg][li] from every lane and adds
+// sum over kk of A[i][kk] B[kk][j] to D[i][j], held as d[r] = D[4 lg + r][li].  Summation
+// indices are assigned to (step, lg) freely as long as both operands agree; in the forward
+// substitution k = 4 lg + step, so a result's d[r] is directly the b operand of step r.
 #include "gdn_common.h"
 
 namespace ld {
@@ -31,16 +36,26 @@ constexpr int kC = 64;                          // tokens per chunk
 constexpr int kScanRows = 16;                   // state rows per scan workgroup
 constexpr int kScanBlocks = kDim / kScanRows;   // scan workgroups per (sequence, head)
 
-// Workspace record of one (chunk, v-head), offsets in floats.
-constexpr int64_t kOffWT = 0;                        // W^T   [128][64]
-constexpr int64_t kOffU = kOffWT + kDim * kC;        // U     [64][128]
-constexpr int64_t kOffQT = kOffU + kC * kDim;        // Qg^T  [128][64]  q^_i exp(G_i)
-constexpr int64_t kOffKd = kOffQT + kDim * kC;       // Kd    [64][128]  k^_j exp(G_n-1 - G_j)
-constexpr int64_t kOffPT = kOffKd + kC * kDim;       // P^T   [64][64]
-constexpr int64_t kOffVn = kOffPT + kC * kC;         // V_new [64][128]
-constexpr int64_t kOffH = kOffVn + kC * kDim;        // H     [128][128] state at chunk start
-constexpr int64_t kOffMisc = kOffH + kDim * kDim;    // [0] exp(G_n-1)
+// Workspace record of one (chunk, v-head), offsets in floats.  Every operand of the scan is
+// stored in the order its loads read it -- [scan wave or tile][step group q][lane][4] -- so
+// that one 16-byte-per-lane load of a wave reads 1 KiB of consecutive memory.  With li, lg
+// the lane's fragment coordinates:
+//   W   [w][q < 8][lane][e] = W[16 w + li][32 lg + 4 q + e]        (W: 64 token x 128 k)
+//   Qg  [w][q < 8][lane][e] = q^_i exp(G_i) at the same positions
+//   U   [b][w][lane][r]     = U[16 w + 4 lg + r][16 b + li]         (b: block of 16 v rows)
+//   Kd  [t][q < 4][lane][e] = k^_j exp(G_n-1 - G_j) for j = 16 lg + 4 q + e, k = 16 t + li
+//   P   [w][q < 4][lane][e] = P[16 w + li][16 lg + 4 q + e]
+constexpr int64_t kOffW = 0;
+constexpr int64_t kOffQg = kOffW + kC * kDim;
+constexpr int64_t kOffU = kOffQg + kC * kDim;
+constexpr int64_t kOffKd = kOffU + kDim * kC;
+constexpr int64_t kOffP = kOffKd + kDim * kC;
+constexpr int64_t kOffMisc = kOffP + kC * kC;        // [0] exp(G_n-1)
 constexpr int64_t kRecord = kOffMisc + 64;           // floats (a multiple of 64: 256 B)
+
+__device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 // Chunks of sequence n start at chunk_base(n) = sum over m < n of ceil(L_m / 64).
 __device__ int chunk_base(const int32_t* cu, int n) {
@@ -68,17 +83,25 @@ __device__ bool find_chunk(const int32_t* cu, int num_sequences, int g, int& seq
   return false;
 }
 
-__device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
-  float acc = a.x * b.x;
-  acc = fmaf(a.y, b.y, acc);
-  acc = fmaf(a.z, b.z, acc);
-  return fmaf(a.w, b.w, acc);
+// The 20 tiles of A (K K^T) and P (Q K^T) on or below the diagonal, five per wave: 5 bits
+// each, (is_p << 4) | (row tile << 2) | column tile.
+constexpr uint32_t tile_code(int is_p, int mt, int nt) { return (is_p << 4) | (mt << 2) | nt; }
+constexpr uint32_t tiles5(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t e) {
+  return a | (b << 5) | (c << 10) | (d << 15) | (e << 20);
 }
+constexpr uint32_t kTiles0 = tiles5(tile_code(0, 0, 0), tile_code(1, 0, 0), tile_code(0, 3, 0),
+                                    tile_code(1, 3, 0), tile_code(0, 3, 1));
+constexpr uint32_t kTiles1 = tiles5(tile_code(0, 1, 0), tile_code(0, 1, 1), tile_code(1, 1, 0),
+                                    tile_code(1, 1, 1), tile_code(1, 3, 1));
+constexpr uint32_t kTiles2 = tiles5(tile_code(0, 2, 0), tile_code(0, 2, 1), tile_code(0, 2, 2),
+                                    tile_code(1, 2, 0), tile_code(1, 2, 1));
+constexpr uint32_t kTiles3 = tiles5(tile_code(1, 2, 2), tile_code(0, 3, 2), tile_code(0, 3, 3),
+                                    tile_code(1, 3, 2), tile_code(1, 3, 3));
 
 // ---- phase 1: per (chunk, v-head) ----------------------------------------------------
 template <bool DtBf16>
-__global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const DecodeParams p,
-                                                              int num_sequences, float* ws) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws) {
   const int head = blockIdx.y;
   int seq = 0, t0 = 0, len = 0;
   if (!find_chunk(p.cu, num_sequences, blockIdx.x, seq, t0, len)) return;
@@ -86,20 +109,29 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const DecodeParams
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
   const int key_head = head / p.group;
   const int q_col = key_head * kDim;
   const int k_col = (p.num_k_heads + key_head) * kDim;
   const int v_col = (2 * p.num_k_heads + head) * kDim;
 
-  constexpr int kRow = kDim + 4;   // padded LDS row (floats) of q^ and k^
-  constexpr int kARow = kC + 4;    // padded LDS row of A^T (16-byte aligned)
-  __shared__ float sQ[kC][kRow];
-  __shared__ float sK[kC][kRow];
-  __shared__ float sAt[kC][kARow];  // A^T: [m][i]
+  constexpr int kRow = kDim + 4;   // padded LDS row (floats)
+  constexpr int kARow = kC + 4;    // padded LDS row of -A
+  constexpr int kTRow = 20;        // padded LDS row of a diagonal block's inverse
+  // sQ holds q^ until A and P are formed, then -A [64][68] and the four inverses
+  // [4][16][20]; sK holds k^, then P [64][68], then W [64][132], each on its way to the
+  // workspace.
+  __shared__ __attribute__((aligned(16))) float sQ[kC][kRow];
+  __shared__ __attribute__((aligned(16))) float sK[kC][kRow];
   __shared__ float sG[kC];
   __shared__ float sBeta[kC];
   __shared__ float sEg[kC];     // exp(G_i)
   __shared__ float sEk[kC];     // exp(G_n-1 - G_i)
+  float* const sA = &sQ[0][0];
+  float* const sT = &sQ[0][0] + kC * kARow;
+  float* const sW = &sK[0][0];
+  float* const sP = &sK[0][0];
 
   // q^ and k^ of the chunk's tokens (zero rows past its end); wave w does tokens
   // 16w .. 16w+15, all 16 tokens' loads in flight before the first norm
@@ -162,117 +194,247 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const DecodeParams
   }
   __syncthreads();
 
-  // A (strictly lower) and P (lower, diagonal included) in 4 x 4 blocks: thread (ib, mb) owns
-  // rows 4 ib .. 4 ib + 3 and columns 4 mb .. 4 mb + 3.  A is kept transposed for the
-  // substitution; P goes to the workspace transposed.
-  const int ib = tid >> 4;
-  const int mb = tid & 15;
-  {
-    f32x4 aa[4], pp[4];
+  // Waves 0, 1 solve for W's columns 64w .. 64w + 63, waves 2, 3 for U's.  U's right-hand
+  // side (beta_i v_i) comes from global memory: its loads go out before the products.
+  const bool solves_u = wave >= 2;
+  const int n0 = (wave & 1) * 64;
+  uint16_t vr[4][4][4];   // [row block][column tile][r]
+  if (solves_u) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) aa[r] = pp[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (mb <= ib) {
-#pragma unroll 2
-      for (int kb = 0; kb < kDim; kb += 4) {
-        f32x4 km[4];
+    for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) km[c] = *reinterpret_cast<const f32x4*>(&sK[4 * mb + c][kb]);
+      for (int r = 0; r < 4; ++r) {
+        const int64_t tok = t0 + min(16 * rb + 4 * lg + r, len - 1);
+        const uint16_t* row = p.qkv + tok * p.qkv_row + v_col + n0 + li;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const f32x4 ki = *reinterpret_cast<const f32x4*>(&sK[4 * ib + r][kb]);
-          const f32x4 qi = *reinterpret_cast<const f32x4*>(&sQ[4 * ib + r][kb]);
-          aa[r] += f32x4{dot4(ki, km[0]), dot4(ki, km[1]), dot4(ki, km[2]), dot4(ki, km[3])};
-          pp[r] += f32x4{dot4(qi, km[0]), dot4(qi, km[1]), dot4(qi, km[2]), dot4(qi, km[3])};
-        }
+        for (int nt = 0; nt < 4; ++nt) vr[rb][nt][r] = row[16 * nt];
       }
+  }
+
+  // A and P tiles: 32 steps of k (k = 32 lg + step) per tile
+  const uint32_t codes = wave == 0 ? kTiles0 : wave == 1 ? kTiles1 : wave == 2 ? kTiles2 : kTiles3;
+  f32x4 prod[5];
+#pragma unroll
+  for (int t = 0; t < 5; ++t) {
+    const uint32_t code = (codes >> (5 * t)) & 31u;
+    const int mt = (code >> 2) & 3;
+    const int nt = code & 3;
+    const float* arow = ((code & 16u) ? &sQ[0][0] : &sK[0][0]) + (16 * mt + li) * kRow + 32 * lg;
+    const float* brow = &sK[0][0] + (16 * nt + li) * kRow + 32 * lg;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(arow + 4 * s4);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(brow + 4 * s4);
+      acc = mfma(a.x, b.x, acc);
+      acc = mfma(a.y, b.y, acc);
+      acc = mfma(a.z, b.z, acc);
+      acc = mfma(a.w, b.w, acc);
     }
+    prod[t] = acc;
+  }
+
+  // the right-hand sides in the fragment layout: x[rb][nt][r] = B[16 rb + 4 lg + r][n0 + 16 nt + li]
+  f32x4 x[4][4];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = 4 * ib + r;
-      const float gi = sG[i];
-      const float bi = sBeta[i];
-      const bool live = i < len;
+      const int i = 16 * rb + 4 * lg + r;
+      const float beta = sBeta[i];  // zero past the end
+      const float wscale = beta * sEg[i];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int m = 4 * mb + c;
-        const float gam = __expf(gi - sG[m]);
-        sAt[m][i] = m < i ? bi * gam * aa[r][c] : 0.0f;
-        rec[kOffPT + m * kC + i] = (live && m <= i) ? gam * pp[r][c] : 0.0f;
-      }
+      for (int nt = 0; nt < 4; ++nt)
+        x[rb][nt][r] = solves_u ? beta * bf16_to_f32(vr[rb][nt][r])
+                                : wscale * sK[i][n0 + 16 * nt + li];
     }
+
+  // Qg and Kd to the workspace while q^ and k^ are still in LDS (item = one 16-byte piece
+  // of the record's order: [w or t][q][lane])
+  {
+    f32x4* qdst = reinterpret_cast<f32x4*>(rec + kOffQg);
+    f32x4* kdst = reinterpret_cast<f32x4*>(rec + kOffKd);
+#pragma unroll
+    for (int it = 0; it < kC * kDim / 4 / kThreads; ++it) {
+      const int item = it * kThreads + tid;
+      const int l = item & 63;
+      const int i = 16 * (item >> 9) + (l & 15);
+      const int k4 = 32 * (l >> 4) + 4 * ((item >> 6) & 7);
+      qdst[item] = *reinterpret_cast<const f32x4*>(&sQ[i][k4]) * sEg[i];
+      const int k = 16 * (item >> 8) + (l & 15);
+      const int j = 16 * (l >> 4) + 4 * ((item >> 6) & 3);
+      kdst[item] = f32x4{sK[j][k] * sEk[j], sK[j + 1][k] * sEk[j + 1], sK[j + 2][k] * sEk[j + 2],
+                         sK[j + 3][k] * sEk[j + 3]};  // zero rows past the end
+    }
+  }
+  __syncthreads();  // q^ and k^ no longer read
+
+  // scale the tiles: A (negated) and P to LDS, P zero above the diagonal
+#pragma unroll
+  for (int t = 0; t < 5; ++t) {
+    const uint32_t code = (codes >> (5 * t)) & 31u;
+    const int mt = (code >> 2) & 3;
+    const int m = 16 * (code & 3) + li;
+    const float gm = sG[m];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * mt + 4 * lg + r;
+      const float gam = __expf(sG[i] - gm);
+      if (code & 16u)
+        sP[i * kARow + m] = (m <= i && i < len) ? gam * prod[t][r] : 0.0f;
+      else
+        sA[i * kARow + m] = m < i ? -(sBeta[i] * gam * prod[t][r]) : 0.0f;
+    }
+  }
+  for (int e = tid; e < kC * kC; e += kThreads) {
+    const int i = e >> 6;
+    const int m = e & 63;
+    if ((m >> 4) > (i >> 4)) sP[i * kARow + m] = 0.0f;
   }
   __syncthreads();
 
-  // forward substitution, one column per thread: W (threads 0..127) and U (128..255).
-  // Column form: once x[m] is final, its multiple of A[i][m] leaves every later x[i] -- the
-  // updates of one step are independent.
+  // P to the workspace in its load order
   {
-    const int c = tid & (kDim - 1);
-    const bool is_u = tid >= kDim;
-    // every lane loads its v column (W lanes too: the select below keeps the loads free of
-    // branches, so all 64 are in flight together)
-    uint16_t vr[kC];
+    f32x4* pdst = reinterpret_cast<f32x4*>(rec + kOffP);
 #pragma unroll
-    for (int i = 0; i < kC; ++i) vr[i] = p.qkv[(t0 + min(i, len - 1)) * p.qkv_row + v_col + c];
-    float x[kC];
-#pragma unroll
-    for (int i = 0; i < kC; ++i) {
-      const float w = sEg[i] * sK[i][c];
-      x[i] = sBeta[i] * (is_u ? bf16_to_f32(vr[i]) : w);  // beta = 0 past the end
+    for (int it = 0; it < kC * kC / 4 / kThreads; ++it) {
+      const int item = it * kThreads + tid;
+      const int l = item & 63;
+      const int i = 16 * (item >> 8) + (l & 15);
+      const int j = 16 * (l >> 4) + 4 * ((item >> 6) & 3);
+      pdst[item] = *reinterpret_cast<const f32x4*>(sP + i * kARow + j);
     }
+  }
+  // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
+  if (lane < 16) {
+    const float* ab = sA + (16 * wave) * kARow + 16 * wave;
+    float col[16];
 #pragma unroll
-    for (int m = 0; m < kC - 1; ++m) {
-      const float xm = x[m];
+    for (int i = 0; i < 16; ++i) col[i] = i == li ? 1.0f : 0.0f;
 #pragma unroll
-      for (int i4 = (m + 1) & ~3; i4 < kC; i4 += 4) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(&sAt[m][i4]);
-        if (i4 > m) x[i4] = fmaf(-a.x, xm, x[i4]);
-        if (i4 + 1 > m) x[i4 + 1] = fmaf(-a.y, xm, x[i4 + 1]);
-        if (i4 + 2 > m) x[i4 + 2] = fmaf(-a.z, xm, x[i4 + 2]);
-        if (i4 + 3 > m) x[i4 + 3] = fmaf(-a.w, xm, x[i4 + 3]);
+    for (int m = 0; m < 15; ++m) {
+      const float cm = col[m];
+#pragma unroll
+      for (int i = m + 1; i < 16; ++i) col[i] = fmaf(ab[i * kARow + m], cm, col[i]);
+    }
+    float* tb = sT + wave * 16 * kTRow;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tb[i * kTRow + li] = col[i];
+  }
+  __syncthreads();
+
+  // blocked forward substitution: X_rb = T_rb (B_rb - sum over j < rb of A_rb,j X_j)
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    f32x4 y[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) y[nt] = x[rb][nt];
+#pragma unroll
+    for (int j = 0; j < rb; ++j) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(sA + (16 * rb + li) * kARow + 16 * j + 4 * lg);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        y[nt] = mfma(a.x, x[j][nt].x, y[nt]);
+        y[nt] = mfma(a.y, x[j][nt].y, y[nt]);
+        y[nt] = mfma(a.z, x[j][nt].z, y[nt]);
+        y[nt] = mfma(a.w, x[j][nt].w, y[nt]);
       }
     }
-    if (!is_u) {
-      f32x4* dst = reinterpret_cast<f32x4*>(rec + kOffWT + c * kC);
+    const f32x4 tr = *reinterpret_cast<const f32x4*>(sT + (rb * 16 + li) * kTRow + 4 * lg);
 #pragma unroll
-      for (int i4 = 0; i4 < kC / 4; ++i4)
-        dst[i4] = f32x4{x[4 * i4], x[4 * i4 + 1], x[4 * i4 + 2], x[4 * i4 + 3]};
-    } else {
-#pragma unroll
-      for (int i = 0; i < kC; ++i) rec[kOffU + i * kDim + c] = x[i];
+    for (int nt = 0; nt < 4; ++nt) {
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      acc = mfma(tr.x, y[nt].x, acc);
+      acc = mfma(tr.y, y[nt].y, acc);
+      acc = mfma(tr.z, y[nt].z, acc);
+      acc = mfma(tr.w, y[nt].w, acc);
+      x[rb][nt] = acc;
     }
   }
 
-  // Qg^T and Kd: thread (k, half) covers tokens 32 half .. 32 half + 31
+  // U straight from the fragments (its row block rb is the scan wave, its column tile the
+  // scan's block of v rows); W through LDS
+  if (solves_u) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * 4 + rb) * 256 + lane * 4) =
+            x[rb][nt];
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sW[(16 * rb + 4 * lg + r) * kRow + n0 + 16 * nt + li] = x[rb][nt][r];
+  }
+  __syncthreads();
   {
-    const int k = tid & (kDim - 1);
-    const int i0 = (tid >> 7) * 32;
-    f32x4* qdst = reinterpret_cast<f32x4*>(rec + kOffQT + k * kC + i0);
+    f32x4* wdst = reinterpret_cast<f32x4*>(rec + kOffW);
 #pragma unroll
-    for (int i4 = 0; i4 < 8; ++i4) {
-      const int i = i0 + 4 * i4;
-      qdst[i4] = f32x4{sQ[i][k] * sEg[i], sQ[i + 1][k] * sEg[i + 1], sQ[i + 2][k] * sEg[i + 2],
-                       sQ[i + 3][k] * sEg[i + 3]};
-    }
-#pragma unroll
-    for (int ii = 0; ii < 32; ++ii) {
-      const int i = i0 + ii;
-      rec[kOffKd + i * kDim + k] = sK[i][k] * sEk[i];  // zero rows past the end
+    for (int it = 0; it < kC * kDim / 4 / kThreads; ++it) {
+      const int item = it * kThreads + tid;
+      const int l = item & 63;
+      const int i = 16 * (item >> 9) + (l & 15);
+      const int k4 = 32 * (l >> 4) + 4 * ((item >> 6) & 7);
+      wdst[item] = *reinterpret_cast<const f32x4*>(sW + i * kRow + k4);
     }
   }
 }
 
+// A chunk's operands for one scan wave (tokens 16 w .. 16 w + 15 of the products, k tiles
+// 2w and 2w + 1 of the state update).
+struct ScanOperands {
+  f32x4 w[8];      // W [16 w + li][32 lg + step]
+  f32x4 qg[8];     // Qg, same positions
+  f32x4 p[4];      // P [16 w + li][16 lg + step]
+  f32x4 kd[2][4];  // Kd^T [16 (2w + t) + li][16 lg + step]
+  f32x4 u;         // U [16 w + 4 lg + r][row0 + li]
+  float gamma;     // exp(G_n-1)
+};
+
+__device__ __forceinline__ void load_operands(ScanOperands& o, const float* r, int wave,
+                                              int lane, int row_block) {
+  const f32x4* w = reinterpret_cast<const f32x4*>(r + kOffW) + wave * 8 * 64 + lane;
+  const f32x4* qg = reinterpret_cast<const f32x4*>(r + kOffQg) + wave * 8 * 64 + lane;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    o.w[q] = w[q * 64];
+    o.qg[q] = qg[q * 64];
+  }
+  const f32x4* pp = reinterpret_cast<const f32x4*>(r + kOffP) + wave * 4 * 64 + lane;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o.p[q] = pp[q * 64];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const f32x4* kd = reinterpret_cast<const f32x4*>(r + kOffKd) + (2 * wave + t) * 4 * 64 + lane;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o.kd[t][q] = kd[q * 64];
+  }
+  o.u = reinterpret_cast<const f32x4*>(r + kOffU)[(row_block * 4 + wave) * 64 + lane];
+  o.gamma = r[kOffMisc];
+}
+
 // ---- phase 2: per (sequence, v-head, block of 16 state rows), chunk by chunk ------------
-__global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const DecodeParams p,
-                                                              int num_sequences, float* ws) {
-  const int tile = blockIdx.x;
-  const int seq = tile / (p.num_v_heads * kScanBlocks);
-  const int rest = tile - seq * p.num_v_heads * kScanBlocks;
-  const int head = rest / kScanBlocks;
-  const int row0 = (rest - head * kScanBlocks) * kScanRows;
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws) {
+  // Workgroups go to the 8 XCDs round-robin by id.  The 8 row blocks of one (sequence,
+  // head) read the same chunk operands, so they are given ids on one XCD and share its L2:
+  // id = ((pair / 8) * 8 + block) * 8 + pair % 8.  The grid is padded to whole groups of 64.
+  const int xcd = blockIdx.x & 7;
+  const int rank = blockIdx.x >> 3;   // position among the XCD's workgroups
+  const int pair = (rank >> 3) * 8 + xcd;
+  if (pair >= num_sequences * p.num_v_heads) return;
+  const int seq = pair / p.num_v_heads;
+  const int head = pair - seq * p.num_v_heads;
+  const int row0 = (rank & 7) * kScanRows;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
   const int bos = p.cu[seq];
   const int eos = p.cu[seq + 1];
   const int slot = p.indices[seq];
@@ -280,173 +442,91 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const DecodeParams
   const int chunks = (eos - bos + kC - 1) / kC;
   const int gbase = chunk_base(p.cu, seq);
 
-  constexpr int kSRow = 20;   // padded LDS row of S^T / V_new (16 rows, 16-byte aligned)
-  __shared__ float sS[kDim][kSRow];   // S^T: [k][row]
-  __shared__ float sW[kDim][kC];      // W^T
-  __shared__ float sKd[kC][kDim];
-  __shared__ float sVn[kC][kSRow];
+  constexpr int kSRow = kDim + 4;
+  constexpr int kVRow = kC + 4;
+  __shared__ __attribute__((aligned(16))) float sS[kScanRows][kSRow];   // S rows [row][k]
+  __shared__ __attribute__((aligned(16))) float sVn[kScanRows][kVRow];  // V_new^T [row][token]
 
-  // thread (k, rh) owns S[row0 + 8 rh + e][k], e < 8, in the update
-  const int k = tid & (kDim - 1);
-  const int rh = tid >> 7;
+  // this wave's part of S^T in the fragment layout: st[t][r] = S[row0 + li][16 (2w + t) + 4 lg + r]
   float* tile_base = p.state + static_cast<int64_t>(slot) * p.state_slot +
-                     static_cast<int64_t>(head) * kDim * kDim;
+                     static_cast<int64_t>(head) * kDim * kDim + (row0 + li) * kDim;
+  f32x4 st[2];
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    sS[k][8 * rh + e] = from_slot ? tile_base[(row0 + 8 * rh + e) * kDim + k] : 0.0f;
-
-  // The next chunk's W^T, Kd (8 + 8 pieces of 16 bytes per thread) and U (one piece) are
-  // loaded into registers while the current chunk computes.
-  constexpr int kCopy = kDim * kC / 4 / kThreads;
-  f32x4 wnext[kCopy], knext[kCopy], unext;
-  float gnext = 0.0f;
-  auto fetch = [&](int c) {
-    const float* r = ws + (static_cast<int64_t>(gbase + c) * p.num_v_heads + head) * kRecord;
-    const f32x4* wsrc = reinterpret_cast<const f32x4*>(r + kOffWT);
-    const f32x4* ksrc = reinterpret_cast<const f32x4*>(r + kOffKd);
-#pragma unroll
-    for (int i = 0; i < kCopy; ++i) {
-      wnext[i] = wsrc[i * kThreads + tid];
-      knext[i] = ksrc[i * kThreads + tid];
-    }
-    unext = *reinterpret_cast<const f32x4*>(r + kOffU + lane * kDim + row0 + 4 * wave);
-    gnext = r[kOffMisc];
-  };
-  if (chunks > 0) fetch(0);
-  for (int c = 0; c < chunks; ++c) {
-    float* rec = ws + (static_cast<int64_t>(gbase + c) * p.num_v_heads + head) * kRecord;
-    __syncthreads();  // S of the chunk's start complete; the previous chunk's LDS reads done
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      rec[kOffH + (row0 + 8 * rh + e) * kDim + k] = sS[k][8 * rh + e];
-    {
-      f32x4* wdst = reinterpret_cast<f32x4*>(&sW[0][0]);
-      f32x4* kdst = reinterpret_cast<f32x4*>(&sKd[0][0]);
-#pragma unroll
-      for (int i = 0; i < kCopy; ++i) {
-        wdst[i * kThreads + tid] = wnext[i];
-        kdst[i * kThreads + tid] = knext[i];
-      }
-    }
-    const f32x4 u = unext;
-    const float gamma = gnext;
-    if (c + 1 < chunks) fetch(c + 1);
-    __syncthreads();
-    // V_new for token `lane` and local rows 4 wave .. 4 wave + 3
-    {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-      for (int kk = 0; kk < kDim; ++kk)
-        acc += sW[kk][lane] * *reinterpret_cast<const f32x4*>(&sS[kk][4 * wave]);
-      const f32x4 vn = u - acc;
-      *reinterpret_cast<f32x4*>(rec + kOffVn + lane * kDim + row0 + 4 * wave) = vn;
-      *reinterpret_cast<f32x4*>(&sVn[lane][4 * wave]) = vn;
-    }
-    __syncthreads();
-    // S' = exp(G_n-1) S + V_new^T Kd
-    {
-      f32x4 lo = gamma * *reinterpret_cast<const f32x4*>(&sS[k][8 * rh]);
-      f32x4 hi = gamma * *reinterpret_cast<const f32x4*>(&sS[k][8 * rh + 4]);
-#pragma unroll 8
-      for (int j = 0; j < kC; ++j) {
-        const float kd = sKd[j][k];
-        lo += kd * *reinterpret_cast<const f32x4*>(&sVn[j][8 * rh]);
-        hi += kd * *reinterpret_cast<const f32x4*>(&sVn[j][8 * rh + 4]);
-      }
-      *reinterpret_cast<f32x4*>(&sS[k][8 * rh]) = lo;
-      *reinterpret_cast<f32x4*>(&sS[k][8 * rh + 4]) = hi;
-    }
+  for (int t = 0; t < 2; ++t) {
+    const int k = 16 * (2 * wave + t) + 4 * lg;
+    st[t] = from_slot ? *reinterpret_cast<const f32x4*>(tile_base + k)
+                      : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    *reinterpret_cast<f32x4*>(&sS[li][k]) = st[t];
   }
-  __syncthreads();
+
+  const int64_t out_row = static_cast<int64_t>(p.num_v_heads) * kDim;
+  uint16_t* out_col = p.out + static_cast<int64_t>(head) * kDim + row0 + li;
+  ScanOperands cur, nxt;
+  auto record = [&](int c) {
+    return ws + (static_cast<int64_t>(gbase + c) * p.num_v_heads + head) * kRecord;
+  };
+  const int row_block = row0 / kScanRows;
+  if (chunks > 0) load_operands(cur, record(0), wave, lane, row_block);
+  // All loads complete before the loop (s_waitcnt vmcnt(0)): the loop-carried operands then
+  // enter the loop in the same state as at every later iteration, where they were copied
+  // from the prefetch; otherwise the first chunk's pending loads make every iteration wait
+  // on the prefetch it has just issued.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  for (int c = 0; c < chunks; ++c) {
+    if (c + 1 < chunks) load_operands(nxt, record(c + 1), wave, lane, row_block);
+    __syncthreads();  // sS holds the state at the chunk's start
+    // V_new and the first term of O for tokens 16 w .. 16 w + 15 (k = 32 lg + step)
+    f32x4 vn = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&sS[li][32 * lg + 4 * q]);
+      vn = mfma(cur.w[q].x, b.x, vn);
+      o = mfma(cur.qg[q].x, b.x, o);
+      vn = mfma(cur.w[q].y, b.y, vn);
+      o = mfma(cur.qg[q].y, b.y, o);
+      vn = mfma(cur.w[q].z, b.z, vn);
+      o = mfma(cur.qg[q].z, b.z, o);
+      vn = mfma(cur.w[q].w, b.w, vn);
+      o = mfma(cur.qg[q].w, b.w, o);
+    }
+    vn = cur.u - vn;
+    *reinterpret_cast<f32x4*>(&sVn[li][16 * wave + 4 * lg]) = vn;
+    __syncthreads();
+    // O += P V_new; S'^T = gamma S^T + Kd^T V_new (j = 16 lg + step)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) st[t] *= cur.gamma;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&sVn[li][16 * lg + 4 * q]);
+      o = mfma(cur.p[q].x, b.x, o);
+      st[0] = mfma(cur.kd[0][q].x, b.x, st[0]);
+      st[1] = mfma(cur.kd[1][q].x, b.x, st[1]);
+      o = mfma(cur.p[q].y, b.y, o);
+      st[0] = mfma(cur.kd[0][q].y, b.y, st[0]);
+      st[1] = mfma(cur.kd[1][q].y, b.y, st[1]);
+      o = mfma(cur.p[q].z, b.z, o);
+      st[0] = mfma(cur.kd[0][q].z, b.z, st[0]);
+      st[1] = mfma(cur.kd[1][q].z, b.z, st[1]);
+      o = mfma(cur.p[q].w, b.w, o);
+      st[0] = mfma(cur.kd[0][q].w, b.w, st[0]);
+      st[1] = mfma(cur.kd[1][q].w, b.w, st[1]);
+    }
+    // raw outputs of tokens 16 w + 4 lg + r, column row0 + li
+    const int tok0 = bos + c * kC + 16 * wave + 4 * lg;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (tok0 + r < eos) out_col[static_cast<int64_t>(tok0 + r) * out_row] = f32_to_bf16(o[r]);
+    // the next chunk's start (this chunk's reads of sS ended before the barrier above)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      *reinterpret_cast<f32x4*>(&sS[li][16 * (2 * wave + t) + 4 * lg]) = st[t];
+    cur = nxt;
+  }
   if (slot > 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) tile_base[(row0 + 8 * rh + e) * kDim + k] = sS[k][8 * rh + e];
-  }
-}
-
-// ---- phase 3: per (chunk, v-head), raw outputs -----------------------------------------
-__global__ __launch_bounds__(kThreads) void chunk_out_kernel(const DecodeParams p,
-                                                             int num_sequences, float* ws) {
-  const int head = blockIdx.y;
-  int seq = 0, t0 = 0, len = 0;
-  if (!find_chunk(p.cu, num_sequences, blockIdx.x, seq, t0, len)) return;
-  const float* rec = ws + (static_cast<int64_t>(blockIdx.x) * p.num_v_heads + head) * kRecord;
-  const int tid = threadIdx.x;
-
-  constexpr int kHRow = kDim + 4;
-  __shared__ float sQt[kDim][kC];      // Qg^T [k][i]
-  __shared__ float sH[kDim][kHRow];    // H^T  [k][v]
-  __shared__ float sPt[kC][kC];        // P^T  [j][i]
-  __shared__ float sVn[kC][kDim];      // V_new [j][v]
-  {
-    const f32x4* q4 = reinterpret_cast<const f32x4*>(rec + kOffQT);
-    const f32x4* v4 = reinterpret_cast<const f32x4*>(rec + kOffVn);
-    f32x4* qd = reinterpret_cast<f32x4*>(&sQt[0][0]);
-    f32x4* vd = reinterpret_cast<f32x4*>(&sVn[0][0]);
-#pragma unroll
-    for (int r = 0; r < kDim * kC / 4 / kThreads; ++r) {
-      qd[r * kThreads + tid] = q4[r * kThreads + tid];
-      vd[r * kThreads + tid] = v4[r * kThreads + tid];
-    }
-    const f32x4* p4 = reinterpret_cast<const f32x4*>(rec + kOffPT);
-    f32x4* pd = reinterpret_cast<f32x4*>(&sPt[0][0]);
-#pragma unroll
-    for (int r = 0; r < kC * kC / 4 / kThreads; ++r) pd[r * kThreads + tid] = p4[r * kThreads + tid];
-    // H[v][k] -> sH[k][v]: thread (k4, vgroup) loads 16 rows' 4 columns at once
-    const int k4 = (tid & 31) * 4;
-    const int v0 = (tid >> 5) * 16;
-    f32x4 h[16];
-#pragma unroll
-    for (int vv = 0; vv < 16; ++vv)
-      h[vv] = *reinterpret_cast<const f32x4*>(rec + kOffH + (v0 + vv) * kDim + k4);
-#pragma unroll
-    for (int vv = 0; vv < 16; ++vv) {
-      sH[k4][v0 + vv] = h[vv].x;
-      sH[k4 + 1][v0 + vv] = h[vv].y;
-      sH[k4 + 2][v0 + vv] = h[vv].z;
-      sH[k4 + 3][v0 + vv] = h[vv].w;
-    }
-  }
-  __syncthreads();
-  // lane block: tokens 4 ib .. 4 ib + 3, columns 8 vb .. 8 vb + 7 (3 LDS reads per 32 FMAs)
-  const int vb = tid & 15;
-  const int ib = tid >> 4;
-  f32x4 acc[4][2];
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) acc[ii][0] = acc[ii][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-  for (int kk = 0; kk < kDim; ++kk) {
-    const f32x4 q = *reinterpret_cast<const f32x4*>(&sQt[kk][4 * ib]);
-    const f32x4 h0 = *reinterpret_cast<const f32x4*>(&sH[kk][8 * vb]);
-    const f32x4 h1 = *reinterpret_cast<const f32x4*>(&sH[kk][8 * vb + 4]);
-    acc[0][0] += q.x * h0; acc[0][1] += q.x * h1;
-    acc[1][0] += q.y * h0; acc[1][1] += q.y * h1;
-    acc[2][0] += q.z * h0; acc[2][1] += q.z * h1;
-    acc[3][0] += q.w * h0; acc[3][1] += q.w * h1;
-  }
-#pragma unroll 4
-  for (int j = 0; j < kC; ++j) {
-    const f32x4 pj = *reinterpret_cast<const f32x4*>(&sPt[j][4 * ib]);
-    const f32x4 v0 = *reinterpret_cast<const f32x4*>(&sVn[j][8 * vb]);
-    const f32x4 v1 = *reinterpret_cast<const f32x4*>(&sVn[j][8 * vb + 4]);
-    acc[0][0] += pj.x * v0; acc[0][1] += pj.x * v1;
-    acc[1][0] += pj.y * v0; acc[1][1] += pj.y * v1;
-    acc[2][0] += pj.z * v0; acc[2][1] += pj.z * v1;
-    acc[3][0] += pj.w * v0; acc[3][1] += pj.w * v1;
-  }
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    const int i = 4 * ib + ii;
-    if (i < len) {
-      uint32_t packed[4];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        packed[2 * h] = f32_to_bf16(acc[ii][h].x) | (static_cast<uint32_t>(f32_to_bf16(acc[ii][h].y)) << 16);
-        packed[2 * h + 1] = f32_to_bf16(acc[ii][h].z) | (static_cast<uint32_t>(f32_to_bf16(acc[ii][h].w)) << 16);
-      }
-      uint16_t* orow = p.out + (static_cast<int64_t>(t0 + i) * p.num_v_heads + head) * kDim + 8 * vb;
-      *reinterpret_cast<uint4*>(orow) = uint4{packed[0], packed[1], packed[2], packed[3]};
-    }
+    for (int t = 0; t < 2; ++t)
+      *reinterpret_cast<f32x4*>(tile_base + 16 * (2 * wave + t) + 4 * lg) = st[t];
   }
 }
 
@@ -474,10 +554,12 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   else
     hipLaunchKernelGGL(chunk_prep_kernel<false>, per_chunk, dim3(kThreads), 0, stream, p,
                        num_sequences, ws);
-  const int64_t scan_tiles = static_cast<int64_t>(num_sequences) * p.num_v_heads * kScanBlocks;
+  static_assert(kScanBlocks == 8, "the scan's id mapping puts 8 row blocks on one XCD");
+  const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
+  const int64_t scan_tiles = (pairs + 7) / 8 * 64;
+  if (scan_tiles > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<uint32_t>(scan_tiles)), dim3(kThreads), 0,
                      stream, p, num_sequences, ws);
-  hipLaunchKernelGGL(chunk_out_kernel, per_chunk, dim3(kThreads), 0, stream, p, num_sequences, ws);
   return check_launch("ld_gdn_prefill (chunked)");
 }
 

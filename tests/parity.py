@@ -34,12 +34,32 @@ def near_bf16_midpoint(x: torch.Tensor, window: float = MIDPOINT_WINDOW) -> torc
     return (low16 - 0.5).abs() < window
 
 
+def rstd_shift_ulps(raw_pre: torch.Tensor, y_pre: torch.Tensor,
+                    window: float = MIDPOINT_WINDOW) -> torch.Tensor:
+    """How far (in bf16 ulps of y) each y = bf16(raw) * rsqrt(mean(bf16(raw)^2) + eps) * ...
+    can move when the rounding-sensitive raw elements of its row (last dimension) round the
+    other way: such a flip changes the row's mean square, hence every y of the row.  The
+    bound leaves eps out of the mean square, which only enlarges it."""
+    raw = raw_pre.float()
+    low = raw.bfloat16().float()
+    ulp = bf16_ulp(raw)
+    other = torch.where(raw >= low, low + ulp, low - ulp)  # the neighbour across the midpoint
+    sensitive = near_bf16_midpoint(raw, window)
+    delta = torch.where(sensitive, (other.square() - low.square()).abs(), torch.zeros_like(raw))
+    ms = low.square().sum(-1, keepdim=True)
+    rel = 0.5 * delta.sum(-1, keepdim=True) / ms.clamp_min(torch.finfo(torch.float32).tiny)
+    y = y_pre.float()
+    return rel * y.abs() / bf16_ulp(y)
+
+
 def assert_bf16_outputs(actual: torch.Tensor, expected: torch.Tensor, pre=None, *,
                         rtol: float = RTOL, atol: float = ATOL, label: str = "out") -> dict:
     """bf16 outputs within rtol/atol of the oracle, except elements whose oracle value
     depends on a rounding that sits on a bf16 midpoint (flagged from the oracle's
     pre-rounding values `pre` = (raw_pre, y_pre)); those may differ by <= MAX_FLIP_ULPS
-    ulps and must stay rare.  The reference's own tolerance must hold everywhere."""
+    ulps and must stay rare.  A y counts as sensitive within the midpoint window widened by
+    the rstd shift its row's sensitive raw elements can cause (rstd_shift_ulps).  The
+    reference's own tolerance must hold everywhere."""
     a = actual.detach().float().cpu()
     e = expected.detach().float().cpu()
     assert a.shape == e.shape, (a.shape, e.shape)
@@ -50,7 +70,9 @@ def assert_bf16_outputs(actual: torch.Tensor, expected: torch.Tensor, pre=None, 
     if bad.any():
         assert pre is not None, f"{label}: {int(bad.sum())} elements outside rtol/atol"
         raw_pre, y_pre = (t.detach().float().cpu() for t in pre)
-        sensitive = near_bf16_midpoint(raw_pre) | near_bf16_midpoint(y_pre)
+        y_low16 = (y_pre.contiguous().view(torch.int32) & 0xFFFF).float() / 65536.0
+        y_window = MIDPOINT_WINDOW + rstd_shift_ulps(raw_pre, y_pre)
+        sensitive = near_bf16_midpoint(raw_pre) | ((y_low16 - 0.5).abs() < y_window)
         # ulp of the larger magnitude: a flip next to a power of two crosses into the
         # coarser binade (e.g. 0.99609375 vs 1.0078125)
         ulp = bf16_ulp(torch.maximum(a.abs(), e.abs()))
