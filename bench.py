@@ -199,14 +199,18 @@ def conv_fused(case, op_args, steps, device):
 
 def prefill(device):
     """Prefill of 32 prompts x 1024 tokens and of one 4096-token prompt (16 qk / 32 v heads,
-    states from slots of a 64-slot pool), timed over a few eager launches each."""
+    states from slots of a 64-slot pool), timed over a few eager launches each, under both
+    algorithms (token-serial recurrence; 64-token chunks in the WY form on the matrix cores)."""
     import torch
+
+    from lightdelta_amd import _lib, ops
 
     order = ("qkv", "a", "b", "a_log", "dt_bias", "slots", "has_initial", "cu_seqlens",
              "pool", "gate", "weight", "out")
     gen = torch.Generator(device=device).manual_seed(7)
     qkv_cols = (2 * H + HV) * DIM
     result = {}
+    saved = ops.prefill_algorithm()
     for label, seqs, length in (("batch_32x1024", 32, 1024), ("single_4096", 1, 4096)):
         total = seqs * length
         qkvz = torch.randn(total, qkv_cols + HV * DIM, generator=gen, device=device).bfloat16()
@@ -225,19 +229,27 @@ def prefill(device):
             out=torch.empty(total, HV, DIM, dtype=torch.bfloat16, device=device),
         )
         run = lambda: torch.ops.lightdelta.prefill(*[case[k] for k in order], 1e-6)  # noqa: E731
-        run()
-        torch.cuda.synchronize()
-        start, end = events()
-        reps = 5
-        start.record()
-        for _ in range(reps):
-            run()
-        end.record()
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / reps
-        result[label] = {"ms": round(ms, 3), "tokens_per_s": round(total / ms * 1e3, 1)}
+        entry = {"auto_selects": "chunked" if _lib.load().ld_gdn_prefill_auto_chunked(
+            total, seqs, HV) else "token_serial"}
+        try:
+            for algorithm in ("token_serial", "chunked"):
+                ops.set_prefill_algorithm(algorithm)
+                run()
+                torch.cuda.synchronize()
+                start, end = events()
+                reps = 5
+                start.record()
+                for _ in range(reps):
+                    run()
+                end.record()
+                torch.cuda.synchronize()
+                ms = start.elapsed_time(end) / reps
+                entry[algorithm] = {"ms": round(ms, 3), "tokens_per_s": round(total / ms * 1e3, 1)}
+        finally:
+            ops.set_prefill_algorithm(saved)
+        result[label] = entry
         del case
-    result["workload"] = ("prefill (state from the slot, token-by-token recurrence, gated "
+    result["workload"] = ("prefill (state from the slot, recurrence over the prompt, gated "
                           "RMSNorm, final state to the slot), 16 qk / 32 v heads")
     return result
 

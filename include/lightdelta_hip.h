@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 7
+#define LD_ABI_VERSION 8
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -156,9 +156,9 @@ int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_args* conv,
  * (non-decreasing, sequences contiguous from cu_seqlens[0]).  Two algorithms with the same
  * contract: token-serial (the decode's arithmetic, token by token; a head's state rows are
  * split over several workgroups when sequences x heads are too few to fill the GPU) and
- * chunked (64-token chunks in the WY form; faster for few long prompts; results within
- * rounding of the token-serial ones).  Either may run the norm as a second launch on the
- * same stream.
+ * chunked (64-token chunks in the WY form on the matrix cores; faster unless the prompts
+ * are many and short; results within rounding of the token-serial ones).  Either may run
+ * the norm as a second launch on the same stream.
  * Replaces the reference's prefill composition (python/lightdelta/integration/
  * vllm_layer.py:93-135: fused_post_conv_prep, gather_state with has_initial_state,
  * chunk_gated_delta_rule, scatter_state, gated RMSNorm) in one launch.
@@ -194,7 +194,7 @@ typedef struct ld_gdn_prefill_args {
   int64_t workspace_bytes;
 } ld_gdn_prefill_args;
 
-#define LD_PREFILL_AUTO 0         /* chunked when sequences x heads < 256 and the workspace fits */
+#define LD_PREFILL_AUTO 0         /* chunked when ld_gdn_prefill_auto_chunked and the workspace fits */
 #define LD_PREFILL_TOKEN_SERIAL 1 /* the decode recurrence token by token */
 #define LD_PREFILL_CHUNKED 2      /* chunks of 64 tokens in the WY form (needs the workspace) */
 
@@ -202,11 +202,21 @@ int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream);
 
 /*
  * Workspace bytes the chunked prefill needs for num_tokens rows in num_sequences sequences
- * and num_v_heads heads (240 KiB per chunk of 64 tokens and head, chunks bounded by
- * num_tokens / 64 + num_sequences).
+ * and num_v_heads heads: one 147,712-byte record per chunk of 64 tokens and head (chunks
+ * bounded by num_tokens / 64 + num_sequences), then a chunk index of num_sequences + 1
+ * int32 rounded up to 256 bytes.  0 for negative arguments.
  */
 int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t num_sequences,
                                        int32_t num_v_heads);
+
+/*
+ * 1 if LD_PREFILL_AUTO takes the chunked form for this shape (given a workspace), else 0:
+ * prompts of 256 tokens or more on average, or of 64 or more when sequences x heads are
+ * fewer than 1024.  Callers use it to decide whether to provide the workspace.  No
+ * counterpart in the reference (its prefill always runs chunk_gated_delta_rule).
+ */
+int32_t ld_gdn_prefill_auto_chunked(int64_t num_tokens, int32_t num_sequences,
+                                    int32_t num_v_heads);
 
 /*
  * Gather pool rows into a packed buffer:

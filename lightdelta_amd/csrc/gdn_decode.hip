@@ -1233,8 +1233,10 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
   const bool ws_fits = a.workspace != nullptr && a.workspace_bytes >= ws_need;
   if (a.algorithm == LD_PREFILL_CHUNKED && !ws_fits)
     return fail(LD_ERR_INVALID_ARGUMENT, "chunked prefill: workspace missing or too small");
-  const bool chunked = a.algorithm == LD_PREFILL_CHUNKED ||
-                       (a.algorithm == LD_PREFILL_AUTO && tiles < 256 && ws_fits);
+  const bool chunked =
+      a.algorithm == LD_PREFILL_CHUNKED ||
+      (a.algorithm == LD_PREFILL_AUTO && ws_fits &&
+       prefill_auto_chunked(a.num_tokens, a.num_sequences, a.num_v_heads));
   if (chunked) {
     const int rc = launch_prefill_chunked(p, a.num_sequences, a.num_tokens, dt_bf16,
                                           a.workspace, s);
@@ -1284,4 +1286,9 @@ extern "C" int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t nu
                                                   int32_t num_v_heads) {
   if (num_tokens < 0 || num_sequences < 0 || num_v_heads < 0) return 0;
   return ld::prefill_chunked_workspace_bytes(num_tokens, num_sequences, num_v_heads);
+}
+
+extern "C" int32_t ld_gdn_prefill_auto_chunked(int64_t num_tokens, int32_t num_sequences,
+                                               int32_t num_v_heads) {
+  return ld::prefill_auto_chunked(num_tokens, num_sequences, num_v_heads) ? 1 : 0;
 }

@@ -57,30 +57,59 @@ __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Chunks of sequence n start at chunk_base(n) = sum over m < n of ceil(L_m / 64).
-__device__ int chunk_base(const int32_t* cu, int n) {
-  int base = 0;
-  for (int m = 0; m < n; ++m) base += (cu[m + 1] - cu[m] + kC - 1) / kC;
-  return base;
+// chunk_start[n] = sum over m < n of ceil(L_m / 64) for n = 0 .. num_sequences: where the
+// chunks of sequence n begin in the global chunk order.  One workgroup, a block-wide scan per
+// 256 sequences.
+__global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int32_t* cu,
+                                                               int num_sequences,
+                                                               int32_t* chunk_start) {
+  __shared__ int32_t wave_total[kWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (tid == 0) chunk_start[0] = 0;
+  int carry = 0;
+  for (int base = 0; base < num_sequences; base += kThreads) {
+    const int n = base + tid;
+    int c = n < num_sequences ? (cu[n + 1] - cu[n] + kC - 1) / kC : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int up = __shfl_up(c, d);
+      if (lane >= d) c += up;
+    }
+    if (lane == 63) wave_total[wave] = c;
+    __syncthreads();
+    int before = carry;
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      before += w < wave ? wave_total[w] : 0;
+      total += wave_total[w];
+    }
+    if (n < num_sequences) chunk_start[n + 1] = before + c;
+    carry += total;
+    __syncthreads();  // wave_total is rewritten by the next round
+  }
 }
 
-// Global chunk g -> (sequence, first row, tokens); false past the last chunk.
-__device__ bool find_chunk(const int32_t* cu, int num_sequences, int g, int& seq, int& t0,
-                           int& len) {
-  int base = 0;
-  for (int n = 0; n < num_sequences; ++n) {
-    const int b = cu[n];
-    const int e = cu[n + 1];
-    const int chunks = (e - b + kC - 1) / kC;
-    if (g < base + chunks) {
-      seq = n;
-      t0 = b + (g - base) * kC;
-      len = min(kC, e - t0);
-      return true;
-    }
-    base += chunks;
+// Global chunk g -> (sequence, first row, tokens) by binary search in chunk_start; false
+// past the last chunk.
+__device__ bool find_chunk(const int32_t* cu, const int32_t* chunk_start, int num_sequences,
+                           int g, int& seq, int& t0, int& len) {
+  if (g >= chunk_start[num_sequences]) return false;
+  int lo = 0;
+  int hi = num_sequences - 1;
+  while (lo < hi) {  // the last n with chunk_start[n] <= g (empty sequences come before it)
+    const int mid = (lo + hi + 1) >> 1;
+    if (chunk_start[mid] <= g)
+      lo = mid;
+    else
+      hi = mid - 1;
   }
-  return false;
+  seq = lo;
+  t0 = cu[lo] + (g - chunk_start[lo]) * kC;
+  len = min(kC, cu[lo + 1] - t0);
+  return true;
 }
 
 // The 20 tiles of A (K K^T) and P (Q K^T) on or below the diagonal, five per wave: 5 bits
@@ -101,10 +130,11 @@ constexpr uint32_t kTiles3 = tiles5(tile_code(1, 2, 2), tile_code(0, 3, 2), tile
 // ---- phase 1: per (chunk, v-head) ----------------------------------------------------
 template <bool DtBf16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws) {
+void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
+                       const int32_t* chunk_start) {
   const int head = blockIdx.y;
   int seq = 0, t0 = 0, len = 0;
-  if (!find_chunk(p.cu, num_sequences, blockIdx.x, seq, t0, len)) return;
+  if (!find_chunk(p.cu, chunk_start, num_sequences, blockIdx.x, seq, t0, len)) return;
   float* rec = ws + (static_cast<int64_t>(blockIdx.x) * p.num_v_heads + head) * kRecord;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -419,7 +449,8 @@ __device__ __forceinline__ void load_operands(ScanOperands& o, const float* r, i
 
 // ---- phase 2: per (sequence, v-head, block of 16 state rows), chunk by chunk ------------
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws) {
+void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
+                       const int32_t* chunk_start) {
   // Workgroups go to the 8 XCDs round-robin by id.  The 8 row blocks of one (sequence,
   // head) read the same chunk operands, so they are given ids on one XCD and share its L2:
   // id = ((pair / 8) * 8 + block) * 8 + pair % 8.  The grid is padded to whole groups of 64.
@@ -440,7 +471,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws) {
   const int slot = p.indices[seq];
   const bool from_slot = slot > 0 && p.has_initial[seq] != 0;
   const int chunks = (eos - bos + kC - 1) / kC;
-  const int gbase = chunk_base(p.cu, seq);
+  const int gbase = chunk_start[seq];
 
   constexpr int kSRow = kDim + 4;
   constexpr int kVRow = kC + 4;
@@ -534,32 +565,42 @@ int64_t max_chunks(int64_t num_tokens, int64_t num_sequences) {
   return num_tokens / kC + num_sequences;  // each sequence adds at most one partial chunk
 }
 
+// Workspace: the records, then chunk_start (num_sequences + 1 int32, rounded up to 256 B).
+int64_t records_bytes(int64_t num_tokens, int64_t num_sequences, int64_t num_v_heads) {
+  return max_chunks(num_tokens, num_sequences) * num_v_heads * kRecord * 4;
+}
+
 }  // namespace
 
 int64_t prefill_chunked_workspace_bytes(int64_t num_tokens, int64_t num_sequences,
                                         int64_t num_v_heads) {
-  return max_chunks(num_tokens, num_sequences) * num_v_heads * kRecord * 4;
+  return records_bytes(num_tokens, num_sequences, num_v_heads) +
+         ((num_sequences + 1) * 4 + 255) / 256 * 256;
 }
 
 int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num_tokens,
                            bool dt_bf16, void* workspace, hipStream_t stream) {
   float* ws = static_cast<float*>(workspace);
+  int32_t* chunk_start = reinterpret_cast<int32_t*>(
+      static_cast<char*>(workspace) + records_bytes(num_tokens, num_sequences, p.num_v_heads));
   const int64_t chunks = max_chunks(num_tokens, num_sequences);
   if (chunks > 0x7fffffff || p.num_v_heads > 65535)
     return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large for the chunked form");
   const dim3 per_chunk(static_cast<uint32_t>(chunks), static_cast<uint32_t>(p.num_v_heads));
+  hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, stream, p.cu, num_sequences,
+                     chunk_start);
   if (dt_bf16)
     hipLaunchKernelGGL(chunk_prep_kernel<true>, per_chunk, dim3(kThreads), 0, stream, p,
-                       num_sequences, ws);
+                       num_sequences, ws, chunk_start);
   else
     hipLaunchKernelGGL(chunk_prep_kernel<false>, per_chunk, dim3(kThreads), 0, stream, p,
-                       num_sequences, ws);
+                       num_sequences, ws, chunk_start);
   static_assert(kScanBlocks == 8, "the scan's id mapping puts 8 row blocks on one XCD");
   const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
   const int64_t scan_tiles = (pairs + 7) / 8 * 64;
   if (scan_tiles > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<uint32_t>(scan_tiles)), dim3(kThreads), 0,
-                     stream, p, num_sequences, ws);
+                     stream, p, num_sequences, ws, chunk_start);
   return check_launch("ld_gdn_prefill (chunked)");
 }
 

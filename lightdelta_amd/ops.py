@@ -234,8 +234,9 @@ def check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, sta
                         gate, weight, out, eps)
 
 
-# Prefill algorithm: "auto" runs 64-token chunks in the WY form when sequences x heads are
-# too few to fill the GPU (< 256), else the token-serial recurrence; "token_serial" and
+# Prefill algorithm: "auto" runs 64-token chunks in the WY form for the shapes where they are
+# faster (ld_gdn_prefill_auto_chunked: long prompts, or prompts of >= 64 tokens that are too
+# few to fill the GPU token-serially), else the token-serial recurrence; "token_serial" and
 # "chunked" force one.  Results agree within rounding; the token-serial form reproduces the
 # decode kernel bit for bit.
 _PREFILL_ALGORITHMS = {"auto": _lib.PREFILL_AUTO, "token_serial": _lib.PREFILL_TOKEN_SERIAL,
@@ -263,7 +264,8 @@ def _prefill_impl(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, sta
     lib = _lib.load()
     algorithm = _prefill_algorithm
     chunked = algorithm == _lib.PREFILL_CHUNKED or (
-        algorithm == _lib.PREFILL_AUTO and slots.numel() * hv < 256)
+        algorithm == _lib.PREFILL_AUTO
+        and lib.ld_gdn_prefill_auto_chunked(qkv.shape[0], slots.numel(), hv) == 1)
     workspace = None
     if chunked:  # from the caching allocator (graph-capturable)
         nbytes = lib.ld_gdn_prefill_workspace_bytes(qkv.shape[0], slots.numel(), hv)

@@ -44,7 +44,10 @@ def decode_case(
 
     qkvz = normal(n, qkv_cols + gate_cols).to(torch.bfloat16)
     ba = normal(n, 2 * num_v_heads).to(torch.bfloat16)
-    ids = torch.randperm(pool_slots - 1, generator=gen)[:n] + 1
+    if pool_slots - 1 >= n:
+        ids = torch.randperm(pool_slots - 1, generator=gen)[:n] + 1
+    else:  # a pool smaller than the batch: slot ids repeat (for callers that replace them)
+        ids = torch.randint(1, pool_slots, (n,), generator=gen)
     case = dict(
         qkv=qkvz[:, :qkv_cols],
         a=ba[:, num_v_heads:],

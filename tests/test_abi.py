@@ -23,7 +23,7 @@ def declared_functions() -> set[str]:
 def test_header_declares_the_entry_points():
     assert declared_functions() == {
         "ld_gdn_decode", "ld_gdn_decode_conv", "ld_gdn_prefill", "ld_gdn_prefill_workspace_bytes",
-        "ld_state_gather",
+        "ld_gdn_prefill_auto_chunked", "ld_state_gather",
         "ld_state_scatter",
         "ld_state_copy", "ld_state_zero", "ld_last_error", "ld_abi_version",
     }
@@ -128,8 +128,11 @@ def test_prefill_rejects_bad_arguments_without_launching():
 
 def test_prefill_workspace_query_and_chunked_without_workspace():
     lib = _lib.load()
-    one = lib.ld_gdn_prefill_workspace_bytes(4096, 1, 32)
-    assert one == (4096 // 64 + 1) * 32 * 61504 * 4
+    # one record of 36928 floats per (chunk, v-head), chunks <= tokens / 64 + sequences, then
+    # the per-sequence chunk index (sequences + 1 int32, rounded up to 256 bytes)
+    record = 36928 * 4
+    assert lib.ld_gdn_prefill_workspace_bytes(4096, 1, 32) == (4096 // 64 + 1) * 32 * record + 256
+    assert lib.ld_gdn_prefill_workspace_bytes(100, 70, 8) == (100 // 64 + 70) * 8 * record + 512
     assert lib.ld_gdn_prefill_workspace_bytes(-1, 1, 32) == 0
     args = _lib.PrefillArgs()
     args.num_sequences, args.num_tokens = 1, 64
@@ -138,3 +141,18 @@ def test_prefill_workspace_query_and_chunked_without_workspace():
     args.algorithm = 7
     assert lib.ld_gdn_prefill(ctypes.byref(args), None) == 1
     assert "unknown prefill algorithm" in lib.ld_last_error().decode()
+
+
+@pytest.mark.parametrize("tokens,sequences,heads,expected", [
+    (4096, 1, 32, 1),        # one long prompt
+    (32 * 1024, 32, 32, 1),  # long prompts that fill the GPU anyway
+    (16 * 128, 16, 32, 1),   # 128-token prompts, 512 (sequence, head) tiles
+    (64 * 64, 64, 32, 0),    # 64-token prompts, 2048 tiles: token-serial fills the GPU
+    (4 * 64, 4, 32, 1),
+    (1024 * 32, 1024, 32, 0),  # short prompts
+    (2 * 16, 2, 32, 0),
+    (0, 1, 32, 0),
+    (100, 0, 32, 0),
+])
+def test_prefill_auto_rule(tokens, sequences, heads, expected):
+    assert _lib.load().ld_gdn_prefill_auto_chunked(tokens, sequences, heads) == expected

@@ -31,7 +31,7 @@ def prefill_case(gpu, lengths, heads=(16, 32), pool_slots=None, seed=0, dt_dtype
     n = len(lengths)
     pool_slots = pool_slots or n + 2
     case = decode_case(max(total, 1), 1, num_k_heads=heads[0], num_v_heads=heads[1],
-                       pool_slots=max(pool_slots, total + 1), seed=seed, device=gpu,
+                       pool_slots=pool_slots, seed=seed, device=gpu,
                        dt_bias_dtype=dt_dtype, weight_dtype=w_dtype)
     for name in ("qkv", "a", "b", "gate", "out"):
         case[name] = case[name][:total]
@@ -191,12 +191,9 @@ def test_split_and_fused_paths_agree(gpu, sequences, token_serial):
     assert torch.equal(case["pool"], batch_pool)
 
 
-def test_chunked_long_prompts_match_the_token_serial_form(gpu):
-    """Two prompts of 1000 and 3000 tokens (partial last chunks) under the chunked form:
-    within the build's tolerance of the token-serial results after thousands of steps."""
-    announce(test="prefill_chunked_long")
-    case = prefill_case(gpu, [1000, 3000], seed=11)
-    case["has_initial"][0] = False
+def chunked_against_token_serial(case):
+    """Runs `case` under the token-serial and the chunked form from the same pool; checks the
+    chunked results within the build's tolerance of the token-serial ones."""
     pool0 = case["pool"].clone()
     saved = ops.prefill_algorithm()
     try:
@@ -215,3 +212,26 @@ def test_chunked_long_prompts_match_the_token_serial_form(gpu):
     torch.testing.assert_close(case["out"].float(), ref_out.float(), atol=8e-3, rtol=2e-2)
     close = ((case["out"].float() - ref_out.float()).abs() <= 2e-3 + 2e-3 * ref_out.float().abs())
     assert close.float().mean() > 0.999
+
+
+def test_chunked_long_prompts_match_the_token_serial_form(gpu):
+    """Two prompts of 1000 and 3000 tokens (partial last chunks) under the chunked form:
+    within the build's tolerance of the token-serial results after thousands of steps."""
+    announce(test="prefill_chunked_long")
+    case = prefill_case(gpu, [1000, 3000], seed=11)
+    case["has_initial"][0] = False
+    chunked_against_token_serial(case)
+
+
+def test_chunked_many_sequences_match_the_token_serial_form(gpu):
+    """300 sequences of 0 to 150 tokens (empty ones among them; more sequences than one round
+    of the chunk-index scan covers), some from zero states, one on the padding slot."""
+    announce(test="prefill_chunked_many")
+    gen = torch.Generator().manual_seed(12)
+    lengths = torch.randint(0, 151, (300,), generator=gen).tolist()
+    lengths[0] = lengths[150] = lengths[299] = 0
+    lengths[256] = 64
+    case = prefill_case(gpu, lengths, seed=12)
+    case["has_initial"][::7] = False
+    case["slots"][3] = 0
+    chunked_against_token_serial(case)
