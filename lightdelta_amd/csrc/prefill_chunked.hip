@@ -414,41 +414,69 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   }
 }
 
-// A chunk's operands for one scan wave (tokens 16 w .. 16 w + 15 of the products, k tiles
-// 2w and 2w + 1 of the state update).
-struct ScanOperands {
+// ---- phase 2: per (sequence, v-head, block of 16 state rows), chunk by chunk ------------
+// Eight waves, two per SIMD.  State wave w (0..3) owns k tiles 2w and 2w + 1 of the block's
+// S^T, forms V_new for tokens 16 w .. 16 w + 15 and updates its tiles; output wave w (4..7,
+// tokens 16 (w - 4) ..) forms the raw outputs.  Each SIMD carries one of each, so one
+// wave's waits (barriers, LDS, loads) leave the matrix core to the other.
+constexpr int kScanThreads = 512;
+
+struct StateOperands {
   f32x4 w[8];      // W [16 w + li][32 lg + step]
-  f32x4 qg[8];     // Qg, same positions
-  f32x4 p[4];      // P [16 w + li][16 lg + step]
   f32x4 kd[2][4];  // Kd^T [16 (2w + t) + li][16 lg + step]
   f32x4 u;         // U [16 w + 4 lg + r][row0 + li]
   float gamma;     // exp(G_n-1)
 };
 
-__device__ __forceinline__ void load_operands(ScanOperands& o, const float* r, int wave,
-                                              int lane, int row_block) {
-  const f32x4* w = reinterpret_cast<const f32x4*>(r + kOffW) + wave * 8 * 64 + lane;
-  const f32x4* qg = reinterpret_cast<const f32x4*>(r + kOffQg) + wave * 8 * 64 + lane;
+struct OutputOperands {
+  f32x4 qg[8];     // Qg [16 w + li][32 lg + step]
+  f32x4 p[4];      // P [16 w + li][16 lg + step]
+};
+
+// Buffer resource over one chunk record (raw, byte-addressed; word 3 = 0x00020000, the
+// gfx9 raw-buffer format) and a 16-byte load at lane offset + uniform offset: the address
+// stays a scalar resource plus one offset register, whatever the compiler's register
+// pressure.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t record_resource(const float* r) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(r), 0,
+                                           static_cast<int>(kRecord * 4), 0x00020000);
+}
+
+__device__ __forceinline__ f32x4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lane16,
+                                        int byte_offset) {
+  return __builtin_bit_cast(
+      f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(lane16), byte_offset, 0));
+}
+
+// r: the chunk's record; lane16 = lane * 16
+__device__ __forceinline__ void load_state_operands(StateOperands& o, const float* r, int w,
+                                                    uint32_t lane16, int row_block) {
+  const __amdgpu_buffer_rsrc_t rs = record_resource(r);
+  const int wbase = static_cast<int>(kOffW * 4) + w * 8 * 1024;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    o.w[q] = w[q * 64];
-    o.qg[q] = qg[q * 64];
-  }
-  const f32x4* pp = reinterpret_cast<const f32x4*>(r + kOffP) + wave * 4 * 64 + lane;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) o.p[q] = pp[q * 64];
+  for (int q = 0; q < 8; ++q) o.w[q] = load16(rs, lane16, wbase + q * 1024);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const f32x4* kd = reinterpret_cast<const f32x4*>(r + kOffKd) + (2 * wave + t) * 4 * 64 + lane;
+    const int kbase = static_cast<int>(kOffKd * 4) + (2 * w + t) * 4 * 1024;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) o.kd[t][q] = kd[q * 64];
+    for (int q = 0; q < 4; ++q) o.kd[t][q] = load16(rs, lane16, kbase + q * 1024);
   }
-  o.u = reinterpret_cast<const f32x4*>(r + kOffU)[(row_block * 4 + wave) * 64 + lane];
+  o.u = load16(rs, lane16, static_cast<int>(kOffU * 4) + (row_block * 4 + w) * 1024);
   o.gamma = r[kOffMisc];
 }
 
-// ---- phase 2: per (sequence, v-head, block of 16 state rows), chunk by chunk ------------
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__device__ __forceinline__ void load_output_operands(OutputOperands& o, const float* r, int w,
+                                                     uint32_t lane16) {
+  const __amdgpu_buffer_rsrc_t rs = record_resource(r);
+  const int qbase = static_cast<int>(kOffQg * 4) + w * 8 * 1024;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o.qg[q] = load16(rs, lane16, qbase + q * 1024);
+  const int pbase = static_cast<int>(kOffP * 4) + w * 4 * 1024;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o.p[q] = load16(rs, lane16, pbase + q * 1024);
+}
+
+__global__ __launch_bounds__(kScanThreads)
 void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
                        const int32_t* chunk_start) {
   // Workgroups go to the 8 XCDs round-robin by id.  The 8 row blocks of one (sequence,
@@ -460,12 +488,18 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   if (pair >= num_sequences * p.num_v_heads) return;
   const int seq = pair / p.num_v_heads;
   const int head = pair - seq * p.num_v_heads;
-  const int row0 = (rank & 7) * kScanRows;
+  const int row_block = rank & 7;
+  const int row0 = row_block * kScanRows;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // the wave index in a scalar register: every operand address is then a scalar base plus
+  // the lane's offset, and the role test a scalar branch
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15;
   const int lg = lane >> 4;
+  const uint32_t lane16 = static_cast<uint32_t>(lane) * 16;
+  const bool state_wave = wave < 4;
+  const int w = wave & 3;
   const int bos = p.cu[seq];
   const int eos = p.cu[seq + 1];
   const int slot = p.indices[seq];
@@ -478,86 +512,126 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   __shared__ __attribute__((aligned(16))) float sS[kScanRows][kSRow];   // S rows [row][k]
   __shared__ __attribute__((aligned(16))) float sVn[kScanRows][kVRow];  // V_new^T [row][token]
 
-  // this wave's part of S^T in the fragment layout: st[t][r] = S[row0 + li][16 (2w + t) + 4 lg + r]
-  float* tile_base = p.state + static_cast<int64_t>(slot) * p.state_slot +
-                     static_cast<int64_t>(head) * kDim * kDim + (row0 + li) * kDim;
-  f32x4 st[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int k = 16 * (2 * wave + t) + 4 * lg;
-    st[t] = from_slot ? *reinterpret_cast<const f32x4*>(tile_base + k)
-                      : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    *reinterpret_cast<f32x4*>(&sS[li][k]) = st[t];
-  }
-
-  const int64_t out_row = static_cast<int64_t>(p.num_v_heads) * kDim;
-  uint16_t* out_col = p.out + static_cast<int64_t>(head) * kDim + row0 + li;
-  ScanOperands cur, nxt;
   auto record = [&](int c) {
     return ws + (static_cast<int64_t>(gbase + c) * p.num_v_heads + head) * kRecord;
   };
-  const int row_block = row0 / kScanRows;
-  if (chunks > 0) load_operands(cur, record(0), wave, lane, row_block);
-  // All loads complete before the loop (s_waitcnt vmcnt(0)): the loop-carried operands then
-  // enter the loop in the same state as at every later iteration, where they were copied
-  // from the prefetch; otherwise the first chunk's pending loads make every iteration wait
-  // on the prefetch it has just issued.
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  for (int c = 0; c < chunks; ++c) {
-    if (c + 1 < chunks) load_operands(nxt, record(c + 1), wave, lane, row_block);
-    __syncthreads();  // sS holds the state at the chunk's start
-    // V_new and the first term of O for tokens 16 w .. 16 w + 15 (k = 32 lg + step)
-    f32x4 vn = {0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+  // B fragments of S^T for k = 32 lg + step (step = 4 q + e)
+  auto s_fragment = [&](int q) {
+    return *reinterpret_cast<const f32x4*>(&sS[li][32 * lg + 4 * q]);
+  };
+  // B fragments of V_new for j = 16 lg + step
+  auto vn_fragment = [&](int q) {
+    return *reinterpret_cast<const f32x4*>(&sVn[li][16 * lg + 4 * q]);
+  };
+
+  if (state_wave) {
+    // st[t][r] = S[row0 + li][16 (2w + t) + 4 lg + r]
+    float* tile_base = p.state + static_cast<int64_t>(slot) * p.state_slot +
+                       static_cast<int64_t>(head) * kDim * kDim + (row0 + li) * kDim;
+    f32x4 st[2];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const f32x4 b = *reinterpret_cast<const f32x4*>(&sS[li][32 * lg + 4 * q]);
-      vn = mfma(cur.w[q].x, b.x, vn);
-      o = mfma(cur.qg[q].x, b.x, o);
-      vn = mfma(cur.w[q].y, b.y, vn);
-      o = mfma(cur.qg[q].y, b.y, o);
-      vn = mfma(cur.w[q].z, b.z, vn);
-      o = mfma(cur.qg[q].z, b.z, o);
-      vn = mfma(cur.w[q].w, b.w, vn);
-      o = mfma(cur.qg[q].w, b.w, o);
+    for (int t = 0; t < 2; ++t) {
+      const int k = 16 * (2 * w + t) + 4 * lg;
+      st[t] = from_slot ? *reinterpret_cast<const f32x4*>(tile_base + k)
+                        : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      *reinterpret_cast<f32x4*>(&sS[li][k]) = st[t];
     }
-    vn = cur.u - vn;
-    *reinterpret_cast<f32x4*>(&sVn[li][16 * wave + 4 * lg]) = vn;
-    __syncthreads();
-    // O += P V_new; S'^T = gamma S^T + Kd^T V_new (j = 16 lg + step)
+    // Operands of chunk c + 2 are loaded while chunk c computes, into a ring of three
+    // register sets (the loop is unrolled by three, so no set is copied: each is waited
+    // for only where it is used).
+    auto step = [&](const StateOperands& op, StateOperands& fill, int c) {
+      // unconditional (the last chunk's record again past the end): a branch around the
+      // loads would make the waits that follow conservative
+      load_state_operands(fill, record(min(c + 2, chunks - 1)), w, lane16, row_block);
+      __syncthreads();  // sS holds the state at the chunk's start
+      f32x4 vn = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) st[t] *= cur.gamma;
+      for (int q = 0; q < 8; ++q) {
+        const f32x4 b = s_fragment(q);
+        vn = mfma(op.w[q].x, b.x, vn);
+        vn = mfma(op.w[q].y, b.y, vn);
+        vn = mfma(op.w[q].z, b.z, vn);
+        vn = mfma(op.w[q].w, b.w, vn);
+      }
+      vn = op.u - vn;
+      *reinterpret_cast<f32x4*>(&sVn[li][16 * w + 4 * lg]) = vn;
+      __syncthreads();  // V_new complete; every read of sS for this chunk done
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 b = *reinterpret_cast<const f32x4*>(&sVn[li][16 * lg + 4 * q]);
-      o = mfma(cur.p[q].x, b.x, o);
-      st[0] = mfma(cur.kd[0][q].x, b.x, st[0]);
-      st[1] = mfma(cur.kd[1][q].x, b.x, st[1]);
-      o = mfma(cur.p[q].y, b.y, o);
-      st[0] = mfma(cur.kd[0][q].y, b.y, st[0]);
-      st[1] = mfma(cur.kd[1][q].y, b.y, st[1]);
-      o = mfma(cur.p[q].z, b.z, o);
-      st[0] = mfma(cur.kd[0][q].z, b.z, st[0]);
-      st[1] = mfma(cur.kd[1][q].z, b.z, st[1]);
-      o = mfma(cur.p[q].w, b.w, o);
-      st[0] = mfma(cur.kd[0][q].w, b.w, st[0]);
-      st[1] = mfma(cur.kd[1][q].w, b.w, st[1]);
+      for (int t = 0; t < 2; ++t) st[t] *= op.gamma;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 b = vn_fragment(q);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          st[t] = mfma(op.kd[t][q].x, b.x, st[t]);
+          st[t] = mfma(op.kd[t][q].y, b.y, st[t]);
+          st[t] = mfma(op.kd[t][q].z, b.z, st[t]);
+          st[t] = mfma(op.kd[t][q].w, b.w, st[t]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        *reinterpret_cast<f32x4*>(&sS[li][16 * (2 * w + t) + 4 * lg]) = st[t];
+    };
+    StateOperands ring0, ring1, ring2;
+    if (chunks > 0) {
+      load_state_operands(ring0, record(0), w, lane16, row_block);
+      load_state_operands(ring1, record(min(1, chunks - 1)), w, lane16, row_block);
     }
-    // raw outputs of tokens 16 w + 4 lg + r, column row0 + li
-    const int tok0 = bos + c * kC + 16 * wave + 4 * lg;
+    for (int c = 0; c < chunks; c += 3) {
+      step(ring0, ring2, c);
+      if (c + 1 >= chunks) break;
+      step(ring1, ring0, c + 1);
+      if (c + 2 >= chunks) break;
+      step(ring2, ring1, c + 2);
+    }
+    if (slot > 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (tok0 + r < eos) out_col[static_cast<int64_t>(tok0 + r) * out_row] = f32_to_bf16(o[r]);
-    // the next chunk's start (this chunk's reads of sS ended before the barrier above)
+      for (int t = 0; t < 2; ++t)
+        *reinterpret_cast<f32x4*>(tile_base + 16 * (2 * w + t) + 4 * lg) = st[t];
+    }
+  } else {
+    const int64_t out_row = static_cast<int64_t>(p.num_v_heads) * kDim;
+    uint16_t* out_col = p.out + static_cast<int64_t>(head) * kDim + row0 + li;
+    auto step = [&](const OutputOperands& op, OutputOperands& fill, int c) {
+      load_output_operands(fill, record(min(c + 2, chunks - 1)), w, lane16);
+      __syncthreads();  // sS holds the state at the chunk's start
+      f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-      *reinterpret_cast<f32x4*>(&sS[li][16 * (2 * wave + t) + 4 * lg]) = st[t];
-    cur = nxt;
-  }
-  if (slot > 0) {
+      for (int q = 0; q < 8; ++q) {
+        const f32x4 b = s_fragment(q);
+        o = mfma(op.qg[q].x, b.x, o);
+        o = mfma(op.qg[q].y, b.y, o);
+        o = mfma(op.qg[q].z, b.z, o);
+        o = mfma(op.qg[q].w, b.w, o);
+      }
+      __syncthreads();  // V_new complete
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-      *reinterpret_cast<f32x4*>(tile_base + 16 * (2 * wave + t) + 4 * lg) = st[t];
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 b = vn_fragment(q);
+        o = mfma(op.p[q].x, b.x, o);
+        o = mfma(op.p[q].y, b.y, o);
+        o = mfma(op.p[q].z, b.z, o);
+        o = mfma(op.p[q].w, b.w, o);
+      }
+      // raw outputs of tokens 16 w + 4 lg + r, column row0 + li
+      const int tok0 = bos + c * kC + 16 * w + 4 * lg;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (tok0 + r < eos) out_col[static_cast<int64_t>(tok0 + r) * out_row] = f32_to_bf16(o[r]);
+    };
+    OutputOperands ring0, ring1, ring2;
+    if (chunks > 0) {
+      load_output_operands(ring0, record(0), w, lane16);
+      load_output_operands(ring1, record(min(1, chunks - 1)), w, lane16);
+    }
+    for (int c = 0; c < chunks; c += 3) {
+      step(ring0, ring2, c);
+      if (c + 1 >= chunks) break;
+      step(ring1, ring0, c + 1);
+      if (c + 2 >= chunks) break;
+      step(ring2, ring1, c + 2);
+    }
   }
 }
 
@@ -599,7 +673,7 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
   const int64_t scan_tiles = (pairs + 7) / 8 * 64;
   if (scan_tiles > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
-  hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<uint32_t>(scan_tiles)), dim3(kThreads), 0,
+  hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<uint32_t>(scan_tiles)), dim3(kScanThreads), 0,
                      stream, p, num_sequences, ws, chunk_start);
   return check_launch("ld_gdn_prefill (chunked)");
 }
