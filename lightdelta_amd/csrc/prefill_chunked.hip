@@ -442,6 +442,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t record_resource(const float* r
                                            static_cast<int>(kRecord * 4), 0x00020000);
 }
 
+// bf16 by the hardware's round-to-nearest-even conversion (v_cvt_pk_bf16_f32): the same
+// value as f32_to_bf16 for every finite input
+__device__ __forceinline__ uint16_t to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
 __device__ __forceinline__ f32x4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lane16,
                                         int byte_offset) {
   return __builtin_bit_cast(
@@ -544,16 +550,24 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       // loads would make the waits that follow conservative
       load_state_operands(fill, record(min(c + 2, chunks - 1)), w, lane16, row_block);
       __syncthreads();  // sS holds the state at the chunk's start
-      f32x4 vn = {0.0f, 0.0f, 0.0f, 0.0f};
+      // two accumulation chains (k < 64, k >= 64 of each lane group) so that consecutive
+      // matrix instructions do not wait on each other's results
+      f32x4 vn0 = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 vn1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const f32x4 b = s_fragment(q);
-        vn = mfma(op.w[q].x, b.x, vn);
-        vn = mfma(op.w[q].y, b.y, vn);
-        vn = mfma(op.w[q].z, b.z, vn);
-        vn = mfma(op.w[q].w, b.w, vn);
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 b0 = s_fragment(q);
+        const f32x4 b1 = s_fragment(q + 4);
+        vn0 = mfma(op.w[q].x, b0.x, vn0);
+        vn1 = mfma(op.w[q + 4].x, b1.x, vn1);
+        vn0 = mfma(op.w[q].y, b0.y, vn0);
+        vn1 = mfma(op.w[q + 4].y, b1.y, vn1);
+        vn0 = mfma(op.w[q].z, b0.z, vn0);
+        vn1 = mfma(op.w[q + 4].z, b1.z, vn1);
+        vn0 = mfma(op.w[q].w, b0.w, vn0);
+        vn1 = mfma(op.w[q + 4].w, b1.w, vn1);
       }
-      vn = op.u - vn;
+      const f32x4 vn = op.u - (vn0 + vn1);
       *reinterpret_cast<f32x4*>(&sVn[li][16 * w + 4 * lg]) = vn;
       __syncthreads();  // V_new complete; every read of sS for this chunk done
 #pragma unroll
@@ -591,34 +605,51 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         *reinterpret_cast<f32x4*>(tile_base + 16 * (2 * w + t) + 4 * lg) = st[t];
     }
   } else {
-    const int64_t out_row = static_cast<int64_t>(p.num_v_heads) * kDim;
-    uint16_t* out_col = p.out + static_cast<int64_t>(head) * kDim + row0 + li;
+    const int out_row = p.num_v_heads * kDim;   // elements per token row of out
+    uint16_t* out_block = p.out + static_cast<int64_t>(head) * kDim + row0;
     auto step = [&](const OutputOperands& op, OutputOperands& fill, int c) {
       load_output_operands(fill, record(min(c + 2, chunks - 1)), w, lane16);
       __syncthreads();  // sS holds the state at the chunk's start
-      f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 o0 = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 o1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const f32x4 b = s_fragment(q);
-        o = mfma(op.qg[q].x, b.x, o);
-        o = mfma(op.qg[q].y, b.y, o);
-        o = mfma(op.qg[q].z, b.z, o);
-        o = mfma(op.qg[q].w, b.w, o);
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 b0 = s_fragment(q);
+        const f32x4 b1 = s_fragment(q + 4);
+        o0 = mfma(op.qg[q].x, b0.x, o0);
+        o1 = mfma(op.qg[q + 4].x, b1.x, o1);
+        o0 = mfma(op.qg[q].y, b0.y, o0);
+        o1 = mfma(op.qg[q + 4].y, b1.y, o1);
+        o0 = mfma(op.qg[q].z, b0.z, o0);
+        o1 = mfma(op.qg[q + 4].z, b1.z, o1);
+        o0 = mfma(op.qg[q].w, b0.w, o0);
+        o1 = mfma(op.qg[q + 4].w, b1.w, o1);
       }
       __syncthreads();  // V_new complete
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 b = vn_fragment(q);
-        o = mfma(op.p[q].x, b.x, o);
-        o = mfma(op.p[q].y, b.y, o);
-        o = mfma(op.p[q].z, b.z, o);
-        o = mfma(op.p[q].w, b.w, o);
+      for (int q = 0; q < 2; ++q) {
+        const f32x4 b0 = vn_fragment(q);
+        const f32x4 b1 = vn_fragment(q + 2);
+        o0 = mfma(op.p[q].x, b0.x, o0);
+        o1 = mfma(op.p[q + 2].x, b1.x, o1);
+        o0 = mfma(op.p[q].y, b0.y, o0);
+        o1 = mfma(op.p[q + 2].y, b1.y, o1);
+        o0 = mfma(op.p[q].z, b0.z, o0);
+        o1 = mfma(op.p[q + 2].z, b1.z, o1);
+        o0 = mfma(op.p[q].w, b0.w, o0);
+        o1 = mfma(op.p[q + 2].w, b1.w, o1);
       }
-      // raw outputs of tokens 16 w + 4 lg + r, column row0 + li
-      const int tok0 = bos + c * kC + 16 * w + 4 * lg;
+      const f32x4 o = o0 + o1;
+      // raw outputs of tokens 16 w + 4 lg + r, column row0 + li, through a buffer over the
+      // chunk's rows of out: rows past the sequence's end fall outside it and are dropped
+      const int t0 = bos + c * kC;
+      const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+          out_block + static_cast<int64_t>(t0) * out_row, 0, min(kC, eos - t0) * out_row * 2,
+          0x00020000);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        if (tok0 + r < eos) out_col[static_cast<int64_t>(tok0 + r) * out_row] = f32_to_bf16(o[r]);
+        __builtin_amdgcn_raw_buffer_store_b16(to_bf16(o[r]), ors,
+                                              ((16 * w + 4 * lg + r) * out_row + li) * 2, 0, 0);
     };
     OutputOperands ring0, ring1, ring2;
     if (chunks > 0) {
