@@ -1001,32 +1001,67 @@ void gdn_prefill_rows_kernel(const DecodeParams args) {
   }
 }
 
-// The gated RMSNorm of prefill rows whose raw outputs (bf16) are already in `out`, in place:
-// one wave per (token, head) over rows cu[0] .. cu[num_sequences] - 1, with the arithmetic
-// of gdn_prefill_kernel's epilogue.
-template <bool WBf16>
+// The gated RMSNorm of prefill rows whose raw outputs (bf16) are already in `out`, in place,
+// with the arithmetic of gdn_prefill_kernel's epilogue (same products in the same order, so
+// both give the same bits).  Rows are items (token, head) over cu[0] .. cu[num_sequences] - 1;
+// each wave takes kNormItems consecutive items and has all their loads in flight before the
+// first sum.  Pairs: a lane's two elements as one 32-bit load or store (needs `gate` rows at
+// 4-byte alignment; `out` is contiguous).
+constexpr int kNormItems = 8;
+
+template <bool WBf16, bool Pairs>
 __global__ __launch_bounds__(kThreads) void prefill_norm_kernel(const DecodeParams p,
                                                                 int num_sequences) {
   const int lane = threadIdx.x & 63;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  const int64_t token = item / p.num_v_heads;
-  const int head = static_cast<int>(item - token * p.num_v_heads);
-  if (token < p.cu[0] || token >= p.cu[num_sequences]) return;
-  uint16_t* row = p.out + (token * p.num_v_heads + head) * kDim;
-  const uint16_t* grow = p.gate + token * p.gate_row + head * kDim;
-  float raw[2];
-  float ss = 0.0f;
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6)) *
+                        kNormItems;
+  const int64_t lo = static_cast<int64_t>(p.cu[0]) * p.num_v_heads;
+  const int64_t hi = static_cast<int64_t>(p.cu[num_sequences]) * p.num_v_heads;
+  if (first >= hi || first + kNormItems <= lo) return;  // no row of this wave (or none at all)
+  float w[2];
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    raw[e] = bf16_to_f32(row[2 * lane + e]);
-    ss = fmaf(raw[e], raw[e], ss);
+  for (int e = 0; e < 2; ++e) w[e] = load_param(p.norm_weight, 2 * lane + e, WBf16);
+  uint32_t raw_bits[kNormItems], gate_bits[kNormItems];
+#pragma unroll
+  for (int n = 0; n < kNormItems; ++n) {
+    const int64_t item = min(max(first + n, lo), hi - 1);  // in range; unused ones not stored
+    const int64_t token = item / p.num_v_heads;
+    const int head = static_cast<int>(item - token * p.num_v_heads);
+    const uint16_t* row = p.out + item * kDim + 2 * lane;
+    const uint16_t* grow = p.gate + token * p.gate_row + head * kDim + 2 * lane;
+    if (Pairs) {
+      raw_bits[n] = *reinterpret_cast<const uint32_t*>(row);
+      gate_bits[n] = *reinterpret_cast<const uint32_t*>(grow);
+    } else {
+      raw_bits[n] = row[0] | (static_cast<uint32_t>(row[1]) << 16);
+      gate_bits[n] = grow[0] | (static_cast<uint32_t>(grow[1]) << 16);
+    }
   }
-  ss = wave_sum(ss);
-  const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const float w = load_param(p.norm_weight, 2 * lane + e, WBf16);
-    row[2 * lane + e] = f32_to_bf16(((raw[e] * rstd) * w) * silu(bf16_to_f32(grow[2 * lane + e])));
+  for (int n = 0; n < kNormItems; ++n) {
+    const int64_t item = first + n;
+    float raw[2], gate[2];
+    raw[0] = bf16_to_f32(static_cast<uint16_t>(raw_bits[n]));
+    raw[1] = bf16_to_f32(static_cast<uint16_t>(raw_bits[n] >> 16));
+    gate[0] = bf16_to_f32(static_cast<uint16_t>(gate_bits[n]));
+    gate[1] = bf16_to_f32(static_cast<uint16_t>(gate_bits[n] >> 16));
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) ss = fmaf(raw[e], raw[e], ss);
+    ss = wave_sum(ss);
+    const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
+    uint16_t y[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) y[e] = f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(gate[e]));
+    if (item >= lo && item < hi) {
+      uint16_t* row = p.out + item * kDim + 2 * lane;
+      if (Pairs) {
+        *reinterpret_cast<uint32_t*>(row) = y[0] | (static_cast<uint32_t>(y[1]) << 16);
+      } else {
+        row[0] = y[0];
+        row[1] = y[1];
+      }
+    }
   }
 }
 
@@ -1268,13 +1303,18 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
     if (check_launch("ld_gdn_prefill") != LD_OK) return LD_ERR_LAUNCH;
     const int64_t items = a.num_tokens * static_cast<int64_t>(a.num_v_heads);
     if (items > 0) {
-      const uint32_t norm_grid = static_cast<uint32_t>((items + kWaves - 1) / kWaves);
-      if (w_bf16)
-        hipLaunchKernelGGL(prefill_norm_kernel<true>, dim3(norm_grid), dim3(kThreads), 0, s, p,
-                           a.num_sequences);
-      else
-        hipLaunchKernelGGL(prefill_norm_kernel<false>, dim3(norm_grid), dim3(kThreads), 0, s, p,
-                           a.num_sequences);
+      const int64_t per_block = static_cast<int64_t>(kWaves) * kNormItems;
+      const uint32_t norm_grid = static_cast<uint32_t>((items + per_block - 1) / per_block);
+      const bool pairs = (reinterpret_cast<uintptr_t>(a.gate) & 3) == 0 && (a.gate_row_stride & 1) == 0;
+#define LD_NORM_LAUNCH(W, P)                                                                  \
+  hipLaunchKernelGGL((prefill_norm_kernel<W, P>), dim3(norm_grid), dim3(kThreads), 0, s, p,  \
+                     a.num_sequences)
+      if (w_bf16) {
+        if (pairs) LD_NORM_LAUNCH(true, true); else LD_NORM_LAUNCH(true, false);
+      } else {
+        if (pairs) LD_NORM_LAUNCH(false, true); else LD_NORM_LAUNCH(false, false);
+      }
+#undef LD_NORM_LAUNCH
     }
   }
 #undef LD_PREFILL_LAUNCH

@@ -235,3 +235,20 @@ def test_chunked_many_sequences_match_the_token_serial_form(gpu):
     case["has_initial"][::7] = False
     case["slots"][3] = 0
     chunked_against_token_serial(case)
+
+
+def test_rows_outside_every_sequence_are_left_alone(gpu, algorithm):
+    """qkv rows that no sequence covers (all sequences empty here, or the tail after the
+    last one): their outputs stay as they were; states are written back unchanged."""
+    announce(test="prefill_uncovered_rows", algorithm=algorithm)
+    for lengths, cu in (([3, 0], [0, 0, 0]), ([5, 4], [0, 5, 6])):
+        case = prefill_case(gpu, lengths, seed=13)
+        case["cu_seqlens"].copy_(torch.tensor(cu, dtype=torch.int32))
+        case["out"].fill_(1.5)
+        exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6,
+                                                  return_pre=True)
+        run(case)
+        torch.cuda.synchronize()
+        assert_bf16_outputs(case["out"], exp_out, pre, label=f"cu={cu}")
+        assert torch.equal(case["out"][cu[-1]:].cpu(), exp_out[cu[-1]:])
+        assert_states(case["pool"], exp_pool, label=f"cu={cu}")
