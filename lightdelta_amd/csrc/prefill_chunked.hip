@@ -138,7 +138,9 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   float* rec = ws + (static_cast<int64_t>(blockIdx.x) * p.num_v_heads + head) * kRecord;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // the wave index in a scalar register: the tile table, the A / P choice and the W / U
+  // role are then scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15;
   const int lg = lane >> 4;
   const int key_head = head / p.group;
@@ -265,19 +267,28 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   }
 
   // the right-hand sides in the fragment layout: x[rb][nt][r] = B[16 rb + 4 lg + r][n0 + 16 nt + li]
+  // (one uniform branch around two straight-line loops)
   f32x4 x[4][4];
+  if (solves_u) {
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * rb + 4 * lg + r;
-      const float beta = sBeta[i];  // zero past the end
-      const float wscale = beta * sEg[i];
+      for (int r = 0; r < 4; ++r) {
+        const float beta = sBeta[16 * rb + 4 * lg + r];  // zero past the end
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        x[rb][nt][r] = solves_u ? beta * bf16_to_f32(vr[rb][nt][r])
-                                : wscale * sK[i][n0 + 16 * nt + li];
-    }
+        for (int nt = 0; nt < 4; ++nt) x[rb][nt][r] = beta * bf16_to_f32(vr[rb][nt][r]);
+      }
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * rb + 4 * lg + r;
+        const float wscale = sBeta[i] * sEg[i];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) x[rb][nt][r] = wscale * sK[i][n0 + 16 * nt + li];
+      }
+  }
 
   // Qg and Kd to the workspace while q^ and k^ are still in LDS (item = one 16-byte piece
   // of the record's order: [w or t][q][lane])
