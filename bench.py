@@ -141,7 +141,7 @@ def cpu_baseline(seconds: float) -> dict:
     packed_reference_step(*args, 1e-6, scratch=scratch)  # warm-up
     times = []
     deadline = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < deadline and len(times) < 200):
+    while len(times) < 3 or (time.perf_counter() < deadline and len(times) < 2000):
         t0 = time.perf_counter()
         packed_reference_step(*args, 1e-6, scratch=scratch)
         times.append(time.perf_counter() - t0)
