@@ -25,9 +25,12 @@ in the 256 MB Infinity Cache between consecutive steps.  A second, cache-cold fi
 (non-temporal state traffic), the regime of a many-layer model.
 
 Further figures in the same line: `conv_fused` (the same step with the width-4 causal
-conv1d + SiLU fused in front), `prefill` (32 x 1024 and 1 x 4096 tokens) and `stack48` (48 layers captured as one HIP graph, batch
-128, 1024 slots per layer = 96 GiB of state, slot ids reshuffled before every replay, 256
-replays timed end to end; --no-stack skips it).
+conv1d + SiLU fused in front), `prefill` (32 x 1024 and 1 x 4096 tokens, both algorithms),
+`mtp_verify` (B=64, T=4 verify plus the commit at a random accepted length), `copies`
+(gather / scatter / slot-to-slot copy of 128 random pairs in a 1024-slot pool, and the bf16
+conv pool) and `stack48` (48 layers captured as one HIP graph, batch 128, 1024 slots per
+layer = 96 GiB of state, slot ids reshuffled before every replay, 256 replays timed end to
+end; --no-stack skips it).
 
 CPU baseline: the reference's packed Torch path (index_select gather, unfused GDN,
 index_copy_ write-back; oracle/decode.py) on the host cores at the same shapes, timed for a
@@ -70,6 +73,8 @@ def parse_args():
                    help="skip the 48-layer, 96 GiB stack measurement")
     p.add_argument("--stack-steps", type=int, default=256)
     p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-mtp", action="store_true", help="skip the B=64, T=4 verify + commit")
+    p.add_argument("--no-copies", action="store_true", help="skip the state-pool copy kernels")
     p.add_argument("--no-graph", action="store_true",
                    help="time K eager launches instead of one K-step graph replay")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -252,6 +257,118 @@ def prefill(device):
     result["workload"] = ("prefill (state from the slot, recurrence over the prompt, gated "
                           "RMSNorm, final state to the slot), 16 qk / 32 v heads")
     return result
+
+
+def copies(device):
+    """State-pool copy kernels alone: a 1024-slot fp32 pool (32 x 128 x 128 per slot, 2 MiB)
+    and a bf16 conv pool (4 x 8192 per slot, 64 KiB); 128 random (src, dst) pairs with
+    padding slots (-1) among them.  gather_state into a packed buffer, scatter_state back,
+    copy_state slot to slot, and the conv pool's gather_slots / scatter_slots, each timed
+    as one HIP graph of 50 launches (launch overhead out of the figure).  Bytes are the rows
+    each kernel actually reads plus the rows it writes (a gather writes zeros for padding
+    rows)."""
+    import torch
+
+    ops = torch.ops.lightdelta
+    gen = torch.Generator(device=device).manual_seed(11)
+    slots_n, pairs = 1024, 128
+    pool = torch.empty(slots_n, HV, DIM, DIM, device=device).normal_(generator=gen)
+    conv = torch.empty(slots_n, 4, 8192, device=device).normal_(generator=gen).bfloat16()
+    perm = torch.randperm(slots_n - 1, generator=gen, device=device)[: 2 * pairs] + 1
+    src, dst = perm[:pairs].int(), perm[pairs:].int()
+    src[::16] = -1
+    dst[5::16] = -1
+    valid = torch.ones(pairs, dtype=torch.bool, device=device)
+    packed = torch.empty(pairs, HV, DIM, DIM, device=device)
+    packed_conv = torch.empty(pairs, 4, 8192, dtype=torch.bfloat16, device=device)
+    n_src = int((src > 0).sum())
+    n_dst = int((dst > 0).sum())
+    n_both = int(((src > 0) & (dst > 0)).sum())
+    row, conv_row = HV * DIM * DIM * 4, 4 * 8192 * 2
+    runs = {
+        "gather_state": (lambda: ops.gather_state(pool, src, valid, packed), (n_src + pairs) * row),
+        "scatter_state": (lambda: ops.scatter_state(packed, dst, pool), 2 * n_dst * row),
+        "copy_state": (lambda: ops.copy_state(pool, src, dst), 2 * n_both * row),
+        "gather_slots_conv": (lambda: ops.gather_slots(conv, src, valid, packed_conv),
+                              (n_src + pairs) * conv_row),
+        "scatter_slots_conv": (lambda: ops.scatter_slots(packed_conv, dst, conv),
+                               2 * n_dst * conv_row),
+    }
+    result = {}
+    launches = 50
+    for name, (fn, nbytes) in runs.items():
+        graph = capture(fn, launches)
+        graph.replay()
+        us = timed_replay(graph) / launches * 1e6
+        result[name] = {"us": round(us, 2), "bytes": nbytes, "TBps": round(nbytes / us / 1e6, 3)}
+        del graph
+    result["workload"] = ("state-pool copies alone: 1024-slot fp32 pool (2 MiB per slot) and "
+                          "bf16 conv pool (64 KiB per slot), 128 random pairs with padding -1")
+    del pool, conv, packed, packed_conv
+    return result
+
+
+def mtp_verify(steps, device):
+    """MTP speculative verify at B = 64, T = 4 (1 accepted + 3 draft tokens per sequence),
+    16 qk / 32 v heads, then the commit.  Sequence r owns a home slot and 3 scratch slots;
+    the verify step reads the state from the home slot and writes the 4 per-token states to
+    [home, s1, s2, s3]; the commit copies the state at a random accepted length a in [1, 4]
+    back to the home slot (copy_state from s_(a-1); nothing when a = 1).  `steps`
+    (verify, commit) pairs, each with its own accepted lengths drawn on the device
+    beforehand, are captured as one HIP graph and replayed once, timed end to end; the
+    verify launches alone are also timed per launch (HIP events)."""
+    import torch
+
+    from lightdelta_amd.workloads import decode_case
+
+    batch, width = 64, 4
+    order = ("qkv", "a", "b", "a_log", "dt_bias", "slots", "cu", "accepted", "pool", "gate",
+             "weight", "out")
+    case = decode_case(batch, width, num_k_heads=H, num_v_heads=HV, pool_slots=batch * width + 2,
+                       seed=5, device=device)
+    case["accepted"].fill_(1)  # the verify starts from slot[r, 0], the home slot
+    slots = case["slots"]
+    gen = torch.Generator(device=device).manual_seed(12)
+    accepted = torch.randint(1, width + 1, (steps, batch), generator=gen, device=device)
+    src = torch.gather(slots.long().expand(steps, -1, -1), 2, (accepted - 1).unsqueeze(2))[..., 0]
+    src = torch.where(accepted > 1, src, torch.full_like(src, -1)).int()
+    dst = torch.where(accepted > 1, slots[:, 0].long().expand(steps, -1),
+                      torch.full_like(src, -1, dtype=torch.long)).int()
+    args = [case[k] for k in order]
+    verify = lambda: torch.ops.lightdelta.decode(*args, 1e-6)  # noqa: E731
+    verify()
+    torch.cuda.synchronize()
+    verify_mean, verify_median = per_launch_us(verify, 50)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        verify()
+        torch.ops.lightdelta.copy_state(case["pool"], src[0], dst[0])
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for step in range(steps):
+            verify()
+            torch.ops.lightdelta.copy_state(case["pool"], src[step], dst[step])
+    graph.replay()  # warm-up replay
+    seconds = timed_replay(graph)
+    step_us = seconds / steps * 1e6
+    verify_bytes = batch * HV * 65536 * (1 + width)
+    commit_bytes = int((accepted > 1).sum()) * HV * 65536 * 2 // steps
+    return {
+        "workload": ("MTP verify B=64, T=4, 16 qk / 32 v heads, per-token states to "
+                     "[home, s1, s2, s3], then commit at a random accepted length (copy_state)"),
+        "us_per_step": round(step_us, 2),
+        "steps_per_s": round(1e6 / step_us, 1),
+        "tokens_per_s": round(batch * width * 1e6 / step_us, 1),
+        "verify_us": round(verify_mean, 2),
+        "verify_median_us": round(verify_median, 2),
+        "verify_TBps": round(verify_bytes / verify_mean / 1e6, 3),
+        "commit_bytes_per_step": commit_bytes,
+        "step_TBps": round((verify_bytes + commit_bytes) / step_us / 1e6, 3),
+        "frac": round((verify_bytes + commit_bytes) / step_us / 1e3 / HBM_PEAK_GBS, 4),
+    }
 
 
 def stack48(steps, device):
@@ -447,6 +564,12 @@ def main():
 
     if not args.no_prefill:
         result["prefill"] = prefill(device)
+
+    if not args.no_mtp:
+        result["mtp_verify"] = mtp_verify(args.steps, device)
+
+    if not args.no_copies:
+        result["copies"] = copies(device)
 
     if not args.no_stack:
         case = op_args = graph = None  # noqa: F841  (release the B=32 pools first)
