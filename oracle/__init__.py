@@ -1,8 +1,8 @@
 """CPU oracle for the fused GDN decode path -- TEST INFRASTRUCTURE ONLY.
 
 Nothing in the product (`lightdelta_amd/`) imports this package.  Only `tests/`,
-`__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` use it, always as the
-checker or the timed CPU baseline, never as the thing measured on the GPU.
+`__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` use it, always to check
+results or as the timed CPU baseline, never as the thing measured on the GPU.
 
 Modules and what pins each one (details in each module's header):
   gdn       fp32 Torch restatement of the reference's unfused post-conv GDN

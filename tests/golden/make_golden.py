@@ -1,6 +1,6 @@
 """Write golden vectors for the post-conv GDN by running the reference's own Torch function.
 
-Run in a container that holds the reference source (never on the GPU box):
+Run where the reference source is present (the GPU test machines do not have it):
 
     python tests/golden/make_golden.py [--reference /root/reference/python]
 

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/gdn.py, oracle/brute.py) before it is trusted as the checker:
+"""Pins the CPU oracle (oracle/gdn.py, oracle/brute.py) before the parity tests rely on it:
 golden vectors written by the reference's own post_conv_gdn, the reference's closed-form
 scalar recurrence, an fp64 brute force, delta-rule invariants, and planted mistakes that
 each of those checks must catch."""
