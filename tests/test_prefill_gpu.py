@@ -252,3 +252,38 @@ def test_rows_outside_every_sequence_are_left_alone(gpu, algorithm):
         assert_bf16_outputs(case["out"], exp_out, pre, label=f"cu={cu}")
         assert torch.equal(case["out"][cu[-1]:].cpu(), exp_out[cu[-1]:])
         assert_states(case["pool"], exp_pool, label=f"cu={cu}")
+
+
+@pytest.mark.parametrize("keys", ["identical", "alternating", "near_parallel"])
+def test_chunked_with_adversarial_keys(gpu, keys):
+    """Keys that make I + A of the WY form as far from the identity as it gets: every token
+    of a sequence with the same key, keys of alternating sign, or keys within 1e-3 of each
+    other; beta near 1 and decay near 1 (b = 6, a = -8).  The chunked form against the
+    oracle's token-by-token recurrence, over 200 tokens (4 chunks)."""
+    announce(test="prefill_chunked_adversarial", keys=keys)
+    case = prefill_case(gpu, [200, 70], seed=21)
+    saved = ops.prefill_algorithm()
+    h, hv = 16, 32
+    qkv = case["qkv"]
+    k_cols = slice(h * 128, 2 * h * 128)
+    gen = torch.Generator().manual_seed(22)
+    base = torch.randn(1, h * 128, generator=gen)
+    rows = qkv.shape[0]
+    if keys == "identical":
+        k = base.expand(rows, -1)
+    elif keys == "alternating":
+        k = base * torch.tensor([1.0, -1.0]).repeat(rows // 2 + 1)[:rows, None]
+    else:
+        k = base + 1e-3 * torch.randn(rows, h * 128, generator=gen)
+    qkv[:, k_cols] = k.to(torch.bfloat16).to(gpu)
+    case["b"].fill_(6.0)
+    case["a"].fill_(-8.0)
+    exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6, return_pre=True)
+    try:
+        ops.set_prefill_algorithm("chunked")
+        run(case)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_prefill_algorithm(saved)
+    assert_bf16_outputs(case["out"], exp_out, pre)
+    assert_states(case["pool"], exp_pool)
