@@ -495,7 +495,7 @@ __device__ __forceinline__ void load_output_operands(OutputOperands& o, const fl
 
 __global__ __launch_bounds__(kScanThreads)
 void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
-                       const int32_t* chunk_start) {
+                       const int32_t* chunk_start, int records) {
   // Workgroups go to the 8 XCDs round-robin by id.  The 8 row blocks of one (sequence,
   // head) read the same chunk operands, so they are given ids on one XCD and share its L2:
   // id = ((pair / 8) * 8 + block) * 8 + pair % 8.  The grid is padded to whole groups of 64.
@@ -521,8 +521,9 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   const int eos = p.cu[seq + 1];
   const int slot = p.indices[seq];
   const bool from_slot = slot > 0 && p.has_initial[seq] != 0;
-  const int chunks = (eos - bos + kC - 1) / kC;
   const int gbase = chunk_start[seq];
+  // (bounded by the records the workspace holds, whatever cu_seqlens says)
+  const int chunks = min((eos - bos + kC - 1) / kC, max(records - gbase, 0));
 
   constexpr int kSRow = kDim + 4;
   constexpr int kVRow = kC + 4;
@@ -716,7 +717,7 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   const int64_t scan_tiles = (pairs + 7) / 8 * 64;
   if (scan_tiles > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<uint32_t>(scan_tiles)), dim3(kScanThreads), 0,
-                     stream, p, num_sequences, ws, chunk_start);
+                     stream, p, num_sequences, ws, chunk_start, static_cast<int>(chunks));
   return check_launch("ld_gdn_prefill (chunked)");
 }
 
