@@ -18,7 +18,8 @@ ROOT = PACKAGE.parent
 CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "liblightdelta_hip.so"
-SOURCES = ("abi.hip", "gdn_decode.hip", "prefill_chunked.hip", "state_io.hip")
+SOURCES = ("abi.hip", "gdn_decode.hip", "prefill_serial.hip", "prefill_chunked.hip",
+           "state_io.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

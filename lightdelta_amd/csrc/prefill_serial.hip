@@ -1,0 +1,469 @@
+// Token-serial prefill for gfx950: the sequence's tokens run in order with a block of state
+// rows in registers for the whole prompt (read once, from the slot or as zeros; written
+// once, to the slot).  The
+// per-token arithmetic is the decode kernel's (stage_token, chunk_step), so a prefill of n
+// tokens gives bit for bit the states and outputs of n single-token decode steps.  Rows of
+// the state evolve independently (row v needs only v[v], k, q and the gates), so a head's
+// 128 rows may be split over 4 / Chunks workgroups of 4 waves, each wave holding 8 * Chunks
+// rows: fewer rows per wave shorten the per-token chain and spread a few long prompts over
+// more of the GPU, at the price of staging q and k in every workgroup.
+//   Chunks == 4 (one workgroup per head): the raw outputs of a group of 4 tokens collect in
+//   LDS (double-buffered); after one barrier per group, wave w runs the gated-RMSNorm
+//   epilogue of the group's token w.
+//   Chunks < 4: every wave writes its rows' raw outputs (rounded to bf16, the reference's
+//   rounding point before the norm) to `out`; prefill_norm_kernel applies the gated RMSNorm
+//   in place afterwards, with the epilogue's arithmetic.
+// The next token's inputs are prefetched.  Three to four waves per SIMD: the token loop
+// keeps them in flight on top of the tile, which does not fit 128 VGPRs without spills.
+//
+// Also here: the gated-RMSNorm pass over raw outputs (prefill_norm_kernel, used by the
+// row-split kernels and the chunked form) and the prefill entry points of the C ABI, which
+// choose between this form and the chunked one (prefill_chunked.hip).
+#include "gdn_step.h"
+
+namespace ld {
+namespace {
+
+constexpr int kPrefillGroup = 4;
+
+template <bool DtBf16, bool WBf16, int Chunks>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4)))
+void gdn_prefill_kernel(const DecodeParams args) {
+  static_assert(Chunks == 1 || Chunks == 2 || Chunks == 4, "8, 16 or 32 rows per wave");
+  constexpr int kBlocks = 4 / Chunks;         // workgroups per (sequence, head)
+  constexpr int kWaveRows = 8 * Chunks;       // state rows per wave
+  constexpr int kTilePieces = 4 * Chunks;     // 16-byte pieces per lane
+  const DecodeParams& p = args;
+  const int tile = blockIdx.x;
+  const int sequence = tile / (p.num_v_heads * kBlocks);
+  const int rest = tile - sequence * p.num_v_heads * kBlocks;
+  const int head = rest / kBlocks;
+  const int block = rest - head * kBlocks;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int bos = p.cu[sequence];
+  const int eos = p.cu[sequence + 1];
+  const int slot = p.indices[sequence];
+  const bool from_slot = slot > 0 && p.has_initial[sequence] != 0;
+
+  const int key_head = head / p.group;
+  const int kq = lane & 15;
+  const int rsub = lane >> 4;
+  const int wave_row0 = block * kWaves * kWaveRows + wave * kWaveRows;  // first row of the wave
+  const int row_base = wave_row0 + rsub;
+  const int q_col = key_head * kDim;
+  const int k_col = (p.num_k_heads + key_head) * kDim;
+  const int v_col = (2 * p.num_k_heads + head) * kDim;
+  const int v_lane = v_col + wave_row0 + (lane & (kWaveRows - 1));
+
+  __shared__ float s_v[kWaves][kWaveRows];
+  __shared__ float s_o[Chunks == 4 ? 2 : 1][Chunks == 4 ? kPrefillGroup : kWaves]
+                      [Chunks == 4 ? kDim : kWaveRows];
+
+  const float dt_bias = load_param(p.dt_bias, head, DtBf16);
+  const float a_log = p.a_log[head];
+  float w[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) w[e] = Chunks == 4 ? load_param(p.norm_weight, 2 * lane + e, WBf16) : 0.0f;
+
+  const int64_t head_offset = static_cast<int64_t>(head) * kDim * kDim;
+  const uint32_t lane_bytes = static_cast<uint32_t>(row_base * kDim + kq * 4) * 4u;
+  f32x4 s[kTilePieces];
+  if (from_slot) {
+    const char* src_tile = reinterpret_cast<const char*>(
+        p.state + static_cast<int64_t>(slot) * p.state_slot + head_offset);
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j)
+      s[j] = *reinterpret_cast<const f32x4*>(src_tile + (lane_bytes + tile_piece_bytes(j)));
+  } else {
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j) s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  TokenIn next;  // inputs of the next token
+  if (bos < eos) next = load_token(p, bos, q_col, k_col, v_lane, head, kq);
+  int buf = 0;
+  for (int g0 = bos; g0 < eos; g0 += kPrefillGroup, buf ^= 1) {
+    // gate of the token whose epilogue this wave runs after the group (one workgroup per head)
+    uint16_t gh[2] = {0, 0};
+    if constexpr (Chunks == 4) {
+      const int64_t etoken = min(g0 + wave, eos - 1);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) gh[e] = p.gate[etoken * p.gate_row + head * kDim + 2 * lane + e];
+    }
+    for (int i = 0; i < kPrefillGroup && g0 + i < eos; ++i) {
+      const int t = g0 + i;
+      const TokenIn in = next;
+      if (t + 1 < eos) next = load_token(p, t + 1, q_col, k_col, v_lane, head, kq);
+      const Staged x = stage_token(in, a_log, dt_bias, p.scale);
+      if (lane < kWaveRows) s_v[wave][lane] = bf16_to_f32(in.v);
+      // s_v (and s_o below) are read back by other lanes of this wave: a wave's LDS
+      // operations run in program order, so only the compiler must not reorder them.
+      asm volatile("" ::: "memory");
+      Vectors vec;
+      vec.q0 = x.q0;
+      vec.q1 = x.q1;
+      vec.k0 = x.k0;
+      vec.k1 = x.k1;
+      // output rows: absolute in the per-group buffer, wave-relative in the per-wave one
+      float* o = Chunks == 4 ? s_o[buf][i] : s_o[0][wave];
+      const int orow = Chunks == 4 ? row_base : rsub;
+#define LD_PREFILL_CHUNK(C)                                                                    \
+  if constexpr ((C) < Chunks)                                                                  \
+    chunk_step<C, false, false, kTilePieces>(s, vec, s_v[wave][8 * (C) + rsub],                \
+                                             s_v[wave][8 * (C) + 4 + rsub], o, x.decay,        \
+                                             x.beta, kq, orow + 8 * (C), nullptr, lane_bytes);
+      LD_PREFILL_CHUNK(0)
+      LD_PREFILL_CHUNK(1)
+      LD_PREFILL_CHUNK(2)
+      LD_PREFILL_CHUNK(3)
+#undef LD_PREFILL_CHUNK
+      asm volatile("" ::: "memory");
+      if constexpr (Chunks < 4) {  // raw outputs of the wave's rows (bf16-exact values)
+        if (lane < kWaveRows)
+          p.out[(static_cast<int64_t>(t) * p.num_v_heads + head) * kDim + wave_row0 + lane] =
+              f32_to_bf16(s_o[0][wave][lane]);
+      }
+    }
+    if constexpr (Chunks == 4) {
+      lds_barrier();  // the group's raw outputs are complete
+      if (g0 + wave < eos) {  // gated RMSNorm epilogue of the group's token `wave`
+        float raw[2];
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          raw[e] = s_o[buf][wave][2 * lane + e];
+          ss = fmaf(raw[e], raw[e], ss);
+        }
+        ss = wave_sum(ss);
+        const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
+        uint16_t* orow_ptr = p.out + (static_cast<int64_t>(g0 + wave) * p.num_v_heads + head) * kDim;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          orow_ptr[2 * lane + e] =
+              f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(bf16_to_f32(gh[e])));
+      }
+    }
+  }
+
+  if (slot > 0) {  // the state after the last token (the initial one for an empty sequence)
+    char* dst_tile = reinterpret_cast<char*>(p.state + static_cast<int64_t>(slot) * p.state_slot +
+                                             head_offset);
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j)
+      *reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j))) = s[j];
+  }
+}
+
+// Prefill with a head's rows split over 4 / Chunks workgroups (Chunks = 1 or 2): for a few
+// prompts, where one workgroup per (sequence, head) leaves most of the GPU idle and every
+// token's latency chain is exposed.  Same arithmetic as gdn_prefill_kernel; the loop is
+// arranged for latency: token inputs are prefetched kDepth tokens ahead, token t + 1 is
+// staged (norms, gates) while token t's rows update, and every lane loads the v values of
+// its own rows directly.  Raw outputs go to `out` for prefill_norm_kernel.
+template <bool DtBf16, bool WBf16, int Chunks>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4)))
+void gdn_prefill_rows_kernel(const DecodeParams args) {
+  static_assert(Chunks == 1 || Chunks == 2, "8 or 16 rows per wave");
+  constexpr int kBlocks = 4 / Chunks;
+  constexpr int kWaveRows = 8 * Chunks;
+  constexpr int kTilePieces = 4 * Chunks;
+  constexpr int kDepth = 3;  // tokens in flight ahead of the one being stepped
+  const DecodeParams& p = args;
+  const int tile = blockIdx.x;
+  const int sequence = tile / (p.num_v_heads * kBlocks);
+  const int rest = tile - sequence * p.num_v_heads * kBlocks;
+  const int head = rest / kBlocks;
+  const int block = rest - head * kBlocks;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int bos = p.cu[sequence];
+  const int eos = p.cu[sequence + 1];
+  const int slot = p.indices[sequence];
+  const bool from_slot = slot > 0 && p.has_initial[sequence] != 0;
+
+  const int key_head = head / p.group;
+  const int kq = lane & 15;
+  const int rsub = lane >> 4;
+  const int wave_row0 = block * kWaves * kWaveRows + wave * kWaveRows;
+  const int row_base = wave_row0 + rsub;
+  const int q_col = key_head * kDim;
+  const int k_col = (p.num_k_heads + key_head) * kDim;
+  const int v_col = (2 * p.num_k_heads + head) * kDim;
+
+  __shared__ float s_o[kWaves][kWaveRows];
+
+  const float dt_bias = load_param(p.dt_bias, head, DtBf16);
+  const float a_log = p.a_log[head];
+  const int64_t head_offset = static_cast<int64_t>(head) * kDim * kDim;
+  const uint32_t lane_bytes = static_cast<uint32_t>(row_base * kDim + kq * 4) * 4u;
+  f32x4 s[kTilePieces];
+  if (from_slot) {
+    const char* src_tile = reinterpret_cast<const char*>(
+        p.state + static_cast<int64_t>(slot) * p.state_slot + head_offset);
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j)
+      s[j] = *reinterpret_cast<const f32x4*>(src_tile + (lane_bytes + tile_piece_bytes(j)));
+  } else {
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j) s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  // A token's inputs: q/k/a/b as load_token lays them out, and v of the lane's 2 * Chunks rows
+  // (rows row_base + 4 i, i < 2 * Chunks).  Tokens past the sequence's end load its last one.
+  struct Pending {
+    TokenIn in;
+    uint16_t v[2 * Chunks];
+  };
+  auto fetch = [&](int t) {
+    Pending f;
+    const int64_t token = min(t, eos - 1);
+    f.in = load_token(p, token, q_col, k_col, v_col + row_base, head, kq);
+    const uint16_t* vrow = p.qkv + token * p.qkv_row + v_col + row_base;
+#pragma unroll
+    for (int i = 0; i < 2 * Chunks; ++i) f.v[i] = vrow[4 * i];
+    return f;
+  };
+  if (bos >= eos) {  // empty sequence: the initial state goes back to the slot
+    if (slot > 0) {
+      char* dst_tile = reinterpret_cast<char*>(p.state + static_cast<int64_t>(slot) * p.state_slot +
+                                               head_offset);
+#pragma unroll
+      for (int j = 0; j < kTilePieces; ++j)
+        *reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j))) = s[j];
+    }
+    return;
+  }
+  Pending pf[kDepth];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) pf[d] = fetch(bos + 1 + d);
+  Pending cur = fetch(bos);
+  Staged x = stage_token(cur.in, a_log, dt_bias, p.scale);
+  for (int t = bos; t < eos; ++t) {
+    float vv[2 * Chunks];
+#pragma unroll
+    for (int i = 0; i < 2 * Chunks; ++i) vv[i] = bf16_to_f32(cur.v[i]);
+    const Staged now = x;
+    // next token: stage it now (its inputs arrived kDepth tokens ago) and refill the queue
+    cur = pf[0];
+#pragma unroll
+    for (int d = 0; d + 1 < kDepth; ++d) pf[d] = pf[d + 1];
+    pf[kDepth - 1] = fetch(t + 1 + kDepth);
+    x = stage_token(cur.in, a_log, dt_bias, p.scale);
+    Vectors vec;
+    vec.q0 = now.q0;
+    vec.q1 = now.q1;
+    vec.k0 = now.k0;
+    vec.k1 = now.k1;
+    float* o = s_o[wave];
+    chunk_step<0, false, false, kTilePieces>(s, vec, vv[0], vv[1], o, now.decay, now.beta, kq,
+                                             rsub, nullptr, lane_bytes);
+    if constexpr (Chunks == 2)
+      chunk_step<1, false, false, kTilePieces>(s, vec, vv[2], vv[3], o, now.decay, now.beta, kq,
+                                               rsub + 8, nullptr, lane_bytes);
+    // s_o is read back by other lanes of this wave: a wave's LDS operations run in program
+    // order, so only the compiler must not reorder them.
+    asm volatile("" ::: "memory");
+    if (lane < kWaveRows)
+      p.out[(static_cast<int64_t>(t) * p.num_v_heads + head) * kDim + wave_row0 + lane] =
+          f32_to_bf16(s_o[wave][lane]);
+    asm volatile("" ::: "memory");
+  }
+  if (slot > 0) {
+    char* dst_tile = reinterpret_cast<char*>(p.state + static_cast<int64_t>(slot) * p.state_slot +
+                                             head_offset);
+#pragma unroll
+    for (int j = 0; j < kTilePieces; ++j)
+      *reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j))) = s[j];
+  }
+}
+
+// The gated RMSNorm of prefill rows whose raw outputs (bf16) are already in `out`, in place,
+// with the arithmetic of gdn_prefill_kernel's epilogue (same products in the same order, so
+// both give the same bits).  Rows are items (token, head) over cu[0] .. cu[num_sequences] - 1;
+// each wave takes kNormItems consecutive items and has all their loads in flight before the
+// first sum.  Pairs: a lane's two elements as one 32-bit load or store (needs `gate` rows at
+// 4-byte alignment; `out` is contiguous).
+constexpr int kNormItems = 8;
+
+template <bool WBf16, bool Pairs>
+__global__ __launch_bounds__(kThreads) void prefill_norm_kernel(const DecodeParams p,
+                                                                int num_sequences) {
+  const int lane = threadIdx.x & 63;
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6)) *
+                        kNormItems;
+  const int64_t lo = static_cast<int64_t>(p.cu[0]) * p.num_v_heads;
+  const int64_t hi = static_cast<int64_t>(p.cu[num_sequences]) * p.num_v_heads;
+  if (first >= hi || first + kNormItems <= lo) return;  // no row of this wave (or none at all)
+  float w[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) w[e] = load_param(p.norm_weight, 2 * lane + e, WBf16);
+  uint32_t raw_bits[kNormItems], gate_bits[kNormItems];
+#pragma unroll
+  for (int n = 0; n < kNormItems; ++n) {
+    const int64_t item = min(max(first + n, lo), hi - 1);  // in range; unused ones not stored
+    const int64_t token = item / p.num_v_heads;
+    const int head = static_cast<int>(item - token * p.num_v_heads);
+    const uint16_t* row = p.out + item * kDim + 2 * lane;
+    const uint16_t* grow = p.gate + token * p.gate_row + head * kDim + 2 * lane;
+    if (Pairs) {
+      raw_bits[n] = *reinterpret_cast<const uint32_t*>(row);
+      gate_bits[n] = *reinterpret_cast<const uint32_t*>(grow);
+    } else {
+      raw_bits[n] = row[0] | (static_cast<uint32_t>(row[1]) << 16);
+      gate_bits[n] = grow[0] | (static_cast<uint32_t>(grow[1]) << 16);
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < kNormItems; ++n) {
+    const int64_t item = first + n;
+    float raw[2], gate[2];
+    raw[0] = bf16_to_f32(static_cast<uint16_t>(raw_bits[n]));
+    raw[1] = bf16_to_f32(static_cast<uint16_t>(raw_bits[n] >> 16));
+    gate[0] = bf16_to_f32(static_cast<uint16_t>(gate_bits[n]));
+    gate[1] = bf16_to_f32(static_cast<uint16_t>(gate_bits[n] >> 16));
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) ss = fmaf(raw[e], raw[e], ss);
+    ss = wave_sum(ss);
+    const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
+    uint16_t y[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) y[e] = f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(gate[e]));
+    if (item >= lo && item < hi) {
+      uint16_t* row = p.out + item * kDim + 2 * lane;
+      if (Pairs) {
+        *reinterpret_cast<uint32_t*>(row) = y[0] | (static_cast<uint32_t>(y[1]) << 16);
+      } else {
+        row[0] = y[0];
+        row[1] = y[1];
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace ld
+
+extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
+  using namespace ld;
+  if (args == nullptr) return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_prefill: args is NULL");
+  const ld_gdn_prefill_args& a = *args;
+  if (a.num_sequences < 0) return fail(LD_ERR_INVALID_ARGUMENT, "num_sequences must be >= 0");
+  if (a.algorithm < LD_PREFILL_AUTO || a.algorithm > LD_PREFILL_CHUNKED)
+    return fail(LD_ERR_INVALID_ARGUMENT, "unknown prefill algorithm");
+  if (a.num_k_heads <= 0 || a.num_v_heads <= 0 || a.num_v_heads % a.num_k_heads != 0)
+    return fail(LD_ERR_INVALID_ARGUMENT, "num_v_heads must be a positive multiple of num_k_heads");
+  if (!(a.eps > 0.0f)) return fail(LD_ERR_INVALID_ARGUMENT, "norm epsilon must be positive");
+  if ((a.dt_bias_dtype != LD_DTYPE_F32 && a.dt_bias_dtype != LD_DTYPE_BF16) ||
+      (a.norm_weight_dtype != LD_DTYPE_F32 && a.norm_weight_dtype != LD_DTYPE_BF16))
+    return fail(LD_ERR_INVALID_ARGUMENT, "weights must be FP32/BF16");
+  if (a.num_sequences == 0) return LD_OK;
+  if (!a.qkv || !a.a || !a.b || !a.a_log || !a.dt_bias || !a.slots || !a.has_initial ||
+      !a.cu_seqlens || !a.state || !a.gate || !a.norm_weight || !a.out)
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_prefill: NULL tensor pointer");
+  if (!aligned16(a.state) || (a.state_slot_stride & 3) != 0)
+    return fail(LD_ERR_INVALID_ARGUMENT, "state slots must be 16-byte aligned");
+  if (a.num_tokens < 0) return fail(LD_ERR_INVALID_ARGUMENT, "num_tokens must be >= 0");
+  const int64_t blocks = static_cast<int64_t>(a.num_sequences) * a.num_v_heads;
+  if (blocks * 4 > 0x7fffffff || a.num_tokens * static_cast<int64_t>(a.num_v_heads) > 0x1ffffffffLL)
+    return fail(LD_ERR_INVALID_ARGUMENT, "too many (sequence, head) tiles");
+  DecodeParams p{};
+  p.qkv = static_cast<const uint16_t*>(a.qkv);
+  p.qkv_row = a.qkv_row_stride;
+  p.a = static_cast<const uint16_t*>(a.a);
+  p.a_row = a.a_row_stride;
+  p.b = static_cast<const uint16_t*>(a.b);
+  p.b_row = a.b_row_stride;
+  p.a_log = a.a_log;
+  p.dt_bias = a.dt_bias;
+  p.indices = a.slots;
+  p.has_initial = a.has_initial;
+  p.cu = a.cu_seqlens;
+  p.state = a.state;
+  p.state_slot = a.state_slot_stride;
+  p.gate = static_cast<const uint16_t*>(a.gate);
+  p.gate_row = a.gate_row_stride;
+  p.norm_weight = a.norm_weight;
+  p.out = static_cast<uint16_t*>(a.out);
+  p.width = 1;
+  p.num_k_heads = a.num_k_heads;
+  p.num_v_heads = a.num_v_heads;
+  p.group = a.num_v_heads / a.num_k_heads;
+  p.scale = a.scale;
+  p.eps = a.eps;
+  const bool dt_bf16 = a.dt_bias_dtype == LD_DTYPE_BF16;
+  const bool w_bf16 = a.norm_weight_dtype == LD_DTYPE_BF16;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t tiles = blocks;
+  const int64_t ws_need = prefill_chunked_workspace_bytes(a.num_tokens, a.num_sequences,
+                                                          a.num_v_heads);
+  const bool ws_fits = a.workspace != nullptr && a.workspace_bytes >= ws_need;
+  if (a.algorithm == LD_PREFILL_CHUNKED && !ws_fits)
+    return fail(LD_ERR_INVALID_ARGUMENT, "chunked prefill: workspace missing or too small");
+  const bool chunked =
+      a.algorithm == LD_PREFILL_CHUNKED ||
+      (a.algorithm == LD_PREFILL_AUTO && ws_fits &&
+       prefill_auto_chunked(a.num_tokens, a.num_sequences, a.num_v_heads));
+  if (chunked) {
+    const int rc = launch_prefill_chunked(p, a.num_sequences, a.num_tokens, dt_bf16,
+                                          a.workspace, s);
+    if (rc != LD_OK) return rc;
+  }
+  // Token-serial: split a head's rows over more workgroups when (sequence, head) tiles alone
+  // would leave the GPU short of work (1024 tiles fill 256 CUs at 4 per CU).
+  const int chunks = chunked ? 0 : (tiles >= 256 ? 4 : (tiles >= 128 ? 2 : 1));
+  const uint32_t grid = chunks > 0 ? static_cast<uint32_t>(tiles * (4 / chunks)) : 0u;
+#define LD_PREFILL_LAUNCH(C)                                                                 \
+  hipLaunchKernelGGL(dt_bf16 ? (w_bf16 ? gdn_prefill_kernel<true, true, C>                   \
+                                       : gdn_prefill_kernel<true, false, C>)                 \
+                             : (w_bf16 ? gdn_prefill_kernel<false, true, C>                  \
+                                       : gdn_prefill_kernel<false, false, C>),               \
+                     dim3(grid), dim3(kThreads), 0, s, p)
+#define LD_PREFILL_ROWS_LAUNCH(C)                                                            \
+  hipLaunchKernelGGL(dt_bf16 ? (w_bf16 ? gdn_prefill_rows_kernel<true, true, C>              \
+                                       : gdn_prefill_rows_kernel<true, false, C>)            \
+                             : (w_bf16 ? gdn_prefill_rows_kernel<false, true, C>             \
+                                       : gdn_prefill_rows_kernel<false, false, C>),          \
+                     dim3(grid), dim3(kThreads), 0, s, p)
+  if (chunks == 4) {
+    LD_PREFILL_LAUNCH(4);
+  } else {
+    if (chunks == 2)
+      LD_PREFILL_ROWS_LAUNCH(2);
+    else if (chunks == 1)
+      LD_PREFILL_ROWS_LAUNCH(1);
+    if (check_launch("ld_gdn_prefill") != LD_OK) return LD_ERR_LAUNCH;
+    const int64_t items = a.num_tokens * static_cast<int64_t>(a.num_v_heads);
+    if (items > 0) {
+      const int64_t per_block = static_cast<int64_t>(kWaves) * kNormItems;
+      const uint32_t norm_grid = static_cast<uint32_t>((items + per_block - 1) / per_block);
+      const bool pairs = (reinterpret_cast<uintptr_t>(a.gate) & 3) == 0 && (a.gate_row_stride & 1) == 0;
+#define LD_NORM_LAUNCH(W, P)                                                                  \
+  hipLaunchKernelGGL((prefill_norm_kernel<W, P>), dim3(norm_grid), dim3(kThreads), 0, s, p,  \
+                     a.num_sequences)
+      if (w_bf16) {
+        if (pairs) LD_NORM_LAUNCH(true, true); else LD_NORM_LAUNCH(true, false);
+      } else {
+        if (pairs) LD_NORM_LAUNCH(false, true); else LD_NORM_LAUNCH(false, false);
+      }
+#undef LD_NORM_LAUNCH
+    }
+  }
+#undef LD_PREFILL_LAUNCH
+#undef LD_PREFILL_ROWS_LAUNCH
+  return check_launch("ld_gdn_prefill");
+}
+
+extern "C" int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t num_sequences,
+                                                  int32_t num_v_heads) {
+  if (num_tokens < 0 || num_sequences < 0 || num_v_heads < 0) return 0;
+  return ld::prefill_chunked_workspace_bytes(num_tokens, num_sequences, num_v_heads);
+}
+
+extern "C" int32_t ld_gdn_prefill_auto_chunked(int64_t num_tokens, int32_t num_sequences,
+                                               int32_t num_v_heads) {
+  return ld::prefill_auto_chunked(num_tokens, num_sequences, num_v_heads) ? 1 : 0;
+}
