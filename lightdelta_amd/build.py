@@ -41,6 +41,12 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions.  gdn_decode.hip: its decode kernel takes the request-metadata pointers
+# and the head count as its first 7 argument dwords, which the hardware then preloads into
+# SGPRs at launch (kernels without such leading scalar arguments preload nothing).
+EXTRA_FLAGS = {"gdn_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=7"]}
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -64,7 +70,8 @@ def build(verbose: bool = False) -> Path:
     for name in SOURCES:
         obj = BUILD / (Path(name).stem + ".o")
         objects.append(obj)
-        commands.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / name), "-o", str(obj)])
+        commands.append([hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(name, []), "-c", str(CSRC / name),
+                         "-o", str(obj)])
     workers = max(1, min(len(commands), os.cpu_count() or 1, 8))
     with ThreadPoolExecutor(workers) as pool:
         list(pool.map(_run, commands))

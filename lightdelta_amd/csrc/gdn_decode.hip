@@ -191,7 +191,13 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 // up to 8; 0 = no conv).
 template <bool DtBf16, bool WBf16, bool Stream, int Width, int ConvCols>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
-void gdn_decode_kernel(const DecodeParams args) {
+void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
+                       const int32_t* md_accepted, int md_num_v_heads, const DecodeParams args) {
+  // The request metadata pointers and the head count are kernel arguments of their own, ahead
+  // of the parameter block: the build preloads the first 7 argument dwords into SGPRs
+  // (-amdgpu-kernarg-preload-count=7), so the metadata loads go out at once instead of after
+  // the argument segment's round trip (19.97 -> 19.82 us at B=32, back-to-back A/B runs on
+  // one MI355X).
   constexpr bool Conv = ConvCols > 0;
   constexpr int kCols = Conv ? ConvCols : 1;
   // Cache hints of the state traffic.  One token: the policy's (plain loads and stores keep
@@ -214,18 +220,18 @@ void gdn_decode_kernel(const DecodeParams args) {
   // (s_load) metadata loads must not follow anything that might have written memory.
   const DecodeParams& p = args;
   const int tile = blockIdx.x;
-  const int request = tile / p.num_v_heads;
-  const int head = tile - request * p.num_v_heads;
+  const int request = tile / md_num_v_heads;
+  const int head = tile - request * md_num_v_heads;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
   // Request metadata in one round trip: token range, accepted count and the (at most 4)
   // slots of the request, read before any state store.
-  const int32_t* req_slots = p.indices + static_cast<int64_t>(request) * Width;
-  const int bos = p.cu[request];
-  const int eos = p.cu[request + 1];
-  const int accepted = p.accepted[request];
+  const int32_t* req_slots = md_indices + static_cast<int64_t>(request) * Width;
+  const int bos = md_cu[request];
+  const int eos = md_cu[request + 1];
+  const int accepted = md_accepted[request];
   int slot[Width];
 #pragma unroll
   for (int t = 0; t < Width; ++t) slot[t] = req_slots[t];
@@ -571,7 +577,8 @@ void launch_decode(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t bl
                                   : gdn_decode_kernel<true, false, Stream, Width, ConvCols>)
                         : (w_bf16 ? gdn_decode_kernel<false, true, Stream, Width, ConvCols>
                                   : gdn_decode_kernel<false, false, Stream, Width, ConvCols>);
-  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, stream, p.indices, p.cu, p.accepted,
+                     p.num_v_heads, p);
 }
 
 template <bool Stream>
