@@ -465,32 +465,70 @@ __device__ __forceinline__ f32x4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t la
       f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(lane16), byte_offset, 0));
 }
 
-// r: the chunk's record; lane16 = lane * 16
-__device__ __forceinline__ void load_state_operands(StateOperands& o, const float* r, int w,
-                                                    uint32_t lane16, int row_block) {
-  const __amdgpu_buffer_rsrc_t rs = record_resource(r);
-  const int wbase = static_cast<int>(kOffW * 4) + w * 8 * 1024;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) o.w[q] = load16(rs, lane16, wbase + q * 1024);
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int kbase = static_cast<int>(kOffKd * 4) + (2 * w + t) * 4 * 1024;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) o.kd[t][q] = load16(rs, lane16, kbase + q * 1024);
-  }
-  o.u = load16(rs, lane16, static_cast<int>(kOffU * 4) + (row_block * 4 + w) * 1024);
-  o.gamma = r[kOffMisc];
+__device__ __forceinline__ float load4(__amdgpu_buffer_rsrc_t rsrc, int byte_offset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, 0, byte_offset, 0));
 }
 
-__device__ __forceinline__ void load_output_operands(OutputOperands& o, const float* r, int w,
-                                                     uint32_t lane16) {
-  const __amdgpu_buffer_rsrc_t rs = record_resource(r);
-  const int qbase = static_cast<int>(kOffQg * 4) + w * 8 * 1024;
+// The operand loads of one chunk come in pieces that the scan issues between its products,
+// a few at a time (issued in one burst at the top of a chunk, the CU's 116 loads would hold
+// every wave at the chunk's first barrier until the last of them was accepted).
+// State piece q < 4: W columns q and q + 4 (with U and gamma at q = 0); piece 4 + q: Kd^T
+// step group q of both tiles.  Output piece q < 4: Qg columns q and q + 4; piece 4 + q
+// (q < 2): P columns q and q + 2.
+__device__ __forceinline__ void load_state_piece(StateOperands& o, __amdgpu_buffer_rsrc_t rs,
+                                                 int w, uint32_t lane16, int row_block,
+                                                 int piece) {
+  if (piece < 4) {
+    const int wbase = static_cast<int>(kOffW * 4) + w * 8 * 1024;
+    o.w[piece] = load16(rs, lane16, wbase + piece * 1024);
+    o.w[piece + 4] = load16(rs, lane16, wbase + (piece + 4) * 1024);
+    if (piece == 0) {
+      o.u = load16(rs, lane16, static_cast<int>(kOffU * 4) + (row_block * 4 + w) * 1024);
+      o.gamma = load4(rs, static_cast<int>(kOffMisc * 4));
+    }
+  } else {
+    const int q = piece - 4;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) o.qg[q] = load16(rs, lane16, qbase + q * 1024);
-  const int pbase = static_cast<int>(kOffP * 4) + w * 4 * 1024;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) o.p[q] = load16(rs, lane16, pbase + q * 1024);
+    for (int t = 0; t < 2; ++t)
+      o.kd[t][q] = load16(rs, lane16, static_cast<int>(kOffKd * 4) + (2 * w + t) * 4 * 1024 +
+                                          q * 1024);
+  }
+}
+
+__device__ __forceinline__ void load_output_piece(OutputOperands& o, __amdgpu_buffer_rsrc_t rs,
+                                                  int w, uint32_t lane16, int piece) {
+  if (piece < 4) {
+    const int qbase = static_cast<int>(kOffQg * 4) + w * 8 * 1024;
+    o.qg[piece] = load16(rs, lane16, qbase + piece * 1024);
+    o.qg[piece + 4] = load16(rs, lane16, qbase + (piece + 4) * 1024);
+  } else {
+    const int pbase = static_cast<int>(kOffP * 4) + w * 4 * 1024;
+    o.p[piece - 4] = load16(rs, lane16, pbase + (piece - 4) * 1024);
+    o.p[piece - 2] = load16(rs, lane16, pbase + (piece - 2) * 1024);
+  }
+}
+
+// Every instruction kind but vector memory may be moved across (a sched_barrier mask).
+constexpr int kAllButVmem = 0x78F;
+
+// Chunks 0 .. chunks - 1 through the ring of three operand sets: step(op, fill, c) computes
+// chunk c from op and loads chunk c + 2 into fill.  Whole rounds of three run in a loop with
+// no exit inside it, the last one or two chunks after it.  (An exit between the steps of a
+// round joins the loop's latch, and the wait counts at the loop head then follow that
+// shorter path: the set prefetched for the next chunk was waited for a chunk early.)
+template <class Step, class Operands>
+__device__ __forceinline__ void ring_scan(Step& step, Operands& ring0, Operands& ring1,
+                                          Operands& ring2, int chunks) {
+  int c = 0;
+  for (; c + 3 <= chunks; c += 3) {
+    step(ring0, ring2, c);
+    step(ring1, ring0, c + 1);
+    step(ring2, ring1, c + 2);
+  }
+  if (c < chunks) {
+    step(ring0, ring2, c);
+    if (c + 1 < chunks) step(ring1, ring0, c + 1);
+  }
 }
 
 __global__ __launch_bounds__(kScanThreads)
@@ -558,9 +596,9 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     // register sets (the loop is unrolled by three, so no set is copied: each is waited
     // for only where it is used).
     auto step = [&](const StateOperands& op, StateOperands& fill, int c) {
-      // unconditional (the last chunk's record again past the end): a branch around the
-      // loads would make the waits that follow conservative
-      load_state_operands(fill, record(min(c + 2, chunks - 1)), w, lane16, row_block);
+      // fill: chunk c + 2, unconditionally (the last chunk's record again past the end: a
+      // branch around the loads would make the waits that follow conservative)
+      const __amdgpu_buffer_rsrc_t next = record_resource(record(min(c + 2, chunks - 1)));
       __syncthreads();  // sS holds the state at the chunk's start
       // two accumulation chains (k < 64, k >= 64 of each lane group) so that consecutive
       // matrix instructions do not wait on each other's results
@@ -568,6 +606,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       f32x4 vn1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        load_state_piece(fill, next, w, lane16, row_block, q);
         const f32x4 b0 = s_fragment(q);
         const f32x4 b1 = s_fragment(q + 4);
         vn0 = mfma(op.w[q].x, b0.x, vn0);
@@ -578,6 +617,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         vn1 = mfma(op.w[q + 4].z, b1.z, vn1);
         vn0 = mfma(op.w[q].w, b0.w, vn0);
         vn1 = mfma(op.w[q + 4].w, b1.w, vn1);
+        __builtin_amdgcn_sched_barrier(kAllButVmem);
       }
       const f32x4 vn = op.u - (vn0 + vn1);
       *reinterpret_cast<f32x4*>(&sVn[li][16 * w + 4 * lg]) = vn;
@@ -586,6 +626,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       for (int t = 0; t < 2; ++t) st[t] *= op.gamma;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        load_state_piece(fill, next, w, lane16, row_block, 4 + q);
         const f32x4 b = vn_fragment(q);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -594,6 +635,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
           st[t] = mfma(op.kd[t][q].z, b.z, st[t]);
           st[t] = mfma(op.kd[t][q].w, b.w, st[t]);
         }
+        __builtin_amdgcn_sched_barrier(kAllButVmem);
       }
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -601,16 +643,22 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     };
     StateOperands ring0, ring1, ring2;
     if (chunks > 0) {
-      load_state_operands(ring0, record(0), w, lane16, row_block);
-      load_state_operands(ring1, record(min(1, chunks - 1)), w, lane16, row_block);
+      // (piece by piece in the loop's order, so that the wait counts at the loop head are
+      // the same from either side)
+      const __amdgpu_buffer_rsrc_t r0 = record_resource(record(0));
+      const __amdgpu_buffer_rsrc_t r1 = record_resource(record(min(1, chunks - 1)));
+#pragma unroll
+      for (int piece = 0; piece < 8; ++piece) {
+        load_state_piece(ring0, r0, w, lane16, row_block, piece);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int piece = 0; piece < 8; ++piece) {
+        load_state_piece(ring1, r1, w, lane16, row_block, piece);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    for (int c = 0; c < chunks; c += 3) {
-      step(ring0, ring2, c);
-      if (c + 1 >= chunks) break;
-      step(ring1, ring0, c + 1);
-      if (c + 2 >= chunks) break;
-      step(ring2, ring1, c + 2);
-    }
+    ring_scan(step, ring0, ring1, ring2, chunks);
     if (slot > 0) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -620,12 +668,13 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     const int out_row = p.num_v_heads * kDim;   // elements per token row of out
     uint16_t* out_block = p.out + static_cast<int64_t>(head) * kDim + row0;
     auto step = [&](const OutputOperands& op, OutputOperands& fill, int c) {
-      load_output_operands(fill, record(min(c + 2, chunks - 1)), w, lane16);
+      const __amdgpu_buffer_rsrc_t next = record_resource(record(min(c + 2, chunks - 1)));
       __syncthreads();  // sS holds the state at the chunk's start
       f32x4 o0 = {0.0f, 0.0f, 0.0f, 0.0f};
       f32x4 o1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        load_output_piece(fill, next, w, lane16, q);
         const f32x4 b0 = s_fragment(q);
         const f32x4 b1 = s_fragment(q + 4);
         o0 = mfma(op.qg[q].x, b0.x, o0);
@@ -636,10 +685,12 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         o1 = mfma(op.qg[q + 4].z, b1.z, o1);
         o0 = mfma(op.qg[q].w, b0.w, o0);
         o1 = mfma(op.qg[q + 4].w, b1.w, o1);
+        __builtin_amdgcn_sched_barrier(kAllButVmem);
       }
       __syncthreads();  // V_new complete
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
+        load_output_piece(fill, next, w, lane16, 4 + q);
         const f32x4 b0 = vn_fragment(q);
         const f32x4 b1 = vn_fragment(q + 2);
         o0 = mfma(op.p[q].x, b0.x, o0);
@@ -650,6 +701,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         o1 = mfma(op.p[q + 2].z, b1.z, o1);
         o0 = mfma(op.p[q].w, b0.w, o0);
         o1 = mfma(op.p[q + 2].w, b1.w, o1);
+        __builtin_amdgcn_sched_barrier(kAllButVmem);
       }
       const f32x4 o = o0 + o1;
       // raw outputs of tokens 16 w + 4 lg + r, column row0 + li, through a buffer over the
@@ -665,16 +717,20 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     };
     OutputOperands ring0, ring1, ring2;
     if (chunks > 0) {
-      load_output_operands(ring0, record(0), w, lane16);
-      load_output_operands(ring1, record(min(1, chunks - 1)), w, lane16);
+      const __amdgpu_buffer_rsrc_t r0 = record_resource(record(0));
+      const __amdgpu_buffer_rsrc_t r1 = record_resource(record(min(1, chunks - 1)));
+#pragma unroll
+      for (int piece = 0; piece < 6; ++piece) {
+        load_output_piece(ring0, r0, w, lane16, piece);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int piece = 0; piece < 6; ++piece) {
+        load_output_piece(ring1, r1, w, lane16, piece);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    for (int c = 0; c < chunks; c += 3) {
-      step(ring0, ring2, c);
-      if (c + 1 >= chunks) break;
-      step(ring1, ring0, c + 1);
-      if (c + 2 >= chunks) break;
-      step(ring2, ring1, c + 2);
-    }
+    ring_scan(step, ring0, ring1, ring2, chunks);
   }
 }
 
