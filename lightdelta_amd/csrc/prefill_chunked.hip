@@ -112,24 +112,33 @@ __device__ bool find_chunk(const int32_t* cu, const int32_t* chunk_start, int nu
   return true;
 }
 
-// The 20 tiles of A (K K^T) and P (Q K^T) on or below the diagonal, five per wave: 5 bits
-// each, (is_p << 4) | (row tile << 2) | column tile.
+// The 20 tiles of A (K K^T) and P (Q K^T) on or below the diagonal over the prep's 8 waves:
+// 3 each for waves 0-3 and 2 each for waves 4-7 (so 5 per SIMD, waves w and w + 4 sharing
+// one), 5 bits a tile, (is_p << 4) | (row tile << 2) | column tile.
 constexpr uint32_t tile_code(int is_p, int mt, int nt) { return (is_p << 4) | (mt << 2) | nt; }
-constexpr uint32_t tiles5(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t e) {
-  return a | (b << 5) | (c << 10) | (d << 15) | (e << 20);
+constexpr uint32_t tiles3(uint32_t a, uint32_t b, uint32_t c = 0) {
+  return a | (b << 5) | (c << 10);
 }
-constexpr uint32_t kTiles0 = tiles5(tile_code(0, 0, 0), tile_code(1, 0, 0), tile_code(0, 3, 0),
-                                    tile_code(1, 3, 0), tile_code(0, 3, 1));
-constexpr uint32_t kTiles1 = tiles5(tile_code(0, 1, 0), tile_code(0, 1, 1), tile_code(1, 1, 0),
-                                    tile_code(1, 1, 1), tile_code(1, 3, 1));
-constexpr uint32_t kTiles2 = tiles5(tile_code(0, 2, 0), tile_code(0, 2, 1), tile_code(0, 2, 2),
-                                    tile_code(1, 2, 0), tile_code(1, 2, 1));
-constexpr uint32_t kTiles3 = tiles5(tile_code(1, 2, 2), tile_code(0, 3, 2), tile_code(0, 3, 3),
-                                    tile_code(1, 3, 2), tile_code(1, 3, 3));
+__device__ __forceinline__ uint32_t prep_tiles(int wave) {
+  switch (wave) {
+    case 0: return tiles3(tile_code(0, 0, 0), tile_code(1, 0, 0), tile_code(0, 3, 0));
+    case 1: return tiles3(tile_code(0, 1, 0), tile_code(0, 1, 1), tile_code(1, 1, 0));
+    case 2: return tiles3(tile_code(0, 2, 0), tile_code(0, 2, 1), tile_code(0, 2, 2));
+    case 3: return tiles3(tile_code(1, 2, 0), tile_code(1, 2, 1), tile_code(1, 2, 2));
+    case 4: return tiles3(tile_code(1, 3, 0), tile_code(0, 3, 1));
+    case 5: return tiles3(tile_code(1, 1, 1), tile_code(1, 3, 1));
+    case 6: return tiles3(tile_code(0, 3, 2), tile_code(0, 3, 3));
+    default: return tiles3(tile_code(1, 3, 2), tile_code(1, 3, 3));
+  }
+}
+
+constexpr int kPrepThreads = 512;
+constexpr int kPrepWaves = kPrepThreads / 64;
+constexpr int kPrepTokens = kC / kPrepWaves;   // tokens normalised per wave
 
 // ---- phase 1: per (chunk, v-head) ----------------------------------------------------
 template <bool DtBf16>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kPrepThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
                        const int32_t* chunk_start) {
   const int head = blockIdx.y;
@@ -166,12 +175,12 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   float* const sP = &sK[0][0];
 
   // q^ and k^ of the chunk's tokens (zero rows past its end); wave w does tokens
-  // 16w .. 16w+15, all 16 tokens' loads in flight before the first norm
+  // 8w .. 8w+7, all 8 tokens' loads in flight before the first norm
   {
-    uint16_t qr[16][2], kr[16][2];
+    uint16_t qr[kPrepTokens][2], kr[kPrepTokens][2];
 #pragma unroll
-    for (int ii = 0; ii < 16; ++ii) {
-      const int64_t tok = t0 + min(wave * 16 + ii, len - 1);
+    for (int ii = 0; ii < kPrepTokens; ++ii) {
+      const int64_t tok = t0 + min(wave * kPrepTokens + ii, len - 1);
       const uint16_t* row = p.qkv + tok * p.qkv_row;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
@@ -180,8 +189,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
     }
 #pragma unroll
-    for (int ii = 0; ii < 16; ++ii) {
-      const int i = wave * 16 + ii;
+    for (int ii = 0; ii < kPrepTokens; ++ii) {
+      const int i = wave * kPrepTokens + ii;
       float q[2], k[2];
       float qq = 0.0f, kk = 0.0f;
 #pragma unroll
@@ -226,11 +235,13 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   }
   __syncthreads();
 
-  // Waves 0, 1 solve for W's columns 64w .. 64w + 63, waves 2, 3 for U's.  U's right-hand
-  // side (beta_i v_i) comes from global memory: its loads go out before the products.
-  const bool solves_u = wave >= 2;
-  const int n0 = (wave & 1) * 64;
-  uint16_t vr[4][4][4];   // [row block][column tile][r]
+  // Waves 0-3 solve for W's columns 32w .. 32w + 31, waves 4-7 for U's (2 column tiles
+  // each).  U's right-hand side (beta_i v_i) comes from global memory: its loads go out
+  // before the products.
+  constexpr int kNt = 2;   // column tiles per wave
+  const bool solves_u = wave >= 4;
+  const int n0 = (wave & 3) * 16 * kNt;
+  uint16_t vr[4][kNt][4];   // [row block][column tile][r]
   if (solves_u) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
@@ -239,15 +250,18 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         const int64_t tok = t0 + min(16 * rb + 4 * lg + r, len - 1);
         const uint16_t* row = p.qkv + tok * p.qkv_row + v_col + n0 + li;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) vr[rb][nt][r] = row[16 * nt];
+        for (int nt = 0; nt < kNt; ++nt) vr[rb][nt][r] = row[16 * nt];
       }
   }
 
-  // A and P tiles: 32 steps of k (k = 32 lg + step) per tile
-  const uint32_t codes = wave == 0 ? kTiles0 : wave == 1 ? kTiles1 : wave == 2 ? kTiles2 : kTiles3;
-  f32x4 prod[5];
+  // A and P tiles: 32 steps of k (k = 32 lg + step) per tile; the third tile for waves
+  // 0-3 only (a uniform branch)
+  const uint32_t codes = prep_tiles(wave);
+  const int tiles = wave < 4 ? 3 : 2;
+  f32x4 prod[3];
 #pragma unroll
-  for (int t = 0; t < 5; ++t) {
+  for (int t = 0; t < 3; ++t) {
+    if (t >= tiles) break;
     const uint32_t code = (codes >> (5 * t)) & 31u;
     const int mt = (code >> 2) & 3;
     const int nt = code & 3;
@@ -268,7 +282,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 
   // the right-hand sides in the fragment layout: x[rb][nt][r] = B[16 rb + 4 lg + r][n0 + 16 nt + li]
   // (one uniform branch around two straight-line loops)
-  f32x4 x[4][4];
+  f32x4 x[4][kNt];
   if (solves_u) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
@@ -276,7 +290,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       for (int r = 0; r < 4; ++r) {
         const float beta = sBeta[16 * rb + 4 * lg + r];  // zero past the end
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) x[rb][nt][r] = beta * bf16_to_f32(vr[rb][nt][r]);
+        for (int nt = 0; nt < kNt; ++nt) x[rb][nt][r] = beta * bf16_to_f32(vr[rb][nt][r]);
       }
   } else {
 #pragma unroll
@@ -286,7 +300,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         const int i = 16 * rb + 4 * lg + r;
         const float wscale = sBeta[i] * sEg[i];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) x[rb][nt][r] = wscale * sK[i][n0 + 16 * nt + li];
+        for (int nt = 0; nt < kNt; ++nt) x[rb][nt][r] = wscale * sK[i][n0 + 16 * nt + li];
       }
   }
 
@@ -296,8 +310,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     f32x4* qdst = reinterpret_cast<f32x4*>(rec + kOffQg);
     f32x4* kdst = reinterpret_cast<f32x4*>(rec + kOffKd);
 #pragma unroll
-    for (int it = 0; it < kC * kDim / 4 / kThreads; ++it) {
-      const int item = it * kThreads + tid;
+    for (int it = 0; it < kC * kDim / 4 / kPrepThreads; ++it) {
+      const int item = it * kPrepThreads + tid;
       const int l = item & 63;
       const int i = 16 * (item >> 9) + (l & 15);
       const int k4 = 32 * (l >> 4) + 4 * ((item >> 6) & 7);
@@ -312,7 +326,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 
   // scale the tiles: A (negated) and P to LDS, P zero above the diagonal
 #pragma unroll
-  for (int t = 0; t < 5; ++t) {
+  for (int t = 0; t < 3; ++t) {
+    if (t >= tiles) break;
     const uint32_t code = (codes >> (5 * t)) & 31u;
     const int mt = (code >> 2) & 3;
     const int m = 16 * (code & 3) + li;
@@ -327,7 +342,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         sA[i * kARow + m] = m < i ? -(sBeta[i] * gam * prod[t][r]) : 0.0f;
     }
   }
-  for (int e = tid; e < kC * kC; e += kThreads) {
+  for (int e = tid; e < kC * kC; e += kPrepThreads) {
     const int i = e >> 6;
     const int m = e & 63;
     if ((m >> 4) > (i >> 4)) sP[i * kARow + m] = 0.0f;
@@ -338,8 +353,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   {
     f32x4* pdst = reinterpret_cast<f32x4*>(rec + kOffP);
 #pragma unroll
-    for (int it = 0; it < kC * kC / 4 / kThreads; ++it) {
-      const int item = it * kThreads + tid;
+    for (int it = 0; it < kC * kC / 4 / kPrepThreads; ++it) {
+      const int item = it * kPrepThreads + tid;
       const int l = item & 63;
       const int i = 16 * (item >> 8) + (l & 15);
       const int j = 16 * (l >> 4) + 4 * ((item >> 6) & 3);
@@ -347,16 +362,18 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     }
   }
   // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
-  if (lane < 16) {
+  // (block w by wave w < 4)
+  if (wave < 4 && lane < 16) {
     const float* ab = sA + (16 * wave) * kARow + 16 * wave;
+    // row by row: col[i] = delta(i, li) + sum over m < i of (-A)[i][m] col[m], the terms in
+    // order of m (row i of -A read as it is needed)
     float col[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) col[i] = i == li ? 1.0f : 0.0f;
+    for (int i = 0; i < 16; ++i) {
+      float acc = i == li ? 1.0f : 0.0f;
 #pragma unroll
-    for (int m = 0; m < 15; ++m) {
-      const float cm = col[m];
-#pragma unroll
-      for (int i = m + 1; i < 16; ++i) col[i] = fmaf(ab[i * kARow + m], cm, col[i]);
+      for (int m = 0; m < i; ++m) acc = fmaf(ab[i * kARow + m], col[m], acc);
+      col[i] = acc;
     }
     float* tb = sT + wave * 16 * kTRow;
 #pragma unroll
@@ -367,14 +384,14 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   // blocked forward substitution: X_rb = T_rb (B_rb - sum over j < rb of A_rb,j X_j)
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
-    f32x4 y[4];
+    f32x4 y[kNt];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) y[nt] = x[rb][nt];
+    for (int nt = 0; nt < kNt; ++nt) y[nt] = x[rb][nt];
 #pragma unroll
     for (int j = 0; j < rb; ++j) {
       const f32x4 a = *reinterpret_cast<const f32x4*>(sA + (16 * rb + li) * kARow + 16 * j + 4 * lg);
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
+      for (int nt = 0; nt < kNt; ++nt) {
         y[nt] = mfma(a.x, x[j][nt].x, y[nt]);
         y[nt] = mfma(a.y, x[j][nt].y, y[nt]);
         y[nt] = mfma(a.z, x[j][nt].z, y[nt]);
@@ -383,7 +400,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     }
     const f32x4 tr = *reinterpret_cast<const f32x4*>(sT + (rb * 16 + li) * kTRow + 4 * lg);
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int nt = 0; nt < kNt; ++nt) {
       f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
       acc = mfma(tr.x, y[nt].x, acc);
       acc = mfma(tr.y, y[nt].y, acc);
@@ -399,14 +416,14 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
+      for (int nt = 0; nt < kNt; ++nt)
         *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * 4 + rb) * 256 + lane * 4) =
             x[rb][nt];
   } else {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
+      for (int nt = 0; nt < kNt; ++nt)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           sW[(16 * rb + 4 * lg + r) * kRow + n0 + 16 * nt + li] = x[rb][nt][r];
@@ -415,8 +432,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   {
     f32x4* wdst = reinterpret_cast<f32x4*>(rec + kOffW);
 #pragma unroll
-    for (int it = 0; it < kC * kDim / 4 / kThreads; ++it) {
-      const int item = it * kThreads + tid;
+    for (int it = 0; it < kC * kDim / 4 / kPrepThreads; ++it) {
+      const int item = it * kPrepThreads + tid;
       const int l = item & 63;
       const int i = 16 * (item >> 9) + (l & 15);
       const int k4 = 32 * (l >> 4) + 4 * ((item >> 6) & 7);
@@ -763,10 +780,10 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, stream, p.cu, num_sequences,
                      chunk_start);
   if (dt_bf16)
-    hipLaunchKernelGGL(chunk_prep_kernel<true>, per_chunk, dim3(kThreads), 0, stream, p,
+    hipLaunchKernelGGL(chunk_prep_kernel<true>, per_chunk, dim3(kPrepThreads), 0, stream, p,
                        num_sequences, ws, chunk_start);
   else
-    hipLaunchKernelGGL(chunk_prep_kernel<false>, per_chunk, dim3(kThreads), 0, stream, p,
+    hipLaunchKernelGGL(chunk_prep_kernel<false>, per_chunk, dim3(kPrepThreads), 0, stream, p,
                        num_sequences, ws, chunk_start);
   static_assert(kScanBlocks == 8, "the scan's id mapping puts 8 row blocks on one XCD");
   const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
