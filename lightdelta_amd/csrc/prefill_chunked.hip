@@ -15,12 +15,12 @@
 //   chunk_prep_kernel  one workgroup per (chunk, v-head), all chunks in parallel: norms,
 //                      gates, A and P, the blocked forward substitution for W and U, and
 //                      the decayed q and k; everything to a workspace record.
-//   chunk_scan_kernel  one workgroup per (sequence, v-head, block of 16 state rows), the only
-//                      sequential part: chunk by chunk, V_new, the raw outputs of its 16
-//                      columns (rounded to bf16 into `out`, the reference's rounding point
-//                      before the gated RMSNorm, which prefill_norm_kernel applies
+//   chunk_scan_kernel  one workgroup per (sequence, v-head, block of 16 or 32 state rows),
+//                      the only sequential part: chunk by chunk, V_new, the raw outputs of
+//                      its columns (rounded to bf16 into `out`, the reference's rounding
+//                      point before the gated RMSNorm, which prefill_norm_kernel applies
 //                      afterwards) and the state update.  Rows evolve independently, so a
-//                      head's 128 rows spread over 8 workgroups.
+//                      head's 128 rows spread over 8 or 4 workgroups.
 //
 // MFMA fragments (16 x 16 x 4, wave64): for lane l, li = l % 16 and lg = l / 16.  One
 // instruction takes a = A[li][kk = lg] and b = B[kk = lg][li] from every lane and adds
@@ -33,8 +33,6 @@ namespace ld {
 namespace {
 
 constexpr int kC = 64;                          // tokens per chunk
-constexpr int kScanRows = 16;                   // state rows per scan workgroup
-constexpr int kScanBlocks = kDim / kScanRows;   // scan workgroups per (sequence, head)
 
 // Workspace record of one (chunk, v-head), offsets in floats.  Every operand of the scan is
 // stored in the order its loads read it -- [scan wave or tile][step group q][lane][4] -- so
@@ -442,17 +440,22 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   }
 }
 
-// ---- phase 2: per (sequence, v-head, block of 16 state rows), chunk by chunk ------------
+// ---- phase 2: per (sequence, v-head, block of 16 RT state rows), chunk by chunk --------
 // Eight waves, two per SIMD.  State wave w (0..3) owns k tiles 2w and 2w + 1 of the block's
 // S^T, forms V_new for tokens 16 w .. 16 w + 15 and updates its tiles; output wave w (4..7,
 // tokens 16 (w - 4) ..) forms the raw outputs.  Each SIMD carries one of each, so one
 // wave's waits (barriers, LDS, loads) leave the matrix core to the other.
+// RT = 1 or 2 row tiles of 16 state rows per workgroup: each operand a wave loads feeds RT
+// products, so with RT = 2 the chunk operands cross each CU half as often per product (for
+// many sequences, where the workgroups are plentiful); RT = 1 has twice the workgroups, for
+// few sequences, where the scan's latency is the time.
 constexpr int kScanThreads = 512;
 
+template <int RT>
 struct StateOperands {
   f32x4 w[8];      // W [16 w + li][32 lg + step]
   f32x4 kd[2][4];  // Kd^T [16 (2w + t) + li][16 lg + step]
-  f32x4 u;         // U [16 w + 4 lg + r][row0 + li]
+  f32x4 u[RT];     // U [16 w + 4 lg + r][row0 + 16 h + li]
   float gamma;     // exp(G_n-1)
 };
 
@@ -491,16 +494,19 @@ __device__ __forceinline__ float load4(__amdgpu_buffer_rsrc_t rsrc, int byte_off
 // every wave at the chunk's first barrier until the last of them was accepted).
 // State piece q < 4: W columns q and q + 4 (with U and gamma at q = 0); piece 4 + q: Kd^T
 // step group q of both tiles.  Output piece q < 4: Qg columns q and q + 4; piece 4 + q
-// (q < 2): P columns q and q + 2.
-__device__ __forceinline__ void load_state_piece(StateOperands& o, __amdgpu_buffer_rsrc_t rs,
-                                                 int w, uint32_t lane16, int row_block,
-                                                 int piece) {
+// (q < 2): P columns q and q + 2.  `tile0`: the workgroup's first 16-row tile of U.
+template <int RT>
+__device__ __forceinline__ void load_state_piece(StateOperands<RT>& o,
+                                                 __amdgpu_buffer_rsrc_t rs, int w,
+                                                 uint32_t lane16, int tile0, int piece) {
   if (piece < 4) {
     const int wbase = static_cast<int>(kOffW * 4) + w * 8 * 1024;
     o.w[piece] = load16(rs, lane16, wbase + piece * 1024);
     o.w[piece + 4] = load16(rs, lane16, wbase + (piece + 4) * 1024);
     if (piece == 0) {
-      o.u = load16(rs, lane16, static_cast<int>(kOffU * 4) + (row_block * 4 + w) * 1024);
+#pragma unroll
+      for (int h = 0; h < RT; ++h)
+        o.u[h] = load16(rs, lane16, static_cast<int>(kOffU * 4) + ((tile0 + h) * 4 + w) * 1024);
       o.gamma = load4(rs, static_cast<int>(kOffMisc * 4));
     }
   } else {
@@ -525,14 +531,18 @@ __device__ __forceinline__ void load_output_piece(OutputOperands& o, __amdgpu_bu
   }
 }
 
-// Every instruction kind but vector memory may be moved across (a sched_barrier mask).
-constexpr int kAllButVmem = 0x78F;
+// A sched_barrier mask for the step groups of the scan: vector and scalar ALU and LDS
+// instructions may be moved across, vector memory and matrix instructions stay in their
+// group.  (Matrix instructions allowed across let the compiler hoist every product above
+// the group's loads, which then went out at the end of the phase: 2.27 -> 2.06 ms at
+// 32 x 1024 with the group kept, 0.32 -> 0.31 ms at 1 x 4096.)
+constexpr int kLoadGroup = 0x386;
 
-// Chunks 0 .. chunks - 1 through the ring of three operand sets: step(op, fill, c) computes
-// chunk c from op and loads chunk c + 2 into fill.  Whole rounds of three run in a loop with
-// no exit inside it, the last one or two chunks after it.  (An exit between the steps of a
-// round joins the loop's latch, and the wait counts at the loop head then follow that
-// shorter path: the set prefetched for the next chunk was waited for a chunk early.)
+// Chunks 0 .. chunks - 1 through a ring of operand sets: step(op, fill, c) computes chunk c
+// from op and loads chunk c + (sets - 1) into fill.  Whole rounds of the ring run in a loop
+// with no exit inside it, the last chunks after it.  (An exit between the steps of a round
+// joins the loop's latch, and the wait counts at the loop head then follow that shorter
+// path: the set prefetched for the next chunk was waited for a chunk early.)
 template <class Step, class Operands>
 __device__ __forceinline__ void ring_scan(Step& step, Operands& ring0, Operands& ring1,
                                           Operands& ring2, int chunks) {
@@ -548,20 +558,38 @@ __device__ __forceinline__ void ring_scan(Step& step, Operands& ring0, Operands&
   }
 }
 
+template <class Step, class Operands>
+__device__ __forceinline__ void ring_scan(Step& step, Operands& ring0, Operands& ring1,
+                                          int chunks) {
+  int c = 0;
+  for (; c + 2 <= chunks; c += 2) {
+    step(ring0, ring1, c);
+    step(ring1, ring0, c + 1);
+  }
+  if (c < chunks) step(ring0, ring1, c);
+}
+
+template <int RT>
 __global__ __launch_bounds__(kScanThreads)
 void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
                        const int32_t* chunk_start, int records) {
-  // Workgroups go to the 8 XCDs round-robin by id.  The 8 row blocks of one (sequence,
-  // head) read the same chunk operands, so they are given ids on one XCD and share its L2:
-  // id = ((pair / 8) * 8 + block) * 8 + pair % 8.  The grid is padded to whole groups of 64.
+  constexpr int kRows = 16 * RT;              // state rows per workgroup
+  constexpr int kBlocks = kDim / kRows;       // workgroups per (sequence, head)
+  // operand sets in flight: three (two chunks ahead) for one row tile; two (one ahead) for
+  // two, whose accumulators and state tiles need the registers
+  constexpr int kSets = RT == 1 ? 3 : 2;
+  // Workgroups go to the 8 XCDs round-robin by id.  The row blocks of one (sequence, head)
+  // read the same chunk operands, so they are given ids on one XCD and share its L2:
+  // id = ((pair / 8) * kBlocks + block) * 8 + pair % 8.  The grid is padded to whole groups
+  // of 8 pairs.
   const int xcd = blockIdx.x & 7;
   const int rank = blockIdx.x >> 3;   // position among the XCD's workgroups
-  const int pair = (rank >> 3) * 8 + xcd;
+  const int pair = (rank / kBlocks) * 8 + xcd;
   if (pair >= num_sequences * p.num_v_heads) return;
   const int seq = pair / p.num_v_heads;
   const int head = pair - seq * p.num_v_heads;
-  const int row_block = rank & 7;
-  const int row0 = row_block * kScanRows;
+  const int row_block = rank % kBlocks;
+  const int row0 = row_block * kRows;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // the wave index in a scalar register: every operand address is then a scalar base plus
@@ -582,172 +610,218 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 
   constexpr int kSRow = kDim + 4;
   constexpr int kVRow = kC + 4;
-  __shared__ __attribute__((aligned(16))) float sS[kScanRows][kSRow];   // S rows [row][k]
-  __shared__ __attribute__((aligned(16))) float sVn[kScanRows][kVRow];  // V_new^T [row][token]
+  __shared__ __attribute__((aligned(16))) float sS[kRows][kSRow];   // S rows [row][k]
+  __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];  // V_new^T [row][token]
 
   auto record = [&](int c) {
     return ws + (static_cast<int64_t>(gbase + c) * p.num_v_heads + head) * kRecord;
   };
-  // B fragments of S^T for k = 32 lg + step (step = 4 q + e)
-  auto s_fragment = [&](int q) {
-    return *reinterpret_cast<const f32x4*>(&sS[li][32 * lg + 4 * q]);
+  // B fragments of S^T for k = 32 lg + step (step = 4 q + e), rows 16 h + li
+  auto s_fragment = [&](int h, int q) {
+    return *reinterpret_cast<const f32x4*>(&sS[16 * h + li][32 * lg + 4 * q]);
   };
-  // B fragments of V_new for j = 16 lg + step
-  auto vn_fragment = [&](int q) {
-    return *reinterpret_cast<const f32x4*>(&sVn[li][16 * lg + 4 * q]);
+  // B fragments of V_new for j = 16 lg + step, rows 16 h + li
+  auto vn_fragment = [&](int h, int q) {
+    return *reinterpret_cast<const f32x4*>(&sVn[16 * h + li][16 * lg + 4 * q]);
   };
 
   if (state_wave) {
-    // st[t][r] = S[row0 + li][16 (2w + t) + 4 lg + r]
+    // st[t][h][r] = S[row0 + 16 h + li][16 (2w + t) + 4 lg + r]
     float* tile_base = p.state + static_cast<int64_t>(slot) * p.state_slot +
                        static_cast<int64_t>(head) * kDim * kDim + (row0 + li) * kDim;
-    f32x4 st[2];
+    f32x4 st[2][RT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int k = 16 * (2 * w + t) + 4 * lg;
-      st[t] = from_slot ? *reinterpret_cast<const f32x4*>(tile_base + k)
-                        : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      *reinterpret_cast<f32x4*>(&sS[li][k]) = st[t];
-    }
-    // Operands of chunk c + 2 are loaded while chunk c computes, into a ring of three
-    // register sets (the loop is unrolled by three, so no set is copied: each is waited
-    // for only where it is used).
-    auto step = [&](const StateOperands& op, StateOperands& fill, int c) {
-      // fill: chunk c + 2, unconditionally (the last chunk's record again past the end: a
-      // branch around the loads would make the waits that follow conservative)
-      const __amdgpu_buffer_rsrc_t next = record_resource(record(min(c + 2, chunks - 1)));
+    for (int h = 0; h < RT; ++h)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int k = 16 * (2 * w + t) + 4 * lg;
+        st[t][h] = from_slot ? *reinterpret_cast<const f32x4*>(tile_base + 16 * h * kDim + k)
+                             : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        *reinterpret_cast<f32x4*>(&sS[16 * h + li][k]) = st[t][h];
+      }
+    // Operands of chunk c + kSets - 1 are loaded while chunk c computes, into a ring of
+    // register sets (the loop is unrolled by the ring's length, so no set is copied: each
+    // is waited for only where it is used).
+    auto step = [&](const StateOperands<RT>& op, StateOperands<RT>& fill, int c) {
+      // fill: unconditionally (the last chunk's record again past the end: a branch around
+      // the loads would make the waits that follow conservative)
+      const __amdgpu_buffer_rsrc_t next =
+          record_resource(record(min(c + kSets - 1, chunks - 1)));
       __syncthreads();  // sS holds the state at the chunk's start
-      // two accumulation chains (k < 64, k >= 64 of each lane group) so that consecutive
-      // matrix instructions do not wait on each other's results
-      f32x4 vn0 = {0.0f, 0.0f, 0.0f, 0.0f};
-      f32x4 vn1 = {0.0f, 0.0f, 0.0f, 0.0f};
+      // two accumulation chains per row tile (k < 64, k >= 64 of each lane group) so that
+      // consecutive matrix instructions do not wait on each other's results
+      f32x4 vn0[RT], vn1[RT];
+#pragma unroll
+      for (int h = 0; h < RT; ++h) {
+        vn0[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        vn1[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_state_piece(fill, next, w, lane16, row_block, q);
-        const f32x4 b0 = s_fragment(q);
-        const f32x4 b1 = s_fragment(q + 4);
-        vn0 = mfma(op.w[q].x, b0.x, vn0);
-        vn1 = mfma(op.w[q + 4].x, b1.x, vn1);
-        vn0 = mfma(op.w[q].y, b0.y, vn0);
-        vn1 = mfma(op.w[q + 4].y, b1.y, vn1);
-        vn0 = mfma(op.w[q].z, b0.z, vn0);
-        vn1 = mfma(op.w[q + 4].z, b1.z, vn1);
-        vn0 = mfma(op.w[q].w, b0.w, vn0);
-        vn1 = mfma(op.w[q + 4].w, b1.w, vn1);
-        __builtin_amdgcn_sched_barrier(kAllButVmem);
+        load_state_piece(fill, next, w, lane16, row_block * RT, q);
+#pragma unroll
+        for (int h = 0; h < RT; ++h) {
+          const f32x4 b0 = s_fragment(h, q);
+          const f32x4 b1 = s_fragment(h, q + 4);
+          vn0[h] = mfma(op.w[q].x, b0.x, vn0[h]);
+          vn1[h] = mfma(op.w[q + 4].x, b1.x, vn1[h]);
+          vn0[h] = mfma(op.w[q].y, b0.y, vn0[h]);
+          vn1[h] = mfma(op.w[q + 4].y, b1.y, vn1[h]);
+          vn0[h] = mfma(op.w[q].z, b0.z, vn0[h]);
+          vn1[h] = mfma(op.w[q + 4].z, b1.z, vn1[h]);
+          vn0[h] = mfma(op.w[q].w, b0.w, vn0[h]);
+          vn1[h] = mfma(op.w[q + 4].w, b1.w, vn1[h]);
+        }
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
       }
-      const f32x4 vn = op.u - (vn0 + vn1);
-      *reinterpret_cast<f32x4*>(&sVn[li][16 * w + 4 * lg]) = vn;
+#pragma unroll
+      for (int h = 0; h < RT; ++h) {
+        const f32x4 vn = op.u[h] - (vn0[h] + vn1[h]);
+        *reinterpret_cast<f32x4*>(&sVn[16 * h + li][16 * w + 4 * lg]) = vn;
+      }
       __syncthreads();  // V_new complete; every read of sS for this chunk done
 #pragma unroll
-      for (int t = 0; t < 2; ++t) st[t] *= op.gamma;
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int h = 0; h < RT; ++h) st[t][h] *= op.gamma;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_state_piece(fill, next, w, lane16, row_block, 4 + q);
-        const f32x4 b = vn_fragment(q);
+        load_state_piece(fill, next, w, lane16, row_block * RT, 4 + q);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          st[t] = mfma(op.kd[t][q].x, b.x, st[t]);
-          st[t] = mfma(op.kd[t][q].y, b.y, st[t]);
-          st[t] = mfma(op.kd[t][q].z, b.z, st[t]);
-          st[t] = mfma(op.kd[t][q].w, b.w, st[t]);
+        for (int h = 0; h < RT; ++h) {
+          const f32x4 b = vn_fragment(h, q);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            st[t][h] = mfma(op.kd[t][q].x, b.x, st[t][h]);
+            st[t][h] = mfma(op.kd[t][q].y, b.y, st[t][h]);
+            st[t][h] = mfma(op.kd[t][q].z, b.z, st[t][h]);
+            st[t][h] = mfma(op.kd[t][q].w, b.w, st[t][h]);
+          }
         }
-        __builtin_amdgcn_sched_barrier(kAllButVmem);
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
       }
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        *reinterpret_cast<f32x4*>(&sS[li][16 * (2 * w + t) + 4 * lg]) = st[t];
+      for (int h = 0; h < RT; ++h)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          *reinterpret_cast<f32x4*>(&sS[16 * h + li][16 * (2 * w + t) + 4 * lg]) = st[t][h];
     };
-    StateOperands ring0, ring1, ring2;
-    if (chunks > 0) {
-      // (piece by piece in the loop's order, so that the wait counts at the loop head are
-      // the same from either side)
-      const __amdgpu_buffer_rsrc_t r0 = record_resource(record(0));
-      const __amdgpu_buffer_rsrc_t r1 = record_resource(record(min(1, chunks - 1)));
+    // The first sets, piece by piece in the loop's order, so that the wait counts at the
+    // loop head are the same from either side.
+    auto prefill_set = [&](StateOperands<RT>& set, int c) {
+      const __amdgpu_buffer_rsrc_t r = record_resource(record(c));
 #pragma unroll
       for (int piece = 0; piece < 8; ++piece) {
-        load_state_piece(ring0, r0, w, lane16, row_block, piece);
+        load_state_piece(set, r, w, lane16, row_block * RT, piece);
         __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int piece = 0; piece < 8; ++piece) {
-        load_state_piece(ring1, r1, w, lane16, row_block, piece);
-        __builtin_amdgcn_sched_barrier(0);
+    };
+    StateOperands<RT> ring0, ring1;
+    if constexpr (kSets == 3) {
+      StateOperands<RT> ring2;
+      if (chunks > 0) {
+        prefill_set(ring0, 0);
+        prefill_set(ring1, min(1, chunks - 1));
       }
+      ring_scan(step, ring0, ring1, ring2, chunks);
+    } else {
+      if (chunks > 0) prefill_set(ring0, 0);
+      ring_scan(step, ring0, ring1, chunks);
     }
-    ring_scan(step, ring0, ring1, ring2, chunks);
     if (slot > 0) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        *reinterpret_cast<f32x4*>(tile_base + 16 * (2 * w + t) + 4 * lg) = st[t];
+      for (int h = 0; h < RT; ++h)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          *reinterpret_cast<f32x4*>(tile_base + 16 * h * kDim + 16 * (2 * w + t) + 4 * lg) =
+              st[t][h];
     }
   } else {
     const int out_row = p.num_v_heads * kDim;   // elements per token row of out
     uint16_t* out_block = p.out + static_cast<int64_t>(head) * kDim + row0;
     auto step = [&](const OutputOperands& op, OutputOperands& fill, int c) {
-      const __amdgpu_buffer_rsrc_t next = record_resource(record(min(c + 2, chunks - 1)));
+      const __amdgpu_buffer_rsrc_t next =
+          record_resource(record(min(c + kSets - 1, chunks - 1)));
       __syncthreads();  // sS holds the state at the chunk's start
-      f32x4 o0 = {0.0f, 0.0f, 0.0f, 0.0f};
-      f32x4 o1 = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 o0[RT], o1[RT];
+#pragma unroll
+      for (int h = 0; h < RT; ++h) {
+        o0[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        o1[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         load_output_piece(fill, next, w, lane16, q);
-        const f32x4 b0 = s_fragment(q);
-        const f32x4 b1 = s_fragment(q + 4);
-        o0 = mfma(op.qg[q].x, b0.x, o0);
-        o1 = mfma(op.qg[q + 4].x, b1.x, o1);
-        o0 = mfma(op.qg[q].y, b0.y, o0);
-        o1 = mfma(op.qg[q + 4].y, b1.y, o1);
-        o0 = mfma(op.qg[q].z, b0.z, o0);
-        o1 = mfma(op.qg[q + 4].z, b1.z, o1);
-        o0 = mfma(op.qg[q].w, b0.w, o0);
-        o1 = mfma(op.qg[q + 4].w, b1.w, o1);
-        __builtin_amdgcn_sched_barrier(kAllButVmem);
+#pragma unroll
+        for (int h = 0; h < RT; ++h) {
+          const f32x4 b0 = s_fragment(h, q);
+          const f32x4 b1 = s_fragment(h, q + 4);
+          o0[h] = mfma(op.qg[q].x, b0.x, o0[h]);
+          o1[h] = mfma(op.qg[q + 4].x, b1.x, o1[h]);
+          o0[h] = mfma(op.qg[q].y, b0.y, o0[h]);
+          o1[h] = mfma(op.qg[q + 4].y, b1.y, o1[h]);
+          o0[h] = mfma(op.qg[q].z, b0.z, o0[h]);
+          o1[h] = mfma(op.qg[q + 4].z, b1.z, o1[h]);
+          o0[h] = mfma(op.qg[q].w, b0.w, o0[h]);
+          o1[h] = mfma(op.qg[q + 4].w, b1.w, o1[h]);
+        }
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
       }
       __syncthreads();  // V_new complete
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         load_output_piece(fill, next, w, lane16, 4 + q);
-        const f32x4 b0 = vn_fragment(q);
-        const f32x4 b1 = vn_fragment(q + 2);
-        o0 = mfma(op.p[q].x, b0.x, o0);
-        o1 = mfma(op.p[q + 2].x, b1.x, o1);
-        o0 = mfma(op.p[q].y, b0.y, o0);
-        o1 = mfma(op.p[q + 2].y, b1.y, o1);
-        o0 = mfma(op.p[q].z, b0.z, o0);
-        o1 = mfma(op.p[q + 2].z, b1.z, o1);
-        o0 = mfma(op.p[q].w, b0.w, o0);
-        o1 = mfma(op.p[q + 2].w, b1.w, o1);
-        __builtin_amdgcn_sched_barrier(kAllButVmem);
+#pragma unroll
+        for (int h = 0; h < RT; ++h) {
+          const f32x4 b0 = vn_fragment(h, q);
+          const f32x4 b1 = vn_fragment(h, q + 2);
+          o0[h] = mfma(op.p[q].x, b0.x, o0[h]);
+          o1[h] = mfma(op.p[q + 2].x, b1.x, o1[h]);
+          o0[h] = mfma(op.p[q].y, b0.y, o0[h]);
+          o1[h] = mfma(op.p[q + 2].y, b1.y, o1[h]);
+          o0[h] = mfma(op.p[q].z, b0.z, o0[h]);
+          o1[h] = mfma(op.p[q + 2].z, b1.z, o1[h]);
+          o0[h] = mfma(op.p[q].w, b0.w, o0[h]);
+          o1[h] = mfma(op.p[q + 2].w, b1.w, o1[h]);
+        }
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
       }
-      const f32x4 o = o0 + o1;
-      // raw outputs of tokens 16 w + 4 lg + r, column row0 + li, through a buffer over the
-      // chunk's rows of out: rows past the sequence's end fall outside it and are dropped
+      // raw outputs of tokens 16 w + 4 lg + r, column row0 + 16 h + li, through a buffer
+      // over the chunk's rows of out: rows past the sequence's end fall outside it and are
+      // dropped
       const int t0 = bos + c * kC;
       const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
           out_block + static_cast<int64_t>(t0) * out_row, 0, min(kC, eos - t0) * out_row * 2,
           0x00020000);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        __builtin_amdgcn_raw_buffer_store_b16(to_bf16(o[r]), ors,
-                                              ((16 * w + 4 * lg + r) * out_row + li) * 2, 0, 0);
+      for (int h = 0; h < RT; ++h) {
+        const f32x4 o = o0[h] + o1[h];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          __builtin_amdgcn_raw_buffer_store_b16(
+              to_bf16(o[r]), ors, ((16 * w + 4 * lg + r) * out_row + 16 * h + li) * 2, 0, 0);
+      }
     };
-    OutputOperands ring0, ring1, ring2;
-    if (chunks > 0) {
-      const __amdgpu_buffer_rsrc_t r0 = record_resource(record(0));
-      const __amdgpu_buffer_rsrc_t r1 = record_resource(record(min(1, chunks - 1)));
+    auto prefill_set = [&](OutputOperands& set, int c) {
+      const __amdgpu_buffer_rsrc_t r = record_resource(record(c));
 #pragma unroll
       for (int piece = 0; piece < 6; ++piece) {
-        load_output_piece(ring0, r0, w, lane16, piece);
+        load_output_piece(set, r, w, lane16, piece);
         __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int piece = 0; piece < 6; ++piece) {
-        load_output_piece(ring1, r1, w, lane16, piece);
-        __builtin_amdgcn_sched_barrier(0);
+    };
+    OutputOperands ring0, ring1;
+    if constexpr (kSets == 3) {
+      OutputOperands ring2;
+      if (chunks > 0) {
+        prefill_set(ring0, 0);
+        prefill_set(ring1, min(1, chunks - 1));
       }
+      ring_scan(step, ring0, ring1, ring2, chunks);
+    } else {
+      if (chunks > 0) prefill_set(ring0, 0);
+      ring_scan(step, ring0, ring1, chunks);
     }
-    ring_scan(step, ring0, ring1, ring2, chunks);
   }
 }
 
@@ -785,12 +859,19 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   else
     hipLaunchKernelGGL(chunk_prep_kernel<false>, per_chunk, dim3(kPrepThreads), 0, stream, p,
                        num_sequences, ws, chunk_start);
-  static_assert(kScanBlocks == 8, "the scan's id mapping puts 8 row blocks on one XCD");
   const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
-  const int64_t scan_tiles = (pairs + 7) / 8 * 64;
-  if (scan_tiles > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
-  hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<uint32_t>(scan_tiles)), dim3(kScanThreads), 0,
-                     stream, p, num_sequences, ws, chunk_start, static_cast<int>(chunks));
+  // two row tiles per workgroup once they still give 2 workgroups per CU
+  const bool two_tiles = pairs * (kDim / 32) >= 512;
+  const int64_t scan_groups = (pairs + 7) / 8 * 8 * (two_tiles ? kDim / 32 : kDim / 16);
+  if (scan_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
+  if (two_tiles)
+    hipLaunchKernelGGL(chunk_scan_kernel<2>, dim3(static_cast<uint32_t>(scan_groups)),
+                       dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
+                       static_cast<int>(chunks));
+  else
+    hipLaunchKernelGGL(chunk_scan_kernel<1>, dim3(static_cast<uint32_t>(scan_groups)),
+                       dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
+                       static_cast<int>(chunks));
   return check_launch("ld_gdn_prefill (chunked)");
 }
 
