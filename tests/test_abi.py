@@ -147,8 +147,9 @@ def test_prefill_workspace_query_and_chunked_without_workspace():
     (4096, 1, 32, 1),        # one long prompt
     (32 * 1024, 32, 32, 1),  # long prompts that fill the GPU anyway
     (16 * 128, 16, 32, 1),   # 128-token prompts, 512 (sequence, head) tiles
-    (64 * 64, 64, 32, 0),    # 64-token prompts, 2048 tiles: token-serial fills the GPU
+    (512 * 64, 512, 32, 1),  # 64-token prompts, 16384 tiles
     (4 * 64, 4, 32, 1),
+    (512 * 63, 512, 32, 0),  # a mean just under one chunk
     (1024 * 32, 1024, 32, 0),  # short prompts
     (2 * 16, 2, 32, 0),
     (0, 1, 32, 0),
