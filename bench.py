@@ -25,7 +25,7 @@ in the 256 MB Infinity Cache between consecutive steps.  A second, cache-cold fi
 (non-temporal state traffic), the regime of a many-layer model.
 
 Further figures in the same line: `conv_fused` (the same step with the width-4 causal
-conv1d + SiLU fused in front), `prefill` (32 x 1024 and 1 x 4096 tokens, both algorithms),
+conv1d + SiLU fused in front), `prefill` (32 x 1024, 1 x 4096 and 1024 x 32 tokens, both algorithms),
 `mtp_verify` (B=64, T=4 verify plus the commit at a random accepted length), `copies`
 (gather / scatter / slot-to-slot copy of 128 random pairs in a 1024-slot pool, and the bf16
 conv pool) and `stack48` (48 layers captured as one HIP graph, batch 128, 1024 slots per
@@ -203,9 +203,10 @@ def conv_fused(case, op_args, steps, device):
 
 
 def prefill(device):
-    """Prefill of 32 prompts x 1024 tokens and of one 4096-token prompt (16 qk / 32 v heads,
-    states from slots of a 64-slot pool), timed over a few eager launches each, under both
-    algorithms (token-serial recurrence; 64-token chunks in the WY form on the matrix cores)."""
+    """Prefill of 32 prompts x 1024 tokens, of one 4096-token prompt and of 1024 prompts x 32
+    tokens (16 qk / 32 v heads, states from pool slots), timed over a few eager launches
+    each, under both algorithms (token-serial recurrence; 64-token chunks in the WY form on
+    the matrix cores); `auto_selects` is the form the default picks."""
     import torch
 
     from lightdelta_amd import _lib, ops
@@ -216,7 +217,8 @@ def prefill(device):
     qkv_cols = (2 * H + HV) * DIM
     result = {}
     saved = ops.prefill_algorithm()
-    for label, seqs, length in (("batch_32x1024", 32, 1024), ("single_4096", 1, 4096)):
+    for label, seqs, length in (("batch_32x1024", 32, 1024), ("single_4096", 1, 4096),
+                                ("short_1024x32", 1024, 32)):
         total = seqs * length
         qkvz = torch.randn(total, qkv_cols + HV * DIM, generator=gen, device=device).bfloat16()
         ba = torch.randn(total, 2 * HV, generator=gen, device=device).bfloat16()
