@@ -25,8 +25,8 @@ in the 256 MB Infinity Cache between consecutive steps.  A second, cache-cold fi
 (non-temporal state traffic), the regime of a many-layer model.
 
 Further figures in the same line: `conv_fused` (the same step with the width-4 causal
-conv1d + SiLU fused in front), `prefill` (32 x 1024, 1 x 4096 and 1024 x 32 tokens, both algorithms),
-`mtp_verify` (B=64, T=4 verify plus the commit at a random accepted length), `copies`
+conv1d + SiLU fused in front), `prefill` (32 x 1024, 1 x 4096 and 1024 x 32 tokens, both
+algorithms), `mtp_verify` (B=64, T=4 verify plus the commit at a random accepted length), `copies`
 (gather / scatter / slot-to-slot copy of 128 random pairs in a 1024-slot pool, and the bf16
 conv pool) and `stack48` (48 layers captured as one HIP graph, batch 128, 1024 slots per
 layer = 96 GiB of state, slot ids reshuffled before every replay, 256 replays timed end to
