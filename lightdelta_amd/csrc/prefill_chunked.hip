@@ -538,8 +538,8 @@ __device__ __forceinline__ void load_output_piece(OutputOperands& o, __amdgpu_bu
 // 32 x 1024 with the group kept, 0.32 -> 0.31 ms at 1 x 4096.)
 constexpr int kLoadGroup = 0x386;
 
-// Chunks 0 .. chunks - 1 through a ring of operand sets: step(op, fill, c) computes chunk c
-// from op and loads chunk c + (sets - 1) into fill.  Whole rounds of the ring run in a loop
+// Chunks 0 .. chunks - 1 through a ring of three operand sets: step(op, fill, c) computes
+// chunk c from op and loads chunk c + 2 into fill.  Whole rounds of the ring run in a loop
 // with no exit inside it, the last chunks after it.  (An exit between the steps of a round
 // joins the loop's latch, and the wait counts at the loop head then follow that shorter
 // path: the set prefetched for the next chunk was waited for a chunk early.)
@@ -558,26 +558,19 @@ __device__ __forceinline__ void ring_scan(Step& step, Operands& ring0, Operands&
   }
 }
 
-template <class Step, class Operands>
-__device__ __forceinline__ void ring_scan(Step& step, Operands& ring0, Operands& ring1,
-                                          int chunks) {
-  int c = 0;
-  for (; c + 2 <= chunks; c += 2) {
-    step(ring0, ring1, c);
-    step(ring1, ring0, c + 1);
-  }
-  if (c < chunks) step(ring0, ring1, c);
-}
-
 template <int RT>
 __global__ __launch_bounds__(kScanThreads)
 void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
                        const int32_t* chunk_start, int records) {
   constexpr int kRows = 16 * RT;              // state rows per workgroup
   constexpr int kBlocks = kDim / kRows;       // workgroups per (sequence, head)
-  // operand sets in flight: three (two chunks ahead) for one row tile; two (one ahead) for
-  // two, whose accumulators and state tiles need the registers
-  constexpr int kSets = RT == 1 ? 3 : 2;
+  // Operand sets: three for one row tile (the whole set of chunk c + 2 loaded while chunk c
+  // computes); one for two row tiles, refilled piece by piece half a chunk ahead (the Kd
+  // pieces of chunk c during its V_new products, the W, U and gamma pieces of chunk c + 1
+  // during its update), which leaves the registers for two workgroups per CU (98 VGPRs;
+  // 1% faster at 32 x 1024 than two sets a chunk ahead at 162).
+  constexpr int kSets = RT == 1 ? 3 : 1;
+  constexpr bool kHalf = kSets == 1;
   // Workgroups go to the 8 XCDs round-robin by id.  The row blocks of one (sequence, head)
   // read the same chunk operands, so they are given ids on one XCD and share its L2:
   // id = ((pair / 8) * kBlocks + block) * 8 + pair % 8.  The grid is padded to whole groups
@@ -639,14 +632,15 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
                              : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         *reinterpret_cast<f32x4*>(&sS[16 * h + li][k]) = st[t][h];
       }
-    // Operands of chunk c + kSets - 1 are loaded while chunk c computes, into a ring of
-    // register sets (the loop is unrolled by the ring's length, so no set is copied: each
-    // is waited for only where it is used).
+    // Operands of later chunks are loaded while chunk c computes: into a ring of three
+    // register sets (the loop is unrolled by three, so no set is copied: each is waited for
+    // only where it is used), or into the one set as its pieces fall free.
     auto step = [&](const StateOperands<RT>& op, StateOperands<RT>& fill, int c) {
       // fill: unconditionally (the last chunk's record again past the end: a branch around
       // the loads would make the waits that follow conservative)
       const __amdgpu_buffer_rsrc_t next =
-          record_resource(record(min(c + kSets - 1, chunks - 1)));
+          record_resource(record(min(c + (kHalf ? 1 : 2), chunks - 1)));
+      const __amdgpu_buffer_rsrc_t cur = kHalf ? record_resource(record(c)) : next;
       __syncthreads();  // sS holds the state at the chunk's start
       // two accumulation chains per row tile (k < 64, k >= 64 of each lane group) so that
       // consecutive matrix instructions do not wait on each other's results
@@ -658,7 +652,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_state_piece(fill, next, w, lane16, row_block * RT, q);
+        load_state_piece(fill, cur, w, lane16, row_block * RT, kHalf ? 4 + q : q);
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b0 = s_fragment(h, q);
@@ -686,7 +680,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         for (int h = 0; h < RT; ++h) st[t][h] *= op.gamma;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_state_piece(fill, next, w, lane16, row_block * RT, 4 + q);
+        load_state_piece(fill, next, w, lane16, row_block * RT, kHalf ? q : 4 + q);
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b = vn_fragment(h, q);
@@ -716,17 +710,24 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    StateOperands<RT> ring0, ring1;
+    StateOperands<RT> ring0;
     if constexpr (kSets == 3) {
-      StateOperands<RT> ring2;
+      StateOperands<RT> ring1, ring2;
       if (chunks > 0) {
         prefill_set(ring0, 0);
         prefill_set(ring1, min(1, chunks - 1));
       }
       ring_scan(step, ring0, ring1, ring2, chunks);
     } else {
-      if (chunks > 0) prefill_set(ring0, 0);
-      ring_scan(step, ring0, ring1, chunks);
+      if (chunks > 0) {
+        const __amdgpu_buffer_rsrc_t r = record_resource(record(0));
+#pragma unroll
+        for (int piece = 0; piece < 4; ++piece) {
+          load_state_piece(ring0, r, w, lane16, row_block * RT, piece);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      for (int c = 0; c < chunks; ++c) step(ring0, ring0, c);
     }
     if (slot > 0) {
 #pragma unroll
@@ -741,7 +742,8 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     uint16_t* out_block = p.out + static_cast<int64_t>(head) * kDim + row0;
     auto step = [&](const OutputOperands& op, OutputOperands& fill, int c) {
       const __amdgpu_buffer_rsrc_t next =
-          record_resource(record(min(c + kSets - 1, chunks - 1)));
+          record_resource(record(min(c + (kHalf ? 1 : 2), chunks - 1)));
+      const __amdgpu_buffer_rsrc_t cur = kHalf ? record_resource(record(c)) : next;
       __syncthreads();  // sS holds the state at the chunk's start
       f32x4 o0[RT], o1[RT];
 #pragma unroll
@@ -751,7 +753,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_output_piece(fill, next, w, lane16, q);
+        if (!kHalf)
+          load_output_piece(fill, next, w, lane16, q);
+        else if (q < 2)
+          load_output_piece(fill, cur, w, lane16, 4 + q);   // P of this chunk
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b0 = s_fragment(h, q);
@@ -770,7 +775,12 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       __syncthreads();  // V_new complete
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        load_output_piece(fill, next, w, lane16, 4 + q);
+        if (!kHalf) {
+          load_output_piece(fill, next, w, lane16, 4 + q);
+        } else {   // Qg of the next chunk
+          load_output_piece(fill, next, w, lane16, 2 * q);
+          load_output_piece(fill, next, w, lane16, 2 * q + 1);
+        }
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b0 = vn_fragment(h, q);
@@ -810,17 +820,24 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    OutputOperands ring0, ring1;
+    OutputOperands ring0;
     if constexpr (kSets == 3) {
-      OutputOperands ring2;
+      OutputOperands ring1, ring2;
       if (chunks > 0) {
         prefill_set(ring0, 0);
         prefill_set(ring1, min(1, chunks - 1));
       }
       ring_scan(step, ring0, ring1, ring2, chunks);
     } else {
-      if (chunks > 0) prefill_set(ring0, 0);
-      ring_scan(step, ring0, ring1, chunks);
+      if (chunks > 0) {
+        const __amdgpu_buffer_rsrc_t r = record_resource(record(0));
+#pragma unroll
+        for (int piece = 0; piece < 4; ++piece) {
+          load_output_piece(ring0, r, w, lane16, piece);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      for (int c = 0; c < chunks; ++c) step(ring0, ring0, c);
     }
   }
 }
