@@ -202,7 +202,7 @@ int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream);
 
 /*
  * Workspace bytes the chunked prefill needs for num_tokens rows in num_sequences sequences
- * and num_v_heads heads: one 147,712-byte record per chunk of 64 tokens and head (chunks
+ * and num_v_heads heads: one 115,712-byte record per chunk of 64 tokens and head (chunks
  * bounded by num_tokens / 64 + num_sequences), then a chunk index of num_sequences + 1
  * int32 rounded up to 256 bytes.  0 for negative arguments.
  */

@@ -14,7 +14,8 @@
 // float64: 7e-8 relative on the state).  Two launches:
 //   chunk_prep_kernel  one workgroup per (chunk, v-head), all chunks in parallel: norms,
 //                      gates, A and P, the blocked forward substitution for W and U, and
-//                      the decayed q and k; everything to a workspace record.
+//                      q and k with their per-token scales; everything to a workspace
+//                      record.
 //   chunk_scan_kernel  one workgroup per (sequence, v-head, block of 16 or 32 state rows),
 //                      the only sequential part: chunk by chunk, V_new, the raw outputs of
 //                      its columns (rounded to bf16 into `out`, the reference's rounding
@@ -35,21 +36,43 @@ namespace {
 constexpr int kC = 64;                          // tokens per chunk
 
 // Workspace record of one (chunk, v-head), offsets in floats.  Every operand of the scan is
-// stored in the order its loads read it -- [scan wave or tile][step group q][lane][4] -- so
-// that one 16-byte-per-lane load of a wave reads 1 KiB of consecutive memory.  With li, lg
-// the lane's fragment coordinates:
-//   W   [w][q < 8][lane][e] = W[16 w + li][32 lg + 4 q + e]        (W: 64 token x 128 k)
-//   Qg  [w][q < 8][lane][e] = q^_i exp(G_i) at the same positions
-//   U   [b][w][lane][r]     = U[16 w + 4 lg + r][16 b + li]         (b: block of 16 v rows)
-//   Kd  [t][q < 4][lane][e] = k^_j exp(G_n-1 - G_j) for j = 16 lg + 4 q + e, k = 16 t + li
-//   P   [w][q < 4][lane][e] = P[16 w + li][16 lg + 4 q + e]
+// stored in the order its loads read it -- [scan wave or tile][step group][lane][16 bytes]
+// -- so that one 16-byte-per-lane load of a wave reads 1 KiB of consecutive memory.  q and
+// k go as the bf16 inputs themselves (exact), their norms and decays as per-token scales
+// applied by the scan.  With li, lg the lane's fragment coordinates:
+//   W    [w][q < 8][lane][e]  = W[16 w + li][32 lg + 4 q + e]       (W: 64 token x 128 k)
+//   U    [b][w][lane][r]      = U[16 w + 4 lg + r][16 b + li]        (b: block of 16 v rows)
+//   P    [w][q < 4][lane][e]  = P[16 w + li][16 lg + 4 q + e]
+//   Qr   [w][qq < 4][lane][e < 8] = q_i[32 lg + 8 qq + e] (bf16), i = 16 w + li
+//   Kr   [t][qq < 2][lane][e < 8] = k_j[16 t + li] (bf16), j = 16 lg + 8 qq + e
+//   misc [0] exp(G_n-1); [64 + i] sq_i = rq_i scale exp(G_i); [128 + j] ck_j = rk_j exp(G_n-1 - G_j)
+// with rq, rk the inverse L2 norms; rows past the chunk's end hold zeros.  So the scan's
+// operands are Qg = diag(sq) Qr (applied to the product's rows) and Kd = diag(ck) Kr
+// (applied to V_new's rows in the update).
 constexpr int64_t kOffW = 0;
-constexpr int64_t kOffQg = kOffW + kC * kDim;
-constexpr int64_t kOffU = kOffQg + kC * kDim;
-constexpr int64_t kOffKd = kOffU + kDim * kC;
-constexpr int64_t kOffP = kOffKd + kDim * kC;
-constexpr int64_t kOffMisc = kOffP + kC * kC;        // [0] exp(G_n-1)
-constexpr int64_t kRecord = kOffMisc + 64;           // floats (a multiple of 64: 256 B)
+constexpr int64_t kOffU = kOffW + kC * kDim;
+constexpr int64_t kOffP = kOffU + kDim * kC;
+constexpr int64_t kOffQr = kOffP + kC * kC;          // bf16 pairs: kC * kDim / 2 floats
+constexpr int64_t kOffKr = kOffQr + kC * kDim / 2;
+constexpr int64_t kOffMisc = kOffKr + kC * kDim / 2;
+constexpr int64_t kMiscSq = 64;
+constexpr int64_t kMiscCk = 128;
+constexpr int64_t kRecord = kOffMisc + 256;          // floats (a multiple of 64: 256 B)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 values held exactly in fp32, two to a word (lo, hi)
+__device__ __forceinline__ uint32_t pack_bf16_exact(float lo, float hi) {
+  return (__builtin_bit_cast(uint32_t, lo) >> 16) | (__builtin_bit_cast(uint32_t, hi) & 0xffff0000u);
+}
+
+// four consecutive bf16 of a 16-byte piece (half 0: elements 0..3, half 1: 4..7) as fp32
+__device__ __forceinline__ f32x4 bf16x4(const u32x4& v, int half) {
+  const uint32_t a = half ? v.z : v.x;
+  const uint32_t b = half ? v.w : v.y;
+  return f32x4{__builtin_bit_cast(float, a << 16), __builtin_bit_cast(float, a & 0xffff0000u),
+               __builtin_bit_cast(float, b << 16), __builtin_bit_cast(float, b & 0xffff0000u)};
+}
 
 __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -158,22 +181,24 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   constexpr int kRow = kDim + 4;   // padded LDS row (floats)
   constexpr int kARow = kC + 4;    // padded LDS row of -A
   constexpr int kTRow = 20;        // padded LDS row of a diagonal block's inverse
-  // sQ holds q^ until A and P are formed, then -A [64][68] and the four inverses
-  // [4][16][20]; sK holds k^, then P [64][68], then W [64][132], each on its way to the
-  // workspace.
+  // sQ holds q (the bf16 inputs, exactly) until A and P are formed, then -A [64][68] and the
+  // four inverses [4][16][20]; sK holds k, then P [64][68], then W [64][132], each on its
+  // way to the workspace.
   __shared__ __attribute__((aligned(16))) float sQ[kC][kRow];
   __shared__ __attribute__((aligned(16))) float sK[kC][kRow];
   __shared__ float sG[kC];
   __shared__ float sBeta[kC];
   __shared__ float sEg[kC];     // exp(G_i)
   __shared__ float sEk[kC];     // exp(G_n-1 - G_i)
+  __shared__ float sRq[kC];     // rq_i scale (zero past the end)
+  __shared__ float sRk[kC];     // rk_i (zero past the end)
   float* const sA = &sQ[0][0];
   float* const sT = &sQ[0][0] + kC * kARow;
   float* const sW = &sK[0][0];
   float* const sP = &sK[0][0];
 
-  // q^ and k^ of the chunk's tokens (zero rows past its end); wave w does tokens
-  // 8w .. 8w+7, all 8 tokens' loads in flight before the first norm
+  // q and k of the chunk's tokens and their inverse norms (zero rows past its end); wave w
+  // does tokens 8w .. 8w+7, all 8 tokens' loads in flight before the first norm
   {
     uint16_t qr[kPrepTokens][2], kr[kPrepTokens][2];
 #pragma unroll
@@ -205,8 +230,12 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       const float rk = fast_rsqrt(kk + 1e-6f);
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        sQ[i][2 * lane + e] = live ? (q[e] * rq) * p.scale : 0.0f;
-        sK[i][2 * lane + e] = live ? k[e] * rk : 0.0f;
+        sQ[i][2 * lane + e] = live ? q[e] : 0.0f;
+        sK[i][2 * lane + e] = live ? k[e] : 0.0f;
+      }
+      if (lane == 0) {
+        sRq[i] = live ? rq * p.scale : 0.0f;
+        sRk[i] = live ? rk : 0.0f;
       }
     }
   }
@@ -296,31 +325,40 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * rb + 4 * lg + r;
-        const float wscale = sBeta[i] * sEg[i];
+        const float wscale = sBeta[i] * sEg[i] * sRk[i];
 #pragma unroll
         for (int nt = 0; nt < kNt; ++nt) x[rb][nt][r] = wscale * sK[i][n0 + 16 * nt + li];
       }
   }
 
-  // Qg and Kd to the workspace while q^ and k^ are still in LDS (item = one 16-byte piece
-  // of the record's order: [w or t][q][lane])
+  // Qr and Kr (the bf16 inputs, repacked in the scan's load order) and the per-token scales
+  // to the workspace while q and k are still in LDS (item = one 16-byte piece)
   {
-    f32x4* qdst = reinterpret_cast<f32x4*>(rec + kOffQg);
-    f32x4* kdst = reinterpret_cast<f32x4*>(rec + kOffKd);
+    u32x4* qdst = reinterpret_cast<u32x4*>(rec + kOffQr);
+    u32x4* kdst = reinterpret_cast<u32x4*>(rec + kOffKr);
 #pragma unroll
-    for (int it = 0; it < kC * kDim / 4 / kPrepThreads; ++it) {
+    for (int it = 0; it < kC * kDim / 8 / kPrepThreads; ++it) {
       const int item = it * kPrepThreads + tid;
       const int l = item & 63;
-      const int i = 16 * (item >> 9) + (l & 15);
-      const int k4 = 32 * (l >> 4) + 4 * ((item >> 6) & 7);
-      qdst[item] = *reinterpret_cast<const f32x4*>(&sQ[i][k4]) * sEg[i];
-      const int k = 16 * (item >> 8) + (l & 15);
-      const int j = 16 * (l >> 4) + 4 * ((item >> 6) & 3);
-      kdst[item] = f32x4{sK[j][k] * sEk[j], sK[j + 1][k] * sEk[j + 1], sK[j + 2][k] * sEk[j + 2],
-                         sK[j + 3][k] * sEk[j + 3]};  // zero rows past the end
+      const int i = 16 * (item >> 8) + (l & 15);
+      const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&sQ[i][c0]);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&sQ[i][c0 + 4]);
+      qdst[item] = u32x4{pack_bf16_exact(a.x, a.y), pack_bf16_exact(a.z, a.w),
+                         pack_bf16_exact(b.x, b.y), pack_bf16_exact(b.z, b.w)};
+      const int k = 16 * (item >> 7) + (l & 15);
+      const int j = 16 * (l >> 4) + 8 * ((item >> 6) & 1);
+      kdst[item] = u32x4{pack_bf16_exact(sK[j][k], sK[j + 1][k]),
+                         pack_bf16_exact(sK[j + 2][k], sK[j + 3][k]),
+                         pack_bf16_exact(sK[j + 4][k], sK[j + 5][k]),
+                         pack_bf16_exact(sK[j + 6][k], sK[j + 7][k])};
     }
+    if (tid < kC)
+      rec[kOffMisc + kMiscSq + tid] = sRq[tid] * sEg[tid];
+    else if (tid < 2 * kC)
+      rec[kOffMisc + kMiscCk + tid - kC] = sRk[tid - kC] * sEk[tid - kC];
   }
-  __syncthreads();  // q^ and k^ no longer read
+  __syncthreads();  // q and k no longer read
 
   // scale the tiles: A (negated) and P to LDS, P zero above the diagonal
 #pragma unroll
@@ -330,14 +368,16 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     const int mt = (code >> 2) & 3;
     const int m = 16 * (code & 3) + li;
     const float gm = sG[m];
+    const float rkm = sRk[m];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 16 * mt + 4 * lg + r;
       const float gam = __expf(sG[i] - gm);
+      // the products are of the raw inputs: q^_i . k^_m = (rq_i scale rk_m) (q_i . k_m)
       if (code & 16u)
-        sP[i * kARow + m] = (m <= i && i < len) ? gam * prod[t][r] : 0.0f;
+        sP[i * kARow + m] = (m <= i && i < len) ? gam * ((sRq[i] * rkm) * prod[t][r]) : 0.0f;
       else
-        sA[i * kARow + m] = m < i ? -(sBeta[i] * gam * prod[t][r]) : 0.0f;
+        sA[i * kARow + m] = m < i ? -(sBeta[i] * gam * ((sRk[i] * rkm) * prod[t][r])) : 0.0f;
     }
   }
   for (int e = tid; e < kC * kC; e += kPrepThreads) {
@@ -454,13 +494,15 @@ constexpr int kScanThreads = 512;
 template <int RT>
 struct StateOperands {
   f32x4 w[8];      // W [16 w + li][32 lg + step]
-  f32x4 kd[2][4];  // Kd^T [16 (2w + t) + li][16 lg + step]
+  u32x4 kr[2][2];  // Kr^T [16 (2w + t) + li][16 lg + 8 qq + e] (bf16)
   f32x4 u[RT];     // U [16 w + 4 lg + r][row0 + 16 h + li]
+  f32x4 ck;        // ck of tokens 16 w + 4 lg + r
   float gamma;     // exp(G_n-1)
 };
 
 struct OutputOperands {
-  f32x4 qg[8];     // Qg [16 w + li][32 lg + step]
+  u32x4 qr[4];     // Qr [16 w + li][32 lg + 8 qq + e] (bf16)
+  f32x4 sq;        // sq of tokens 16 w + 4 lg + r
   f32x4 p[4];      // P [16 w + li][16 lg + step]
 };
 
@@ -485,6 +527,12 @@ __device__ __forceinline__ f32x4 load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t la
       f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(lane16), byte_offset, 0));
 }
 
+__device__ __forceinline__ u32x4 load16u(__amdgpu_buffer_rsrc_t rsrc, uint32_t lane16,
+                                         int byte_offset) {
+  return __builtin_bit_cast(
+      u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(lane16), byte_offset, 0));
+}
+
 __device__ __forceinline__ float load4(__amdgpu_buffer_rsrc_t rsrc, int byte_offset) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, 0, byte_offset, 0));
 }
@@ -492,13 +540,15 @@ __device__ __forceinline__ float load4(__amdgpu_buffer_rsrc_t rsrc, int byte_off
 // The operand loads of one chunk come in pieces that the scan issues between its products,
 // a few at a time (issued in one burst at the top of a chunk, the CU's 116 loads would hold
 // every wave at the chunk's first barrier until the last of them was accepted).
-// State piece q < 4: W columns q and q + 4 (with U and gamma at q = 0); piece 4 + q: Kd^T
-// step group q of both tiles.  Output piece q < 4: Qg columns q and q + 4; piece 4 + q
-// (q < 2): P columns q and q + 2.  `tile0`: the workgroup's first 16-row tile of U.
+// State piece q < 4: W columns q and q + 4 (with U, ck and gamma at q = 0); piece 4 + q:
+// Kr of tile 2w + (q & 1), step groups 8 (q >> 1) ..  Output piece q < 4: Qr step groups
+// 2q, 2q + 1 (with sq at q = 0); piece 4 + q (q < 2): P columns q and q + 2.  `tile0`: the
+// workgroup's first 16-row tile of U; lg16 = 16 lg (the lane's 4 tokens of ck and sq).
 template <int RT>
 __device__ __forceinline__ void load_state_piece(StateOperands<RT>& o,
                                                  __amdgpu_buffer_rsrc_t rs, int w,
-                                                 uint32_t lane16, int tile0, int piece) {
+                                                 uint32_t lane16, uint32_t lg16, int tile0,
+                                                 int piece) {
   if (piece < 4) {
     const int wbase = static_cast<int>(kOffW * 4) + w * 8 * 1024;
     o.w[piece] = load16(rs, lane16, wbase + piece * 1024);
@@ -507,23 +557,22 @@ __device__ __forceinline__ void load_state_piece(StateOperands<RT>& o,
 #pragma unroll
       for (int h = 0; h < RT; ++h)
         o.u[h] = load16(rs, lane16, static_cast<int>(kOffU * 4) + ((tile0 + h) * 4 + w) * 1024);
+      o.ck = load16(rs, lg16, static_cast<int>((kOffMisc + kMiscCk) * 4) + w * 64);
       o.gamma = load4(rs, static_cast<int>(kOffMisc * 4));
     }
   } else {
     const int q = piece - 4;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      o.kd[t][q] = load16(rs, lane16, static_cast<int>(kOffKd * 4) + (2 * w + t) * 4 * 1024 +
-                                          q * 1024);
+    o.kr[q & 1][q >> 1] = load16u(
+        rs, lane16, static_cast<int>(kOffKr * 4) + ((2 * w + (q & 1)) * 2 + (q >> 1)) * 1024);
   }
 }
 
 __device__ __forceinline__ void load_output_piece(OutputOperands& o, __amdgpu_buffer_rsrc_t rs,
-                                                  int w, uint32_t lane16, int piece) {
+                                                  int w, uint32_t lane16, uint32_t lg16,
+                                                  int piece) {
   if (piece < 4) {
-    const int qbase = static_cast<int>(kOffQg * 4) + w * 8 * 1024;
-    o.qg[piece] = load16(rs, lane16, qbase + piece * 1024);
-    o.qg[piece + 4] = load16(rs, lane16, qbase + (piece + 4) * 1024);
+    o.qr[piece] = load16u(rs, lane16, static_cast<int>(kOffQr * 4) + (w * 4 + piece) * 1024);
+    if (piece == 0) o.sq = load16(rs, lg16, static_cast<int>((kOffMisc + kMiscSq) * 4) + w * 64);
   } else {
     const int pbase = static_cast<int>(kOffP * 4) + w * 4 * 1024;
     o.p[piece - 4] = load16(rs, lane16, pbase + (piece - 4) * 1024);
@@ -605,6 +654,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   constexpr int kVRow = kC + 4;
   __shared__ __attribute__((aligned(16))) float sS[kRows][kSRow];   // S rows [row][k]
   __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];  // V_new^T [row][token]
+  __shared__ __attribute__((aligned(16))) float sVk[kRows][kVRow];  // ditto, token j times ck_j
 
   auto record = [&](int c) {
     return ws + (static_cast<int64_t>(gbase + c) * p.num_v_heads + head) * kRecord;
@@ -617,6 +667,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   auto vn_fragment = [&](int h, int q) {
     return *reinterpret_cast<const f32x4*>(&sVn[16 * h + li][16 * lg + 4 * q]);
   };
+  auto vk_fragment = [&](int h, int q) {
+    return *reinterpret_cast<const f32x4*>(&sVk[16 * h + li][16 * lg + 4 * q]);
+  };
+  const uint32_t lg16 = static_cast<uint32_t>(lg) * 16;
 
   if (state_wave) {
     // st[t][h][r] = S[row0 + 16 h + li][16 (2w + t) + 4 lg + r]
@@ -652,7 +706,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_state_piece(fill, cur, w, lane16, row_block * RT, kHalf ? 4 + q : q);
+        load_state_piece(fill, cur, w, lane16, lg16, row_block * RT, kHalf ? 4 + q : q);
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b0 = s_fragment(h, q);
@@ -672,6 +726,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       for (int h = 0; h < RT; ++h) {
         const f32x4 vn = op.u[h] - (vn0[h] + vn1[h]);
         *reinterpret_cast<f32x4*>(&sVn[16 * h + li][16 * w + 4 * lg]) = vn;
+        *reinterpret_cast<f32x4*>(&sVk[16 * h + li][16 * w + 4 * lg]) = vn * op.ck;
       }
       __syncthreads();  // V_new complete; every read of sS for this chunk done
 #pragma unroll
@@ -680,16 +735,17 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         for (int h = 0; h < RT; ++h) st[t][h] *= op.gamma;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_state_piece(fill, next, w, lane16, row_block * RT, kHalf ? q : 4 + q);
+        load_state_piece(fill, next, w, lane16, lg16, row_block * RT, kHalf ? q : 4 + q);
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
-          const f32x4 b = vn_fragment(h, q);
+          const f32x4 b = vk_fragment(h, q);
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            st[t][h] = mfma(op.kd[t][q].x, b.x, st[t][h]);
-            st[t][h] = mfma(op.kd[t][q].y, b.y, st[t][h]);
-            st[t][h] = mfma(op.kd[t][q].z, b.z, st[t][h]);
-            st[t][h] = mfma(op.kd[t][q].w, b.w, st[t][h]);
+            const f32x4 a = bf16x4(op.kr[t][q >> 1], q & 1);
+            st[t][h] = mfma(a.x, b.x, st[t][h]);
+            st[t][h] = mfma(a.y, b.y, st[t][h]);
+            st[t][h] = mfma(a.z, b.z, st[t][h]);
+            st[t][h] = mfma(a.w, b.w, st[t][h]);
           }
         }
         __builtin_amdgcn_sched_barrier(kLoadGroup);
@@ -706,7 +762,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       const __amdgpu_buffer_rsrc_t r = record_resource(record(c));
 #pragma unroll
       for (int piece = 0; piece < 8; ++piece) {
-        load_state_piece(set, r, w, lane16, row_block * RT, piece);
+        load_state_piece(set, r, w, lane16, lg16, row_block * RT, piece);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -723,7 +779,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         const __amdgpu_buffer_rsrc_t r = record_resource(record(0));
 #pragma unroll
         for (int piece = 0; piece < 4; ++piece) {
-          load_state_piece(ring0, r, w, lane16, row_block * RT, piece);
+          load_state_piece(ring0, r, w, lane16, lg16, row_block * RT, piece);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -754,32 +810,40 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         if (!kHalf)
-          load_output_piece(fill, next, w, lane16, q);
+          load_output_piece(fill, next, w, lane16, lg16, q);
         else if (q < 2)
-          load_output_piece(fill, cur, w, lane16, 4 + q);   // P of this chunk
+          load_output_piece(fill, cur, w, lane16, lg16, 4 + q);   // P of this chunk
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b0 = s_fragment(h, q);
           const f32x4 b1 = s_fragment(h, q + 4);
-          o0[h] = mfma(op.qg[q].x, b0.x, o0[h]);
-          o1[h] = mfma(op.qg[q + 4].x, b1.x, o1[h]);
-          o0[h] = mfma(op.qg[q].y, b0.y, o0[h]);
-          o1[h] = mfma(op.qg[q + 4].y, b1.y, o1[h]);
-          o0[h] = mfma(op.qg[q].z, b0.z, o0[h]);
-          o1[h] = mfma(op.qg[q + 4].z, b1.z, o1[h]);
-          o0[h] = mfma(op.qg[q].w, b0.w, o0[h]);
-          o1[h] = mfma(op.qg[q + 4].w, b1.w, o1[h]);
+          const f32x4 a0 = bf16x4(op.qr[q >> 1], q & 1);
+          const f32x4 a1 = bf16x4(op.qr[2 + (q >> 1)], q & 1);
+          o0[h] = mfma(a0.x, b0.x, o0[h]);
+          o1[h] = mfma(a1.x, b1.x, o1[h]);
+          o0[h] = mfma(a0.y, b0.y, o0[h]);
+          o1[h] = mfma(a1.y, b1.y, o1[h]);
+          o0[h] = mfma(a0.z, b0.z, o0[h]);
+          o1[h] = mfma(a1.z, b1.z, o1[h]);
+          o0[h] = mfma(a0.w, b0.w, o0[h]);
+          o1[h] = mfma(a1.w, b1.w, o1[h]);
         }
         __builtin_amdgcn_sched_barrier(kLoadGroup);
+      }
+      // rows of q S^T scaled to (q^ exp(G)) S^T; P V_new accumulates on top
+#pragma unroll
+      for (int h = 0; h < RT; ++h) {
+        o0[h] = (o0[h] + o1[h]) * op.sq;
+        o1[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       }
       __syncthreads();  // V_new complete
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         if (!kHalf) {
-          load_output_piece(fill, next, w, lane16, 4 + q);
+          load_output_piece(fill, next, w, lane16, lg16, 4 + q);
         } else {   // Qg of the next chunk
-          load_output_piece(fill, next, w, lane16, 2 * q);
-          load_output_piece(fill, next, w, lane16, 2 * q + 1);
+          load_output_piece(fill, next, w, lane16, lg16, 2 * q);
+          load_output_piece(fill, next, w, lane16, lg16, 2 * q + 1);
         }
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
@@ -816,7 +880,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       const __amdgpu_buffer_rsrc_t r = record_resource(record(c));
 #pragma unroll
       for (int piece = 0; piece < 6; ++piece) {
-        load_output_piece(set, r, w, lane16, piece);
+        load_output_piece(set, r, w, lane16, lg16, piece);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -833,7 +897,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         const __amdgpu_buffer_rsrc_t r = record_resource(record(0));
 #pragma unroll
         for (int piece = 0; piece < 4; ++piece) {
-          load_output_piece(ring0, r, w, lane16, piece);
+          load_output_piece(ring0, r, w, lane16, lg16, piece);
           __builtin_amdgcn_sched_barrier(0);
         }
       }

@@ -128,9 +128,9 @@ def test_prefill_rejects_bad_arguments_without_launching():
 
 def test_prefill_workspace_query_and_chunked_without_workspace():
     lib = _lib.load()
-    # one record of 36928 floats per (chunk, v-head), chunks <= tokens / 64 + sequences, then
+    # one record of 28928 floats per (chunk, v-head), chunks <= tokens / 64 + sequences, then
     # the per-sequence chunk index (sequences + 1 int32, rounded up to 256 bytes)
-    record = 36928 * 4
+    record = 28928 * 4
     assert lib.ld_gdn_prefill_workspace_bytes(4096, 1, 32) == (4096 // 64 + 1) * 32 * record + 256
     assert lib.ld_gdn_prefill_workspace_bytes(100, 70, 8) == (100 // 64 + 70) * 8 * record + 512
     assert lib.ld_gdn_prefill_workspace_bytes(-1, 1, 32) == 0
