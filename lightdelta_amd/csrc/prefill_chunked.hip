@@ -1,6 +1,9 @@
 // Chunked prefill for gfx950: the delta rule over chunks of 64 tokens in the WY form, with
-// every product on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 operands, fp32
-// accumulation, so the arithmetic is the vector ALUs' up to summation order).
+// every product on the matrix cores: products with an fp32 operand on the fp32 ones
+// (v_mfma_f32_16x16x4_f32: fp32 operands, fp32 accumulation, so the arithmetic is the
+// vector ALUs' up to summation order), the dot products of the bf16 inputs q . k and k . k
+// on the bf16 ones (v_mfma_f32_16x16x32_bf16: the inputs as they are, exact products, fp32
+// sums; the norms are applied to the sums).
 //
 // Per chunk (tokens i = 0 .. n-1, n <= 64), with g_i the log decay, G_i = g_0 + .. + g_i,
 // Gam_ij = exp(G_i - G_j), beta_i, normalised q^_i (scaled) and k^_i, and S the state at
@@ -60,11 +63,6 @@ constexpr int64_t kMiscCk = 128;
 constexpr int64_t kRecord = kOffMisc + 256;          // floats (a multiple of 64: 256 B)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// bf16 values held exactly in fp32, two to a word (lo, hi)
-__device__ __forceinline__ uint32_t pack_bf16_exact(float lo, float hi) {
-  return (__builtin_bit_cast(uint32_t, lo) >> 16) | (__builtin_bit_cast(uint32_t, hi) & 0xffff0000u);
-}
 
 // four consecutive bf16 of a 16-byte piece (half 0: elements 0..3, half 1: 4..7) as fp32
 __device__ __forceinline__ f32x4 bf16x4(const u32x4& v, int half) {
@@ -158,6 +156,8 @@ constexpr int kPrepWaves = kPrepThreads / 64;
 constexpr int kPrepTokens = kC / kPrepWaves;   // tokens normalised per wave
 
 // ---- phase 1: per (chunk, v-head) ----------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
 template <bool DtBf16>
 __global__ __launch_bounds__(kPrepThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
@@ -178,64 +178,55 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   const int k_col = (p.num_k_heads + key_head) * kDim;
   const int v_col = (2 * p.num_k_heads + head) * kDim;
 
-  constexpr int kRow = kDim + 4;   // padded LDS row (floats)
-  constexpr int kARow = kC + 4;    // padded LDS row of -A
+  constexpr int kHRow = kDim + 8;  // padded LDS row of the bf16 q / k (272 bytes)
+  constexpr int kRow = kDim + 4;   // padded LDS row of W (floats)
+  constexpr int kARow = kC + 4;    // padded LDS row of -A and P
   constexpr int kTRow = 20;        // padded LDS row of a diagonal block's inverse
-  // sQ holds q (the bf16 inputs, exactly) until A and P are formed, then -A [64][68] and the
-  // four inverses [4][16][20]; sK holds k, then P [64][68], then W [64][132], each on its
-  // way to the workspace.
-  __shared__ __attribute__((aligned(16))) float sQ[kC][kRow];
-  __shared__ __attribute__((aligned(16))) float sK[kC][kRow];
+  // One 34 KiB region: q and k (the bf16 inputs, [64][136] each) until A and P are formed;
+  // then -A and P ([64][68] fp32 each, in place of q and k); then W ([64][132] fp32) on its
+  // way to the workspace.  The four inverses [4][16][20] have their own 5 KiB.
+  constexpr int kHalfBytes = kC * kHRow * 2;
+  static_assert(kC * kARow * 4 <= kHalfBytes && kC * kRow * 4 <= 2 * kHalfBytes, "LDS plan");
+  __shared__ __attribute__((aligned(16))) uint8_t sBuf[2 * kHalfBytes];
+  __shared__ __attribute__((aligned(16))) float sT[4 * 16 * kTRow];
   __shared__ float sG[kC];
   __shared__ float sBeta[kC];
   __shared__ float sEg[kC];     // exp(G_i)
   __shared__ float sEk[kC];     // exp(G_n-1 - G_i)
   __shared__ float sRq[kC];     // rq_i scale (zero past the end)
   __shared__ float sRk[kC];     // rk_i (zero past the end)
-  float* const sA = &sQ[0][0];
-  float* const sT = &sQ[0][0] + kC * kARow;
-  float* const sW = &sK[0][0];
-  float* const sP = &sK[0][0];
+  uint16_t (*const sQh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sBuf);
+  uint16_t (*const sKh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sBuf + kHalfBytes);
+  float* const sA = reinterpret_cast<float*>(sBuf);
+  float* const sP = reinterpret_cast<float*>(sBuf + kHalfBytes);
+  float* const sW = reinterpret_cast<float*>(sBuf);
 
   // q and k of the chunk's tokens and their inverse norms (zero rows past its end); wave w
   // does tokens 8w .. 8w+7, all 8 tokens' loads in flight before the first norm
   {
-    uint16_t qr[kPrepTokens][2], kr[kPrepTokens][2];
+    uint32_t qr[kPrepTokens], kr[kPrepTokens];
 #pragma unroll
     for (int ii = 0; ii < kPrepTokens; ++ii) {
       const int64_t tok = t0 + min(wave * kPrepTokens + ii, len - 1);
       const uint16_t* row = p.qkv + tok * p.qkv_row;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        qr[ii][e] = row[q_col + 2 * lane + e];
-        kr[ii][e] = row[k_col + 2 * lane + e];
-      }
+      qr[ii] = row[q_col + 2 * lane] | (static_cast<uint32_t>(row[q_col + 2 * lane + 1]) << 16);
+      kr[ii] = row[k_col + 2 * lane] | (static_cast<uint32_t>(row[k_col + 2 * lane + 1]) << 16);
     }
 #pragma unroll
     for (int ii = 0; ii < kPrepTokens; ++ii) {
       const int i = wave * kPrepTokens + ii;
-      float q[2], k[2];
-      float qq = 0.0f, kk = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        q[e] = bf16_to_f32(qr[ii][e]);
-        k[e] = bf16_to_f32(kr[ii][e]);
-        qq = fmaf(q[e], q[e], qq);
-        kk = fmaf(k[e], k[e], kk);
-      }
-      qq = wave_sum(qq);
-      kk = wave_sum(kk);
+      const float q0 = __builtin_bit_cast(float, qr[ii] << 16);
+      const float q1 = __builtin_bit_cast(float, qr[ii] & 0xffff0000u);
+      const float k0 = __builtin_bit_cast(float, kr[ii] << 16);
+      const float k1 = __builtin_bit_cast(float, kr[ii] & 0xffff0000u);
+      const float qq = wave_sum(fmaf(q1, q1, q0 * q0));
+      const float kk = wave_sum(fmaf(k1, k1, k0 * k0));
       const bool live = i < len;
-      const float rq = fast_rsqrt(qq + 1e-6f);
-      const float rk = fast_rsqrt(kk + 1e-6f);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        sQ[i][2 * lane + e] = live ? q[e] : 0.0f;
-        sK[i][2 * lane + e] = live ? k[e] : 0.0f;
-      }
+      *reinterpret_cast<uint32_t*>(&sQh[i][2 * lane]) = live ? qr[ii] : 0u;
+      *reinterpret_cast<uint32_t*>(&sKh[i][2 * lane]) = live ? kr[ii] : 0u;
       if (lane == 0) {
-        sRq[i] = live ? rq * p.scale : 0.0f;
-        sRk[i] = live ? rk : 0.0f;
+        sRq[i] = live ? fast_rsqrt(qq + 1e-6f) * p.scale : 0.0f;
+        sRk[i] = live ? fast_rsqrt(kk + 1e-6f) : 0.0f;
       }
     }
   }
@@ -281,8 +272,10 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
   }
 
-  // A and P tiles: 32 steps of k (k = 32 lg + step) per tile; the third tile for waves
-  // 0-3 only (a uniform branch)
+  // A and P tiles of the raw inputs, q_i . k_m and k_i . k_m: bf16 operands with exact
+  // products and fp32 accumulation (v_mfma_f32_16x16x32_bf16, lane (li, lg) giving
+  // X[row li][32 s + 8 lg + e]), 4 steps of 32 per tile; the third tile for waves 0-3 only
+  // (a uniform branch)
   const uint32_t codes = prep_tiles(wave);
   const int tiles = wave < 4 ? 3 : 2;
   f32x4 prod[3];
@@ -292,17 +285,14 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     const uint32_t code = (codes >> (5 * t)) & 31u;
     const int mt = (code >> 2) & 3;
     const int nt = code & 3;
-    const float* arow = ((code & 16u) ? &sQ[0][0] : &sK[0][0]) + (16 * mt + li) * kRow + 32 * lg;
-    const float* brow = &sK[0][0] + (16 * nt + li) * kRow + 32 * lg;
+    const uint16_t* arow = ((code & 16u) ? &sQh[0][0] : &sKh[0][0]) + (16 * mt + li) * kHRow + 8 * lg;
+    const uint16_t* brow = &sKh[0][0] + (16 * nt + li) * kHRow + 8 * lg;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(arow + 4 * s4);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(brow + 4 * s4);
-      acc = mfma(a.x, b.x, acc);
-      acc = mfma(a.y, b.y, acc);
-      acc = mfma(a.z, b.z, acc);
-      acc = mfma(a.w, b.w, acc);
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + 32 * s4);
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(brow + 32 * s4);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
     }
     prod[t] = acc;
   }
@@ -327,12 +317,13 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         const int i = 16 * rb + 4 * lg + r;
         const float wscale = sBeta[i] * sEg[i] * sRk[i];
 #pragma unroll
-        for (int nt = 0; nt < kNt; ++nt) x[rb][nt][r] = wscale * sK[i][n0 + 16 * nt + li];
+        for (int nt = 0; nt < kNt; ++nt)
+          x[rb][nt][r] = wscale * bf16_to_f32(sKh[i][n0 + 16 * nt + li]);
       }
   }
 
-  // Qr and Kr (the bf16 inputs, repacked in the scan's load order) and the per-token scales
-  // to the workspace while q and k are still in LDS (item = one 16-byte piece)
+  // Qr and Kr (the bf16 inputs in the scan's load order) and the per-token scales to the
+  // workspace while q and k are still in LDS (item = one 16-byte piece)
   {
     u32x4* qdst = reinterpret_cast<u32x4*>(rec + kOffQr);
     u32x4* kdst = reinterpret_cast<u32x4*>(rec + kOffKr);
@@ -342,16 +333,13 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       const int l = item & 63;
       const int i = 16 * (item >> 8) + (l & 15);
       const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
-      const f32x4 a = *reinterpret_cast<const f32x4*>(&sQ[i][c0]);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(&sQ[i][c0 + 4]);
-      qdst[item] = u32x4{pack_bf16_exact(a.x, a.y), pack_bf16_exact(a.z, a.w),
-                         pack_bf16_exact(b.x, b.y), pack_bf16_exact(b.z, b.w)};
+      qdst[item] = *reinterpret_cast<const u32x4*>(&sQh[i][c0]);
       const int k = 16 * (item >> 7) + (l & 15);
       const int j = 16 * (l >> 4) + 8 * ((item >> 6) & 1);
-      kdst[item] = u32x4{pack_bf16_exact(sK[j][k], sK[j + 1][k]),
-                         pack_bf16_exact(sK[j + 2][k], sK[j + 3][k]),
-                         pack_bf16_exact(sK[j + 4][k], sK[j + 5][k]),
-                         pack_bf16_exact(sK[j + 6][k], sK[j + 7][k])};
+      kdst[item] = u32x4{sKh[j][k] | (static_cast<uint32_t>(sKh[j + 1][k]) << 16),
+                         sKh[j + 2][k] | (static_cast<uint32_t>(sKh[j + 3][k]) << 16),
+                         sKh[j + 4][k] | (static_cast<uint32_t>(sKh[j + 5][k]) << 16),
+                         sKh[j + 6][k] | (static_cast<uint32_t>(sKh[j + 7][k]) << 16)};
     }
     if (tid < kC)
       rec[kOffMisc + kMiscSq + tid] = sRq[tid] * sEg[tid];
@@ -449,7 +437,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   }
 
   // U straight from the fragments (its row block rb is the scan wave, its column tile the
-  // scan's block of v rows); W through LDS
+  // scan's block of v rows); W through LDS, once every wave is past its reads of -A (W takes
+  // the region of -A and P)
   if (solves_u) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
@@ -457,7 +446,9 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       for (int nt = 0; nt < kNt; ++nt)
         *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * 4 + rb) * 256 + lane * 4) =
             x[rb][nt];
-  } else {
+  }
+  __syncthreads();
+  if (!solves_u) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
