@@ -605,10 +605,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   constexpr int kRows = 16 * RT;              // state rows per workgroup
   constexpr int kBlocks = kDim / kRows;       // workgroups per (sequence, head)
   // Operand sets: three for one row tile (the whole set of chunk c + 2 loaded while chunk c
-  // computes); one for two row tiles, refilled piece by piece half a chunk ahead (the Kd
+  // computes); one for two row tiles, refilled piece by piece half a chunk ahead (the Kr
   // pieces of chunk c during its V_new products, the W, U and gamma pieces of chunk c + 1
-  // during its update), which leaves the registers for two workgroups per CU (98 VGPRs;
-  // 1% faster at 32 x 1024 than two sets a chunk ahead at 162).
+  // during its update), which leaves the registers for two workgroups per CU (1% faster
+  // at 32 x 1024 than two sets a chunk ahead, which needed 162 VGPRs).
   constexpr int kSets = RT == 1 ? 3 : 1;
   constexpr bool kHalf = kSets == 1;
   // Workgroups go to the 8 XCDs round-robin by id.  The row blocks of one (sequence, head)
@@ -832,7 +832,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       for (int q = 0; q < 2; ++q) {
         if (!kHalf) {
           load_output_piece(fill, next, w, lane16, lg16, 4 + q);
-        } else {   // Qg of the next chunk
+        } else {   // Qr of the next chunk
           load_output_piece(fill, next, w, lane16, lg16, 2 * q);
           load_output_piece(fill, next, w, lane16, lg16, 2 * q + 1);
         }
