@@ -68,6 +68,33 @@ def test_matches_oracle(gpu, heads, width, state_io, policy):
     assert torch.equal(case["pool"][0], before[0])
 
 
+@pytest.mark.parametrize("width", [1, 4])
+def test_cache_policies_give_identical_bits(gpu, width):
+    """The keep and stream policies differ in cache hints and, for one token, in the
+    kernel's shape (4 waves of 32 V rows per tile, or 16 of 8): eight consecutive steps at
+    the workload shape from the same pool give the same outputs and states bit for bit."""
+    announce(test="policies_identical", width=width)
+    case = decode_case(32, width, num_k_heads=16, num_v_heads=32, pool_slots=32 * width + 2,
+                       seed=40 + width, device=gpu)
+    pool0 = case["pool"].clone()
+    saved = ops.state_cache_policy()
+    results = {}
+    try:
+        for policy in ("keep", "stream"):
+            ops.set_state_cache_policy(policy)
+            case["pool"].copy_(pool0)
+            outs = []
+            for _ in range(8):
+                torch.ops.lightdelta.decode(*args_of(case), 1e-6)
+                outs.append(case["out"].clone())
+            torch.cuda.synchronize()
+            results[policy] = (torch.stack(outs), case["pool"].clone())
+    finally:
+        ops.set_state_cache_policy(saved)
+    assert torch.equal(results["keep"][0], results["stream"][0])
+    assert torch.equal(results["keep"][1], results["stream"][1])
+
+
 @pytest.mark.parametrize("dt_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("w_dtype", [torch.float32, torch.bfloat16])
 def test_parameter_dtypes(gpu, dt_dtype, w_dtype):
