@@ -223,6 +223,18 @@ def test_chunked_long_prompts_match_the_token_serial_form(gpu):
     chunked_against_token_serial(case)
 
 
+def test_chunked_two_row_tiles_over_many_chunks(gpu):
+    """16 prompts of 200 to 330 tokens (partial last chunks), 16 qk / 32 v heads: 512
+    (sequence, head) pairs, so the scan takes two 16-row state tiles per workgroup with one
+    operand set refilled half a chunk ahead, over several chunks per sequence."""
+    announce(test="prefill_chunked_two_row_tiles")
+    gen = torch.Generator().manual_seed(15)
+    lengths = torch.randint(200, 331, (16,), generator=gen).tolist()
+    case = prefill_case(gpu, lengths, seed=15)
+    case["has_initial"][1::3] = False
+    chunked_against_token_serial(case)
+
+
 def test_chunked_many_sequences_match_the_token_serial_form(gpu):
     """300 sequences of 0 to 150 tokens (empty ones among them; more sequences than one round
     of the chunk-index scan covers), some from zero states, one on the padding slot."""
