@@ -161,11 +161,20 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 template <bool DtBf16>
 __global__ __launch_bounds__(kPrepThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
-                       const int32_t* chunk_start) {
-  const int head = blockIdx.y;
+                       const int32_t* chunk_start, int records) {
+  // Workgroups go to the 8 XCDs round-robin by id.  The v-heads of one k-head group read
+  // the same q and k rows, so they get consecutive ids on one XCD and share its L2:
+  // id = ((unit / 8) * group + g) * 8 + unit % 8 for unit = chunk * H + k-head.
+  const int xcd = blockIdx.x & 7;
+  const int rank = blockIdx.x >> 3;
+  const int64_t unit = static_cast<int64_t>(rank / p.group) * 8 + xcd;
+  const int member = rank - (rank / p.group) * p.group;
+  const int g = static_cast<int>(unit / p.num_k_heads);   // global chunk
+  if (g >= records) return;
+  const int head = static_cast<int>(unit - static_cast<int64_t>(g) * p.num_k_heads) * p.group + member;
   int seq = 0, t0 = 0, len = 0;
-  if (!find_chunk(p.cu, chunk_start, num_sequences, blockIdx.x, seq, t0, len)) return;
-  float* rec = ws + (static_cast<int64_t>(blockIdx.x) * p.num_v_heads + head) * kRecord;
+  if (!find_chunk(p.cu, chunk_start, num_sequences, g, seq, t0, len)) return;
+  float* rec = ws + (static_cast<int64_t>(g) * p.num_v_heads + head) * kRecord;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // the wave index in a scalar register: the tile table, the A / P choice and the W / U
@@ -922,15 +931,18 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   const int64_t chunks = max_chunks(num_tokens, num_sequences);
   if (chunks > 0x7fffffff || p.num_v_heads > 65535)
     return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large for the chunked form");
-  const dim3 per_chunk(static_cast<uint32_t>(chunks), static_cast<uint32_t>(p.num_v_heads));
+  // (chunk, k-head) units padded to whole groups of 8, times the group's v-heads
+  const int64_t prep_groups = (chunks * p.num_k_heads + 7) / 8 * 8 * p.group;
+  if (prep_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
+  const dim3 per_chunk(static_cast<uint32_t>(prep_groups));
   hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, stream, p.cu, num_sequences,
                      chunk_start);
   if (dt_bf16)
     hipLaunchKernelGGL(chunk_prep_kernel<true>, per_chunk, dim3(kPrepThreads), 0, stream, p,
-                       num_sequences, ws, chunk_start);
+                       num_sequences, ws, chunk_start, static_cast<int>(chunks));
   else
     hipLaunchKernelGGL(chunk_prep_kernel<false>, per_chunk, dim3(kPrepThreads), 0, stream, p,
-                       num_sequences, ws, chunk_start);
+                       num_sequences, ws, chunk_start, static_cast<int>(chunks));
   const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
   // two row tiles per workgroup once they still give 2 workgroups per CU
   const bool two_tiles = pairs * (kDim / 32) >= 512;
