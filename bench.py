@@ -252,6 +252,13 @@ def prefill(device):
                 torch.cuda.synchronize()
                 ms = start.elapsed_time(end) / reps
                 entry[algorithm] = {"ms": round(ms, 3), "tokens_per_s": round(total / ms * 1e3, 1)}
+                if algorithm == "chunked":
+                    # matrix-core work of the WY form per (64-token chunk, v-head): the scan's
+                    # 3,584 fp32 16x16x4 products and the prep's 640 fp32 16x16x4 (forward
+                    # substitution) and 80 bf16 16x16x32 ones (the q.k and k.k tiles)
+                    chunk_flop = (3584 + 640) * 2048 + 80 * 16384
+                    flop = seqs * -(-length // 64) * HV * chunk_flop
+                    entry[algorithm]["mfma_TFLOPs"] = round(flop / ms / 1e9, 1)
         finally:
             ops.set_prefill_algorithm(saved)
         result[label] = entry
