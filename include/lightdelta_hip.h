@@ -28,10 +28,11 @@ extern "C" {
 #define LD_DTYPE_F32 0
 #define LD_DTYPE_BF16 1
 
-/* State cache policy of ld_gdn_decode.  KEEP: ordinary loads and stores, so a working set
- * that fits the 256 MB Infinity Cache stays there for the next step (one layer stepped
- * repeatedly).  STREAM: non-temporal loads and stores, for working sets far larger than the
- * caches (many layers between two steps of one layer). */
+/* State cache policy of ld_gdn_decode / ld_gdn_decode_conv (kernel shape and cache hints of
+ * the state traffic; never a change of results).  KEEP: tuned for a working set that stays in
+ * the 256 MB Infinity Cache until the next step (one layer stepped repeatedly).  STREAM: tuned
+ * for working sets far larger than the caches (many layers between two steps of one layer):
+ * non-temporal loads and system-scope stores for one token. */
 #define LD_CACHE_KEEP 0
 #define LD_CACHE_STREAM 1
 

@@ -10,16 +10,20 @@
 //   out[v] = bf16(raw[v] * rsqrt(mean(raw^2) + eps) * w[v] * silu(gate[v]))
 //
 // Work decomposition (one workgroup = one (request, v-head) 128x128 fp32 state tile):
-//   * 256 threads = 4 wave64s; wave w owns V rows 32w .. 32w+31.
-//   * Inside a wave, the 16 lanes of a DPP row span one 512-byte K row: lane kq holds
-//     k = 4kq..4kq+3 and 64+4kq..64+4kq+3 (two 16-byte pieces); the 4 DPP rows of the wave
-//     take 4 consecutive V rows.  One global_load_dwordx4 therefore reads four half rows,
-//     i.e. eight whole 128-byte lines.  A lane keeps 8 V rows x 8 K values = 64 fp32
+//   * 256 threads = 4 wave64s (16 wave64s for the single-token step under the stream
+//     policy).  Inside a wave, the 16 lanes of a DPP row span one 512-byte K row: lane kq
+//     holds k = 4kq..4kq+3 and 64+4kq..64+4kq+3 (two 16-byte pieces); the 4 DPP rows of the
+//     wave take 4 consecutive V rows.  Wave w's rows are 4w..4w+3 plus multiples of 4 * waves:
+//     a piece pair of all waves covers one contiguous block of the tile (16 rows = 8 KiB with
+//     4 waves, the whole 32 KiB half tile with 16).  A cold in-place read-modify-write of
+//     64 KiB tiles at random slots runs 13% faster laid out that way than with each wave
+//     owning contiguous rows, whose first piece pairs spread over the whole tile (B=128, 16
+//     waves: 85.7 against 98.0 us).  With 4 waves a lane keeps 8 V rows x 8 K values = 64 fp32
 //     (16 x 128-bit loads) of the tile in VGPRs for the whole step.
-//   * All 16 tile loads are issued up front, then the slice is processed in 4 chunks of
-//     8 V rows in load order: each chunk waits only for its own 4 loads, runs every token
-//     on its rows and stores them, so arithmetic on chunk c overlaps the loads of the later
-//     chunks and the stores of the earlier ones.
+//   * All tile loads are issued up front, then the slice is processed in chunks of 2 rows per
+//     lane in load order: each chunk waits only for its own 4 loads, runs every token on its
+//     rows and stores them, so arithmetic on chunk c overlaps the loads of the later chunks
+//     and the stores of the earlier ones.
 //   * Row dot products S k^ and S q^ are 8 products per lane plus a 4-step DPP butterfly
 //     over the 16-lane row (quad_perm, row_half_mirror, row_mirror); every lane ends with
 //     the full sums, so no LDS round trip and no broadcast step is needed.
@@ -35,8 +39,8 @@ constexpr int kMaxConvLen = 8;
 constexpr int kMaxConvTickets = 1 << 20;
 __device__ uint32_t g_conv_ticket[kMaxConvTickets];
 
-// Destination of the state of an MTP token that has no slot to go to (past the request's last
-// token, or a padding slot) under non-temporal stores: one tile, written and never read.
+// Destination of the state of a token that has no slot to go to (past the request's last
+// token, or a padding slot) under pointer stores: one tile, written and never read.
 __device__ __align__(256) f32x4 g_state_sink[kDim * kDim / 4];
 
 // The q/k part of a token in the lane layout of load_token, from conv outputs in LDS
@@ -171,10 +175,11 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 
 
 // Four waves per SIMD (<= 128 VGPRs) keep four workgroups, i.e. four tiles, resident per CU.
-// DtBf16 / WBf16: dt_bias / norm_weight stored as bf16 (else fp32).  Stream: non-temporal
-// state loads and stores (for working sets larger than the caches).  Width: the indices
-// width W (tokens per request at most); fixing it at compile time unrolls every token loop
-// into straight-line code, which keeps the tile's per-piece load waits exact.
+// DtBf16 / WBf16: dt_bias / norm_weight stored as bf16 (else fp32).  LoadPol / StorePol: cache
+// policy bits of the state loads and stores (kPolPlain, kPolNT, kPolSys; never a change of
+// results).  Width: the indices width W (tokens per request at most); fixing it at compile
+// time unrolls every token loop into straight-line code, which keeps the tile's per-piece load
+// waits exact.
 //
 // Conv: the causal depthwise conv1d (width 4, SiLU) runs first on the pre-conv activations.
 // Each workgroup convolves the 256 q/k channels of its k-head and the 128 v channels of its
@@ -191,10 +196,11 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 // up to 8; 0 = no conv).
 //
 // Waves: 4 (32 V rows and 16 tile pieces per wave), or 16 (8 rows, 4 pieces) for the
-// single-token step under the stream policy.  A cold in-place read-modify-write of 64 KiB
-// per workgroup runs 6.5% faster as 1024 threads x 4 pieces than as 256 x 16 (5.85 against
-// 5.49 TB/s on 512 MiB), and hot ones alike.
-template <bool DtBf16, bool WBf16, bool Stream, int Width, int ConvCols, int Waves = kWaves>
+// non-conv steps under the stream policy.  A cold in-place read-modify-write of 64 KiB per
+// workgroup in this layout runs at 6.26 TB/s as 1024 threads x 4 pieces against 5.63 as
+// 256 x 16 (B=128 tiles at random slots, non-temporal loads, system-scope stores).
+template <bool DtBf16, bool WBf16, int LoadPol, int StorePol, int Width, int ConvCols,
+          int Waves = kWaves>
 __global__ __launch_bounds__(64 * Waves)
 __attribute__((amdgpu_waves_per_eu(Waves == kWaves ? 4 : 8, Waves == kWaves ? 4 : 8)))
 void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
@@ -209,17 +215,15 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   constexpr int kBlock = 64 * Waves;           // threads
   constexpr int kRows = kDim / Waves;          // V rows per wave
   constexpr int kPc = kRows / 2;               // 16-byte tile pieces per lane
-  constexpr int kChunks = kPc / 4;             // chunks of 8 rows per wave
-  static_assert(Waves == kWaves || (Waves == 16 && !Conv && Width == 1),
-                "16 waves only for the single-token step without the conv");
-  // Cache hints of the state traffic.  One token: the policy's (plain loads and stores keep
-  // a layer's state in the Infinity Cache between steps; non-temporal ones stream it).
-  // Several tokens (verify): the writes are 4 times the reads, and plain loads with
-  // non-temporal stores measured fastest under either policy (B=64, T=4: 103 us against
-  // 134-139 us with both hints alike), the stores being unconditional (sink tile) so that
-  // load waits stay exact.
-  constexpr bool kLoadNT = Stream && Width == 1;
-  constexpr bool kStoreNT = Stream || Width > 1;
+  // A piece pair of every wave (4 rows per wave) covers one contiguous block of 4 * Waves
+  // rows: lane (rsub, kq) of wave w holds rows 4w + rsub + kPair * i, i < kPc / 2.
+  constexpr int kPair = 4 * Waves;
+  // Token 0 staged by every wave for itself (no barrier before the recurrence), or -- verify
+  // steps with 16 waves, whose registers (<= 64 for 8 waves per SIMD) do not hold two tokens'
+  // inputs at once -- by wave 0 once, like tokens 1..W-1, behind one barrier.
+  constexpr bool kShared0 = Width > 1 && Waves == 16;
+  constexpr int kChunks = kPc / 4;             // chunks of 2 rows per lane (8 per wave)
+  static_assert(Waves == kWaves || (Waves == 16 && !Conv), "16 waves only without the conv");
   // The conv runs before the tile loads for several tokens or more than 4 state columns;
   // one token with 3..4 columns keeps it in registers while the tile streams in.
   constexpr bool kConvFirst = Conv && (Width > 1 || kCols > 4);
@@ -295,13 +299,17 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // recurrence): q^ and k^ (128 each), v of the wave's 32 rows, decay and beta.  MTP tokens
   // t >= 1 are staged once, by wave t, in the shared area (one barrier, after chunk 0's
   // token 0).  s_o collects the raw outputs of all rows for the epilogue.
-  __shared__ f32x4 s_qk0[Waves][2][kDim / 4];
-  __shared__ float s_v0[Waves][kRows];
-  __shared__ float s_db0[Waves][2];
+  __shared__ f32x4 s_qk0[kShared0 ? 1 : Waves][2][kDim / 4];
+  __shared__ float s_v0[kShared0 ? 1 : Waves][kRows];
+  __shared__ float s_db0[kShared0 ? 1 : Waves][2];
   __shared__ f32x4 s_qkt[Width][2][kDim / 4];
   __shared__ float s_vt[Width][kDim];
   __shared__ float s_dbt[Width][2];
   __shared__ float s_o[Width][kDim];
+  // Epilogue inputs, parked here once they arrive so that no register holds them through the
+  // recurrence: silu(gate) of token t (written by wave t) and the norm weight (wave 0).
+  __shared__ float s_sg[Width][kDim];
+  __shared__ float s_w[kDim];
   // Conv variant: bf16 conv outputs of the 256 q/k channels and 128 v channels per token,
   // and the shifted q/k conv state kept for the end-of-kernel write.
   __shared__ uint16_t s_conv[Conv ? Width : 1][Conv ? 3 * kDim : 2];
@@ -311,7 +319,10 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   const int key_head = head / p.group;
   const int kq = lane & 15;
   const int rsub = lane >> 4;
-  const int row_base = wave * kRows + rsub;  // V row of the lane's piece 0
+  const int row_base = 4 * wave + rsub;  // V row of the lane's piece 0
+  // Row of the wave's i-th staged v value (i < kRows): the rows of its lanes, in the order
+  // chunk_step reads them (s_v0[wave][8C + rsub] and [8C + 4 + rsub] for chunk C).
+  const int v_row = 4 * wave + (lane & 3) + kPair * ((lane & (kRows - 1)) >> 2);
   const int q_col = key_head * kDim;
   const int k_col = (p.num_k_heads + key_head) * kDim;
   const int v_col = (2 * p.num_k_heads + head) * kDim;
@@ -382,14 +393,14 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     cb_v = bias_src[conv_v];
     in0.a = p.a[static_cast<int64_t>(bos) * p.a_row + head];
     in0.b = p.b[static_cast<int64_t>(bos) * p.b_row + head];
-  } else {
-    in0 = load_token(p, bos, q_col, k_col, v_col + wave * kRows + (lane & (kRows - 1)), head, kq);
+  } else if constexpr (!kShared0) {
+    in0 = load_token(p, bos, q_col, k_col, v_col + v_row, head, kq);
   }
   // Every MTP token slot t < W is staged and stepped, past the request's last token too
   // (with a copy of that token), so the token loops have no branches; such tokens' states
   // go to the sink tile (non-temporal stores) or are not stored, and their outputs are not
   // written.
-  const bool stages_mtp = Width > 1 && wave >= 1 && wave < Width;
+  const bool stages_mtp = Width > 1 && wave >= (kShared0 ? 0 : 1) && wave < Width;
   const int64_t token_w = bos + min(wave, num_tokens - 1);
   TokenIn inw;
   uint16_t vw_hi = 0;
@@ -427,9 +438,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   f32x4 s[kPc];
 #pragma unroll
   for (int j = 0; j < kPc; ++j) {
-    const f32x4* src =
-        reinterpret_cast<const f32x4*>(src_tile + (lane_bytes + tile_piece_bytes(j)));
-    s[j] = kLoadNT ? __builtin_nontemporal_load(src) : *src;
+    s[j] = load_tile_piece<LoadPol>(src_tile, lane_bytes + tile_piece_bytes<kPair>(j));
     __builtin_amdgcn_sched_barrier(0);  // keep program order: chunk c's loads issue first
   }
 
@@ -472,9 +481,9 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
       in0.q[e] = c.q[e];
       in0.k[e] = c.k[e];
     }
-    in0.v = s_conv[0][2 * kDim + wave * kRows + (lane & (kRows - 1))];
+    in0.v = s_conv[0][2 * kDim + v_row];
   }
-  {
+  if constexpr (!kShared0) {
     const Staged x = stage_token(in0, a_log, dt_bias, p.scale);
     if (rsub == 0) {
       s_qk0[wave][0][kq] = x.q0;
@@ -487,6 +496,14 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
       s_db0[wave][0] = x.decay;
       s_db0[wave][1] = x.beta;
     }
+  }
+  if (wave < Width) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) s_sg[wave][2 * lane + e] = silu(bf16_to_f32(gh[e]));
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) s_w[2 * lane + e] = w[e];
   }
   if (stages_mtp) {
     const Staged x = stage_token(inw, a_log, dt_bias, p.scale);
@@ -511,30 +528,35 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
 
   // ---- recurrence, chunk by chunk in load order (each chunk's first use of a piece waits
   // for that piece alone: s_waitcnt vmcnt(N)); every token of a chunk before the next ----
-  char* const state_bytes = reinterpret_cast<char*>(p.state + head_offset);
-  const int64_t slot_bytes = p.state_slot * 4;
-  char* dst[Width];
+  // Token t's state goes to slot indices[r, t]; past the request's last token or to a padding
+  // slot it goes nowhere (TileStore: sink tile or empty resource, no branch).
+  TileStore<StorePol> dst[Width];
 #pragma unroll
-  for (int t = 0; t < Width; ++t)
-    dst[t] = (t < num_tokens && slot[t] > 0) ? state_bytes + slot[t] * slot_bytes
-             : kStoreNT                       ? reinterpret_cast<char*>(g_state_sink)
-                                              : nullptr;
+  for (int t = 0; t < Width; ++t) {
+    const bool stored = t < num_tokens && slot[t] > 0;
+    dst[t].set(reinterpret_cast<char*>(p.state + static_cast<int64_t>(stored ? slot[t] : 0) *
+                                                     p.state_slot + head_offset),
+               stored, reinterpret_cast<char*>(g_state_sink));
+  }
 
 #define LD_CHUNK(C)                                                                         \
   {                                                                                         \
-    const int r = row_base + 8 * (C);                                                       \
-    chunk_step<C, kStoreNT>(s, load_vectors(s_qk0[wave], kq), s_v0[wave][8 * (C) + rsub],     \
-                          s_v0[wave][8 * (C) + 4 + rsub], s_o[0], s_db0[wave][0],           \
-                          s_db0[wave][1], kq, r, dst[0], lane_bytes);                       \
-    if ((C) == 0 && Width > 1) lds_barrier();                                               \
-    _Pragma("unroll") for (int t = 1; t < Width; ++t) {                                     \
-      chunk_step<C, kStoreNT>(s, load_vectors(s_qkt[t], kq), s_vt[t][r], s_vt[t][r + 4],      \
-                            s_o[t], s_dbt[t][0], s_dbt[t][1], kq, r, dst[t], lane_bytes);   \
+    const int r = row_base + 2 * kPair * (C);                                               \
+    if constexpr (!kShared0) {                                                              \
+      chunk_step<C, kPair>(s, load_vectors(s_qk0[wave], kq), s_v0[wave][8 * (C) + rsub],      \
+                           s_v0[wave][8 * (C) + 4 + rsub], s_o[0], s_db0[wave][0],            \
+                           s_db0[wave][1], kq, r, dst[0], lane_bytes);                      \
+      if ((C) == 0 && Width > 1) lds_barrier();                                             \
+    }                                                                                       \
+    _Pragma("unroll") for (int t = kShared0 ? 0 : 1; t < Width; ++t) {                      \
+      chunk_step<C, kPair>(s, load_vectors(s_qkt[t], kq), s_vt[t][r], s_vt[t][r + kPair],     \
+                           s_o[t], s_dbt[t][0], s_dbt[t][1], kq, r, dst[t], lane_bytes);    \
     }                                                                                       \
   }
+  if constexpr (kShared0) lds_barrier();  // every token staged
   LD_CHUNK(0)
-  if constexpr (kChunks > 1) {
-    LD_CHUNK(1)
+  if constexpr (kChunks > 1) LD_CHUNK(1)
+  if constexpr (kChunks > 2) {
     LD_CHUNK(2)
     LD_CHUNK(3)
   }
@@ -560,8 +582,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int v = 2 * lane + e;
-      const float gate = bf16_to_f32(gh[e]);
-      orow[v] = f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(gate));
+      orow[v] = f32_to_bf16(((raw[e] * rstd) * s_w[v]) * s_sg[wave][v]);
     }
   }
 
@@ -584,40 +605,43 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
 }
 
 
-template <bool Stream, int Width, int ConvCols>
-void launch_decode(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
+template <int LoadPol, int StorePol, int Width, int ConvCols, int Waves>
+void launch_kernel(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
                    hipStream_t stream) {
-  constexpr int W = (Stream && Width == 1 && ConvCols == 0) ? 16 : kWaves;
-  auto kernel = dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, Stream, Width, ConvCols, W>
-                                  : gdn_decode_kernel<true, false, Stream, Width, ConvCols, W>)
-                        : (w_bf16 ? gdn_decode_kernel<false, true, Stream, Width, ConvCols, W>
-                                  : gdn_decode_kernel<false, false, Stream, Width, ConvCols, W>);
-  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * W), 0, stream, p.indices, p.cu, p.accepted,
-                     p.num_v_heads, p);
+  auto kernel =
+      dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, LoadPol, StorePol, Width, ConvCols, Waves>
+                        : gdn_decode_kernel<true, false, LoadPol, StorePol, Width, ConvCols, Waves>)
+              : (w_bf16 ? gdn_decode_kernel<false, true, LoadPol, StorePol, Width, ConvCols, Waves>
+                        : gdn_decode_kernel<false, false, LoadPol, StorePol, Width, ConvCols, Waves>);
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * Waves), 0, stream, p.indices, p.cu,
+                     p.accepted, p.num_v_heads, p);
 }
 
-template <bool Stream>
+// One cache policy: hints and wave count of the single-token step (LP1, SP1, Waves1) and of
+// verify steps (LPn, SPn, WavesN); the conv-fused kernels run 4 waves, with the hints LPc, SPc
+// for one token and LPn, SPn for several.
+template <int LP1, int SP1, int Waves1, int LPn, int SPn, int WavesN, int LPc, int SPc>
 void launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
                    uint32_t blocks, hipStream_t stream) {
   if (conv) {
     switch (p.width) {
       case 1:  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
         if (p.conv_len <= 4)
-          launch_decode<Stream, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
+          launch_kernel<LPc, SPc, 1, 4, kWaves>(p, dt_bf16, w_bf16, blocks, stream);
         else
-          launch_decode<Stream, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
+          launch_kernel<LPc, SPc, 1, kMaxConvLen, kWaves>(p, dt_bf16, w_bf16, blocks, stream);
         break;
-      case 2: launch_decode<Stream, 2, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
-      case 3: launch_decode<Stream, 3, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
-      default: launch_decode<Stream, 4, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
+      case 2: launch_kernel<LPn, SPn, 2, kMaxConvLen, kWaves>(p, dt_bf16, w_bf16, blocks, stream); break;
+      case 3: launch_kernel<LPn, SPn, 3, kMaxConvLen, kWaves>(p, dt_bf16, w_bf16, blocks, stream); break;
+      default: launch_kernel<LPn, SPn, 4, kMaxConvLen, kWaves>(p, dt_bf16, w_bf16, blocks, stream); break;
     }
     return;
   }
   switch (p.width) {
-    case 1: launch_decode<Stream, 1, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 2: launch_decode<Stream, 2, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 3: launch_decode<Stream, 3, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
-    default: launch_decode<Stream, 4, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 1: launch_kernel<LP1, SP1, 1, 0, Waves1>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 2: launch_kernel<LPn, SPn, 2, 0, WavesN>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 3: launch_kernel<LPn, SPn, 3, 0, WavesN>(p, dt_bf16, w_bf16, blocks, stream); break;
+    default: launch_kernel<LPn, SPn, 4, 0, WavesN>(p, dt_bf16, w_bf16, blocks, stream); break;
   }
 }
 
@@ -679,10 +703,27 @@ int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, b
   const bool dt_bf16 = a.dt_bias_dtype == LD_DTYPE_BF16;
   const bool w_bf16 = a.norm_weight_dtype == LD_DTYPE_BF16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  // Measured on MI355X (B=32 and B=128 single-token steps, B=64 4-token verify, B=32
+  // conv-fused step; hot = the same slots every step, cold = slot sets rotated through a pool
+  // far beyond the 256 MB Infinity Cache):
+  //   one token, keep:   4 waves, plain loads and stores (B=32 hot 19.98 us; 16 waves with
+  //                      the same hints 20.21, the stream kernel 20.90).
+  //   one token, stream: 16 waves, non-temporal loads, system-scope stores (B=128 cold
+  //                      89.3 us = 6.01 TB/s; with non-temporal stores 90.9, the keep
+  //                      kernel 107.6; B=32 cold 24.8 against 29.8).
+  //   verify, either:    16 waves, plain loads, non-temporal stores (B=64, T=4: 99.4 us hot
+  //                      and 125.0 cold, against 105.1 and 138.9 with 4 waves).
+  //   conv-fused, one token: 4 waves, plain loads and stores (keep; 22.4 us hot) or
+  //                      non-temporal ones (stream; 28.5 us cold, against 30.0 with
+  //                      system-scope stores); conv-fused verify: 4 waves, plain loads,
+  //                      non-temporal stores.
+  const uint32_t n = static_cast<uint32_t>(blocks);
   if (a.cache_policy == LD_CACHE_STREAM)
-    launch_decode<true>(p, conv, dt_bf16, w_bf16, static_cast<uint32_t>(blocks), s);
+    launch_decode<kPolNT, kPolSys, 16, kPolPlain, kPolNT, 16, kPolNT, kPolNT>(p, conv, dt_bf16,
+                                                                             w_bf16, n, s);
   else
-    launch_decode<false>(p, conv, dt_bf16, w_bf16, static_cast<uint32_t>(blocks), s);
+    launch_decode<kPolPlain, kPolPlain, kWaves, kPolPlain, kPolNT, 16, kPolPlain, kPolPlain>(
+        p, conv, dt_bf16, w_bf16, n, s);
   return check_launch(conv ? "ld_gdn_decode_conv" : "ld_gdn_decode");
 }
 

@@ -1,13 +1,16 @@
 // The per-token step shared by the decode / verify kernel (gdn_decode.hip) and the
 // token-serial prefill (prefill_serial.hip).
 //
-// Lane layout of a 128 x 128 fp32 state tile in a workgroup of 4 wave64s: wave w owns V
-// rows 32w .. 32w+31 (or 8 * Chunks rows in the prefill's row-split kernels); the 16 lanes
-// of a DPP row span one 512-byte K row, lane kq holding k = 4kq .. 4kq+3 and 64+4kq ..
-// 64+4kq+3 (two 16-byte pieces); the 4 DPP rows of a wave take 4 consecutive V rows.  A
-// token is staged once (q^, k^ in the lane layout, v of the wave's rows, decay and beta)
-// and applied to the tile chunk by chunk (chunk_step), with the row sums S k^ and S q^ by a
-// 4-step DPP butterfly, so every lane holds the full sums.
+// Lane layout of a 128 x 128 fp32 state tile: the 16 lanes of a DPP row span one 512-byte K
+// row, lane kq holding k = 4kq .. 4kq+3 and 64+4kq .. 64+4kq+3 (pieces 2i and 2i+1, 16 bytes
+// each); the 4 DPP rows of a wave take 4 consecutive V rows; a lane's pieces 2i, 2i+1 lie
+// PairRows rows below its pieces 2i-2, 2i-1.  The token-serial prefill uses PairRows = 4
+// (wave w owning the contiguous rows of its share); the decode uses PairRows = 4 * waves, so
+// that a piece pair of all waves of the workgroup covers one contiguous block of the tile
+// (see gdn_decode.hip).  A token is staged once (q^, k^ in the lane layout, v of the lane's
+// rows, decay and beta) and applied to the tile chunk by chunk (chunk_step), with the row
+// sums S k^ and S q^ by a 4-step DPP butterfly, so every lane holds the full sums.  Which lane
+// holds which row does not change any row's arithmetic.
 #pragma once
 
 #include "gdn_common.h"
@@ -28,9 +31,11 @@ __device__ __forceinline__ void row_sum2(float& x, float& y) {
 }
 
 // Byte offset of a lane's 16-byte piece j of the tile, relative to its first piece: piece j
-// is V row 4*(j/2) further down (2 KiB per 4 rows) and, for odd j, 64 floats further along K.
+// is V row PairRows*(j/2) further down (512 bytes per row) and, for odd j, 64 floats further
+// along K.
+template <int PairRows = 4>
 __device__ __forceinline__ constexpr uint32_t tile_piece_bytes(int j) {
-  return static_cast<uint32_t>(j >> 1) * 4u * kDim * 4u + static_cast<uint32_t>(j & 1) * 256u;
+  return static_cast<uint32_t>(j >> 1) * PairRows * kDim * 4u + static_cast<uint32_t>(j & 1) * 256u;
 }
 
 __device__ __forceinline__ float dot8(f32x4 s0, f32x4 s1, f32x4 x0, f32x4 x1) {
@@ -123,15 +128,57 @@ __device__ __forceinline__ Staged stage_token(const TokenIn& in, float a_log, fl
   return x;
 }
 
-// One token on chunk C of the lane's slice (pieces 4C..4C+3 = V rows row0 and row0 + 4,
-// whose v values are v0 and v1):
+// Where chunk_step puts a chunk's updated pieces: nowhere (the prefill keeps the tile in
+// registers), or a 64 KiB tile with cache policy Pol.  Plain and non-temporal stores go
+// through the tile's address; policies with scope bits through a buffer resource over it.
+// The store is unconditional, so the compiler's count of memory operations in flight stays
+// exact and later chunks wait for their own loads only: a token without a destination (a
+// padding slot, a token past the request's last) writes the sink tile (pointer stores), or a
+// resource over 0 bytes, whose stores the hardware drops.
+struct NoStore {
+  __device__ __forceinline__ void store(uint32_t, f32x4) const {}
+};
+
+template <int Pol>
+struct TileStore {
+  static constexpr bool kBuffer = (Pol & ~kPolNT) != 0;
+  char* tile;                    // pointer stores
+  __amdgpu_buffer_rsrc_t rsrc;   // buffer stores
+  __device__ __forceinline__ void set(char* destination, bool stored, char* sink) {
+    if constexpr (kBuffer)
+      rsrc = buffer_rsrc(destination, stored ? kTileBytes : 0);
+    else
+      tile = stored ? destination : sink;
+  }
+  __device__ __forceinline__ void store(uint32_t offset, f32x4 v) const {
+    if constexpr (kBuffer)
+      buffer_store16<Pol>(v, rsrc, offset);
+    else if constexpr (Pol == kPolNT)
+      __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(tile + offset));
+    else
+      *reinterpret_cast<f32x4*>(tile + offset) = v;
+  }
+};
+
+// Piece of a source tile at `offset`, loaded with cache policy Pol (as TileStore).
+template <int Pol>
+__device__ __forceinline__ f32x4 load_tile_piece(const char* tile, uint32_t offset) {
+  if constexpr ((Pol & ~kPolNT) != 0)
+    return buffer_load16<Pol>(buffer_rsrc(tile, kTileBytes), offset);
+  else if constexpr (Pol == kPolNT)
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(tile + offset));
+  else
+    return *reinterpret_cast<const f32x4*>(tile + offset);
+}
+
+// One token on chunk C of the lane's slice (pieces 4C..4C+3 = V rows row0 and
+// row0 + PairRows, whose v values are v0 and v1):
 //   S <- decay*S ; delta = (v - S k^) * beta ; S += delta k^ ; raw = bf16(S q^)
-// The updated pieces are stored to `dst_tile` (NULL: padding slot, nothing stored) and the
-// two rows' raw outputs go to LDS (one lane per row).
-template <int C, bool Stream, bool Store = true, int N = kPieces>
+// The updated pieces go to `dst` and the two rows' raw outputs to LDS (one lane per row).
+template <int C, int PairRows = 4, int N = kPieces, typename Dst>
 __device__ __forceinline__ void chunk_step(f32x4 (&s)[N], const Vectors& x, float v0,
                                            float v1, float* o, float decay, float beta,
-                                           int kq, int row0, char* dst_tile,
+                                           int kq, int row0, const Dst& dst,
                                            uint32_t lane_bytes) {
   constexpr int j0 = 4 * C;
 #pragma unroll
@@ -148,28 +195,14 @@ __device__ __forceinline__ void chunk_step(f32x4 (&s)[N], const Vectors& x, floa
     s[j0 + 2][e] = fmaf(d1, x.k0[e], s[j0 + 2][e]);
     s[j0 + 3][e] = fmaf(d1, x.k1[e], s[j0 + 3][e]);
   }
-  // Stream: unconditional (a token without a destination writes the sink tile), so the
-  // compiler's count of memory operations in flight is exact and later chunks wait for
-  // their own loads only.  Keep: skipped for a null destination; the branch makes the
-  // compiler assume the stores may not have been issued, so chunks 2 and 3 also wait for
-  // the earlier chunks' stores -- measured 1.5% faster when the state is served from the
-  // Infinity Cache, and 2% slower when it streams from HBM.
-  if (Store && (Stream || dst_tile != nullptr)) {
 #pragma unroll
-    for (int j = j0; j < j0 + 4; ++j) {
-      f32x4* dst = reinterpret_cast<f32x4*>(dst_tile + (lane_bytes + tile_piece_bytes(j)));
-      if (Stream)
-        __builtin_nontemporal_store(s[j], dst);
-      else
-        *dst = s[j];
-    }
-  }
+  for (int j = j0; j < j0 + 4; ++j) dst.store(lane_bytes + tile_piece_bytes<PairRows>(j), s[j]);
   float out0 = dot8(s[j0], s[j0 + 1], x.q0, x.q1);
   float out1 = dot8(s[j0 + 2], s[j0 + 3], x.q0, x.q1);
   row_sum2(out0, out1);
   if (kq == 0) {
     o[row0] = round_bf16(out0);
-    o[row0 + 4] = round_bf16(out1);
+    o[row0 + PairRows] = round_bf16(out1);
   }
 }
 

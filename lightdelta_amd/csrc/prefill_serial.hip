@@ -111,9 +111,9 @@ void gdn_prefill_kernel(const DecodeParams args) {
       const int orow = Chunks == 4 ? row_base : rsub;
 #define LD_PREFILL_CHUNK(C)                                                                    \
   if constexpr ((C) < Chunks)                                                                  \
-    chunk_step<C, false, false, kTilePieces>(s, vec, s_v[wave][8 * (C) + rsub],                \
-                                             s_v[wave][8 * (C) + 4 + rsub], o, x.decay,        \
-                                             x.beta, kq, orow + 8 * (C), nullptr, lane_bytes);
+    chunk_step<C, 4, kTilePieces>(s, vec, s_v[wave][8 * (C) + rsub],                            \
+                               s_v[wave][8 * (C) + 4 + rsub], o, x.decay, x.beta, kq,          \
+                               orow + 8 * (C), NoStore{}, lane_bytes);
       LD_PREFILL_CHUNK(0)
       LD_PREFILL_CHUNK(1)
       LD_PREFILL_CHUNK(2)
@@ -258,11 +258,11 @@ void gdn_prefill_rows_kernel(const DecodeParams args) {
     vec.k0 = now.k0;
     vec.k1 = now.k1;
     float* o = s_o[wave];
-    chunk_step<0, false, false, kTilePieces>(s, vec, vv[0], vv[1], o, now.decay, now.beta, kq,
-                                             rsub, nullptr, lane_bytes);
+    chunk_step<0, 4, kTilePieces>(s, vec, vv[0], vv[1], o, now.decay, now.beta, kq, rsub,
+                               NoStore{}, lane_bytes);
     if constexpr (Chunks == 2)
-      chunk_step<1, false, false, kTilePieces>(s, vec, vv[2], vv[3], o, now.decay, now.beta, kq,
-                                               rsub + 8, nullptr, lane_bytes);
+      chunk_step<1, 4, kTilePieces>(s, vec, vv[2], vv[3], o, now.decay, now.beta, kq, rsub + 8,
+                                 NoStore{}, lane_bytes);
     // s_o is read back by other lanes of this wave: a wave's LDS operations run in program
     // order, so only the compiler must not reorder them.
     asm volatile("" ::: "memory");

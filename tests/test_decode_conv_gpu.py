@@ -213,3 +213,39 @@ def test_verify_graph_replay(gpu):
         torch.cuda.synchronize()
         check_step(case, expected, f"verify replay {replay}")
         case["pool"].copy_(expected[1].to(case["pool"].device))
+
+
+@pytest.mark.parametrize("batch,width,steps", [(32, 1, 32), (8, 3, 16)])
+def test_drift_without_resync(gpu, batch, width, steps):
+    """The GPU carries its own SSM and conv pools for `steps` consecutive steps (no copy of
+    the oracle's state back into the GPU pool), the oracle its own trajectory from the same
+    inputs: the conv state stays bit-exact, every step's outputs meet the decode tolerance
+    and the SSM pool stays within rtol = atol = 2e-3 of the oracle's at the end.  With
+    width > 1, every step's accepted count is random in 1..width, so the source state and
+    the conv history come from different per-token slots and columns each step."""
+    announce(test="conv_drift", batch=batch, width=width, steps=steps)
+    case = conv_case(gpu, batch, (16, 32), pool_slots=batch * width + 2, length=3 + width - 1,
+                     bias=width > 1, seed=70 + width, width=width)
+    cpu = {k: (None if v is None else v.cpu().clone()) for k, v in case.items()}
+    gen = torch.Generator().manual_seed(71 + width)
+    flips = 0
+    for step in range(steps):
+        fresh = torch.randn(case["qkv"].shape, generator=gen).bfloat16()
+        case["qkv"].copy_(fresh.to(gpu))
+        cpu["qkv"] = fresh
+        if width > 1:
+            acc = torch.randint(1, width + 1, (batch,), generator=gen, dtype=torch.int32)
+            case["accepted"].copy_(acc.to(gpu))
+            cpu["accepted"] = acc
+        exp_out, exp_pool, pre, exp_conv, _ = expected_decode_conv(
+            cpu["qkv"], cpu["conv_state"], cpu["conv_weight"], cpu["conv_bias"],
+            *[cpu[k] for k in ORDER], 1e-6, return_pre=True)
+        torch.ops.lightdelta.decode_conv(case["qkv"], case["conv_state"], case["conv_weight"],
+                                         case["conv_bias"], *[case[k] for k in ORDER], 1e-6)
+        torch.cuda.synchronize()
+        if not torch.equal(case["conv_state"].cpu(), exp_conv):
+            raise AssertionError(f"drift step {step}: conv state differs")
+        flips += assert_bf16_outputs(case["out"], exp_out, pre, label=f"drift step {step}")["flips"]
+        cpu["pool"], cpu["conv_state"], cpu["out"] = exp_pool, exp_conv, exp_out
+    assert_states(case["pool"], cpu["pool"], label=f"SSM pool after {steps} steps")
+    print(f"conv drift B={batch} W={width}: {flips} rounding flips over {steps} steps")
