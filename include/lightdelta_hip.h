@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 8
+#define LD_ABI_VERSION 9
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -200,6 +200,26 @@ typedef struct ld_gdn_prefill_args {
 #define LD_PREFILL_CHUNKED 2      /* chunks of 64 tokens in the WY form (needs the workspace) */
 
 int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream);
+
+/* Bytes of the static device scratch of ld_gdn_prefill_static (64 MiB per GPU). */
+#define LD_PREFILL_STATIC_SCRATCH_BYTES (64LL << 20)
+
+/*
+ * ld_gdn_prefill without any allocation by anyone: the chunked form's workspace is a static
+ * device array of LD_PREFILL_STATIC_SCRATCH_BYTES in this library (one per GPU it runs on,
+ * held until the process ends) instead of args->workspace, which must be NULL with
+ * workspace_bytes 0.  Same contract and results as ld_gdn_prefill otherwise: LD_PREFILL_AUTO
+ * takes the chunked form when the shape favours it and its workspace
+ * (ld_gdn_prefill_workspace_bytes) fits the scratch, else the token-serial one;
+ * LD_PREFILL_CHUNKED beyond the scratch is rejected with LD_ERR_INVALID_ARGUMENT.  The
+ * stream must belong to the current device.  Calls on one GPU share its scratch: calls that
+ * overlap in time on one GPU race (stream-order them).  The first call on a device looks the
+ * scratch up (hipGetSymbolAddress); make it before a graph capture.  Calls no hipMalloc and no
+ * allocating routine.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ */
+int ld_gdn_prefill_static(const ld_gdn_prefill_args* args, void* stream);
 
 /*
  * Workspace bytes the chunked prefill needs for num_tokens rows in num_sequences sequences

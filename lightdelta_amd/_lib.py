@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must precede the CDLL load (see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("liblightdelta_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 CACHE_KEEP = 0
@@ -117,12 +117,14 @@ class PrefillArgs(ctypes.Structure):
 
 
 PREFILL_AUTO, PREFILL_TOKEN_SERIAL, PREFILL_CHUNKED = 0, 1, 2
+PREFILL_STATIC_SCRATCH_BYTES = 64 << 20
 
 
 # Exported entry points and their C signatures (argtypes, restype).
 SIGNATURES = {
     "ld_gdn_decode": ([ctypes.POINTER(DecodeArgs), _vp], ctypes.c_int),
     "ld_gdn_prefill": ([ctypes.POINTER(PrefillArgs), _vp], ctypes.c_int),
+    "ld_gdn_prefill_static": ([ctypes.POINTER(PrefillArgs), _vp], ctypes.c_int),
     "ld_gdn_prefill_workspace_bytes": ([_c_i64, _c_i32, _c_i32], _c_i64),
     "ld_gdn_prefill_auto_chunked": ([_c_i64, _c_i32, _c_i32], _c_i32),
     "ld_gdn_decode_conv": (

@@ -19,6 +19,8 @@
 // Also here: the gated-RMSNorm pass over raw outputs (prefill_norm_kernel, used by the
 // row-split kernels and the chunked form) and the prefill entry points of the C ABI, which
 // choose between this form and the chunked one (prefill_chunked.hip).
+#include <mutex>
+
 #include "gdn_step.h"
 
 namespace ld {
@@ -344,13 +346,10 @@ __global__ __launch_bounds__(kThreads) void prefill_norm_kernel(const DecodePara
   }
 }
 
-}  // namespace
-}  // namespace ld
-
-extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
-  using namespace ld;
-  if (args == nullptr) return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_prefill: args is NULL");
-  const ld_gdn_prefill_args& a = *args;
+// The prefill of ld_gdn_prefill, with the chunked form's workspace passed separately
+// (`workspace`, `workspace_bytes`: the caller's, or the static scratch below).
+int prefill(const ld_gdn_prefill_args& a, void* workspace, int64_t workspace_bytes,
+            void* stream) {
   if (a.num_sequences < 0) return fail(LD_ERR_INVALID_ARGUMENT, "num_sequences must be >= 0");
   if (a.algorithm < LD_PREFILL_AUTO || a.algorithm > LD_PREFILL_CHUNKED)
     return fail(LD_ERR_INVALID_ARGUMENT, "unknown prefill algorithm");
@@ -400,7 +399,7 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
   const int64_t tiles = blocks;
   const int64_t ws_need = prefill_chunked_workspace_bytes(a.num_tokens, a.num_sequences,
                                                           a.num_v_heads);
-  const bool ws_fits = a.workspace != nullptr && a.workspace_bytes >= ws_need;
+  const bool ws_fits = workspace != nullptr && workspace_bytes >= ws_need;
   if (a.algorithm == LD_PREFILL_CHUNKED && !ws_fits)
     return fail(LD_ERR_INVALID_ARGUMENT, "chunked prefill: workspace missing or too small");
   const bool chunked =
@@ -409,7 +408,7 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
        prefill_auto_chunked(a.num_tokens, a.num_sequences, a.num_v_heads));
   if (chunked) {
     const int rc = launch_prefill_chunked(p, a.num_sequences, a.num_tokens, dt_bf16,
-                                          a.workspace, s);
+                                          workspace, s);
     if (rc != LD_OK) return rc;
   }
   // Token-serial: split a head's rows over more workgroups when (sequence, head) tiles alone
@@ -455,6 +454,88 @@ extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
 #undef LD_PREFILL_LAUNCH
 #undef LD_PREFILL_ROWS_LAUNCH
   return check_launch("ld_gdn_prefill");
+}
+
+// ---- the allocation-free prefill: the chunked workspace in a static device array ----------
+//
+// `scratch` is this library's copy of the chunked form's workspace for ld_gdn_prefill_static,
+// one per GPU the library is loaded on, held until the process ends.  In host code its name
+// stands for a host-side shadow, not device memory: kernels get the address that
+// hipGetSymbolAddress returns for the current device (static_scratch), never `scratch`
+// itself.  The chunked form writes every byte of the workspace it reads later in the same
+// call (chunk index, then the per-chunk records), so nothing in it has to start at zero and
+// the previous call's contents do no harm; two calls that overlap in time on one GPU share it
+// and race.
+constexpr int64_t kStaticScratchBytes = int64_t{64} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices];  // per device ordinal, set on the device's first call
+
+// Device address of the current device's `scratch`, looked up once per device (with that
+// device current) and kept.  The stream must belong to the current device.
+int static_scratch(void* stream, void** address) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return launch_failed("ld_gdn_prefill_static: hipGetDevice", err);
+  if (device < 0 || device >= kMaxDevices)
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_prefill_static: device ordinal out of range");
+  hipDevice_t stream_device = -1;
+  err = hipStreamGetDevice(static_cast<hipStream_t>(stream), &stream_device);
+  if (err != hipSuccess) return launch_failed("ld_gdn_prefill_static: hipStreamGetDevice", err);
+  if (stream_device != device)
+    return fail(LD_ERR_INVALID_ARGUMENT,
+                "ld_gdn_prefill_static: the stream belongs to another device than the current "
+                "one");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[device] == nullptr) {
+    void* found = nullptr;
+    err = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || found == nullptr)
+      return launch_failed("ld_gdn_prefill_static: hipGetSymbolAddress(scratch)", err);
+    g_scratch_address[device] = found;
+  }
+  *address = g_scratch_address[device];
+  return LD_OK;
+}
+
+}  // namespace
+}  // namespace ld
+
+extern "C" int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream) {
+  using namespace ld;
+  if (args == nullptr) return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_prefill: args is NULL");
+  return prefill(*args, args->workspace, args->workspace_bytes, stream);
+}
+
+extern "C" int ld_gdn_prefill_static(const ld_gdn_prefill_args* args, void* stream) {
+  using namespace ld;
+  if (args == nullptr)
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_gdn_prefill_static: args is NULL");
+  const ld_gdn_prefill_args& a = *args;
+  if (a.workspace != nullptr || a.workspace_bytes != 0)
+    return fail(LD_ERR_INVALID_ARGUMENT,
+                "ld_gdn_prefill_static: workspace must be NULL (the static scratch is used)");
+  if (a.num_tokens < 0 || a.num_sequences < 0 || a.num_v_heads <= 0)
+    return prefill(a, nullptr, 0, stream);  // rejected there with its message
+  const int64_t need = prefill_chunked_workspace_bytes(a.num_tokens, a.num_sequences,
+                                                       a.num_v_heads);
+  const bool wants_chunked =
+      a.algorithm == LD_PREFILL_CHUNKED ||
+      (a.algorithm == LD_PREFILL_AUTO &&
+       prefill_auto_chunked(a.num_tokens, a.num_sequences, a.num_v_heads));
+  if (a.algorithm == LD_PREFILL_CHUNKED && need > kStaticScratchBytes)
+    return fail(LD_ERR_INVALID_ARGUMENT,
+                "ld_gdn_prefill_static: the chunked form needs more workspace than the static "
+                "scratch holds (LD_PREFILL_STATIC_SCRATCH_BYTES); use LD_PREFILL_TOKEN_SERIAL, "
+                "fewer tokens, or ld_gdn_prefill with a workspace");
+  if (a.num_sequences == 0 || !wants_chunked || need > kStaticScratchBytes)
+    return prefill(a, nullptr, 0, stream);  // token-serial: no scratch
+  void* address = nullptr;
+  const int rc = static_scratch(stream, &address);
+  if (rc != LD_OK) return rc;
+  return prefill(a, address, kStaticScratchBytes, stream);
 }
 
 extern "C" int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t num_sequences,

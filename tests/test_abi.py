@@ -22,8 +22,8 @@ def declared_functions() -> set[str]:
 
 def test_header_declares_the_entry_points():
     assert declared_functions() == {
-        "ld_gdn_decode", "ld_gdn_decode_conv", "ld_gdn_prefill", "ld_gdn_prefill_workspace_bytes",
-        "ld_gdn_prefill_auto_chunked", "ld_state_gather",
+        "ld_gdn_decode", "ld_gdn_decode_conv", "ld_gdn_prefill", "ld_gdn_prefill_static",
+        "ld_gdn_prefill_workspace_bytes", "ld_gdn_prefill_auto_chunked", "ld_state_gather",
         "ld_state_scatter",
         "ld_state_copy", "ld_state_zero", "ld_last_error", "ld_abi_version",
     }
@@ -157,3 +157,21 @@ def test_prefill_workspace_query_and_chunked_without_workspace():
 ])
 def test_prefill_auto_rule(tokens, sequences, heads, expected):
     assert _lib.load().ld_gdn_prefill_auto_chunked(tokens, sequences, heads) == expected
+
+
+def test_static_prefill_rejects_without_launching():
+    """ld_gdn_prefill_static: a caller workspace, and a chunked prefill larger than the
+    static scratch, are refused before anything touches a device."""
+    lib = _lib.load()
+    args = _lib.PrefillArgs()
+    args.num_sequences, args.num_k_heads, args.num_v_heads = 32, 16, 32
+    args.num_tokens, args.eps, args.scale = 32 * 1024, 1e-6, 128**-0.5
+    args.algorithm = _lib.PREFILL_CHUNKED
+    args.workspace, args.workspace_bytes = 256, 1 << 20
+    assert lib.ld_gdn_prefill_static(args, None) == 1
+    assert b"workspace must be NULL" in lib.ld_last_error()
+    args.workspace, args.workspace_bytes = None, 0
+    need = lib.ld_gdn_prefill_workspace_bytes(32 * 1024, 32, 32)
+    assert need > _lib.PREFILL_STATIC_SCRATCH_BYTES
+    assert lib.ld_gdn_prefill_static(args, None) == 1
+    assert b"static scratch" in lib.ld_last_error()
