@@ -24,17 +24,27 @@ in the 256 MB Infinity Cache between consecutive steps.  A second, cache-cold fi
 16 disjoint slot sets through a 1024-slot (2 GiB) pool with the "stream" policy
 (non-temporal state traffic), the regime of a many-layer model.
 
-Further figures in the same line: `conv_fused` (the same step with the width-4 causal
-conv1d + SiLU fused in front), `prefill` (32 x 1024, 1 x 4096 and 1024 x 32 tokens, both
-algorithms), `mtp_verify` (B=64, T=4 verify plus the commit at a random accepted length), `copies`
-(gather / scatter / slot-to-slot copy of 128 random pairs in a 1024-slot pool, and the bf16
-conv pool) and `stack48` (48 layers captured as one HIP graph, batch 128, 1024 slots per
-layer = 96 GiB of state, slot ids reshuffled before every replay, 256 replays timed end to
-end; --no-stack skips it).
+Further figures in the same line:
+  conv_fused      the step with the width-4 causal conv1d + SiLU fused in front: hot (B=32),
+                  cold (slot sets rotated through 2048-slot pools) and a B=64, T=4 verify;
+  config1         the first workload configuration (B=1, 4/8 heads, conv-fused, zero conv
+                  state): graph and eager latency per step;
+  operator_table  the reference's own operator benchmark (16/48 heads, B 1/4/8 x T 1-4,
+                  eager "indexed" and HIP-graph medians, its method), beside its H100 medians;
+  host_cost       host time of one eager GDNBackend call at B=1 and B=8;
+  prefill         32 x 1024, 1 x 4096 and 1024 x 32 tokens under both algorithms;
+  mtp_verify      B=64, T=4 verify plus the commit at a random accepted length (hot);
+  mtp_verify_cold the same verify with slot sets rotated through a 4 GiB pool;
+  copies          gather / scatter / slot-to-slot copy of 128 random pairs in a 1024-slot
+                  pool, and the bf16 conv pool;
+  stack48         48 layers captured as one HIP graph, batch 128, 1024 slots per layer =
+                  96 GiB of state, slot ids reshuffled before every replay, 256 replays timed
+                  end to end (--no-stack skips it).
 
 CPU baseline: the reference's packed Torch path (index_select gather, unfused GDN,
-index_copy_ write-back; oracle/decode.py) on the host cores at the same shapes, timed for a
-bounded number of steps.
+index_copy_ write-back; oracle/decode.py) on every host core this process may use, at the
+headline shapes and at the first configuration (with torch's conv1d in front), timed on
+bounded samples.
 """
 
 from __future__ import annotations
@@ -57,6 +67,13 @@ HBM_PEAK_GBS = 8000.0
 ORDER = ("qkv", "a", "b", "a_log", "dt_bias", "slots", "cu", "accepted", "pool", "gate",
          "weight", "out")
 TRAFFIC_FILE = ROOT / "profiles" / "gdn_decode_b32_traffic.json"
+# The reference's published H100 operator medians (docs/performance.md:12-25 of the
+# reference; 16/48 heads): (batch, tokens per request) -> (indexed us, graph us).
+REF_H100_US = {
+    (1, 1): (17.47, 12.38), (1, 2): (18.91, 14.11), (1, 3): (21.22, 16.14), (1, 4): (19.90, 19.17),
+    (4, 1): (18.27, 14.72), (4, 2): (19.73, 19.50), (4, 3): (24.70, 24.48), (4, 4): (30.46, 30.10),
+    (8, 1): (20.48, 20.21), (8, 2): (31.98, 31.84), (8, 3): (42.24, 42.29), (8, 4): (53.73, 53.57),
+}
 
 
 def parse_args():
@@ -75,6 +92,9 @@ def parse_args():
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-mtp", action="store_true", help="skip the B=64, T=4 verify + commit")
     p.add_argument("--no-copies", action="store_true", help="skip the state-pool copy kernels")
+    p.add_argument("--no-table", action="store_true",
+                   help="skip the reference's operator table (16/48 heads, B 1-8, T 1-4) and "
+                        "the host-cost figure")
     p.add_argument("--no-graph", action="store_true",
                    help="time K eager launches instead of one K-step graph replay")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -131,75 +151,315 @@ def timed_replay(graph):
     return start.elapsed_time(end) / 1000.0
 
 
-def cpu_baseline(seconds: float) -> dict:
-    """The reference Torch path on the host CPU, same shapes, bounded sample."""
-    import torch
-
-    from lightdelta_amd.workloads import decode_case
-    from oracle.decode import packed_reference_step
-
-    threads = torch.get_num_threads()
-    case = decode_case(BATCH, 1, num_k_heads=H, num_v_heads=HV, pool_slots=POOL, seed=0,
-                       device="cpu")
-    scratch = case["pool"].new_empty((1 + BATCH, *case["pool"].shape[1:]))
-    args = [case[k] for k in ORDER]
-    packed_reference_step(*args, 1e-6, scratch=scratch)  # warm-up
-    times = []
-    deadline = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < deadline and len(times) < 2000):
-        t0 = time.perf_counter()
-        packed_reference_step(*args, 1e-6, scratch=scratch)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    median = times[len(times) // 2]
+def _cpu_model() -> str:
     cpu = platform.processor() or platform.machine()
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
             if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return cpu
+
+
+def _time_cpu(step, seconds, at_least=3, at_most=2000):
+    """Median seconds per call of step() over a sample bounded by `seconds` of CPU time."""
+    step()  # warm-up
+    times = []
+    deadline = time.perf_counter() + seconds
+    while len(times) < at_least or (time.perf_counter() < deadline and len(times) < at_most):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The reference's Torch path on the host CPU, timed on bounded samples of the same
+    workloads: the packed path (index_select gather, unfused GDN, index_copy_ write-back;
+    oracle/decode.py) at the headline configuration (B=32, 16/32 heads), and at B=1, 4/8
+    heads with the width-4 causal conv (oracle/conv.py) in front.  Torch uses every core this
+    process may run on (os.sched_getaffinity)."""
+    import torch
+
+    from lightdelta_amd.workloads import decode_case
+    from oracle import conv as conv_oracle
+    from oracle.decode import packed_reference_step
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    case = decode_case(BATCH, 1, num_k_heads=H, num_v_heads=HV, pool_slots=POOL, seed=0,
+                       device="cpu")
+    scratch = case["pool"].new_empty((1 + BATCH, *case["pool"].shape[1:]))
+    args = [case[k] for k in ORDER]
+    median, count = _time_cpu(lambda: packed_reference_step(*args, 1e-6, scratch=scratch),
+                              seconds * 0.75)
+
+    c1 = decode_case(1, 1, num_k_heads=4, num_v_heads=8, pool_slots=3, seed=0, device="cpu")
+    conv_dim = c1["qkv"].shape[1]
+    conv_state = torch.zeros(3, conv_dim, 3, dtype=torch.bfloat16)
+    conv_weight = (torch.randn(conv_dim, 4, generator=torch.Generator().manual_seed(1)) / 2
+                   ).bfloat16()
+    pre_conv = c1["qkv"].clone()
+    c1_args = [c1[k] for k in ORDER]
+    c1_scratch = c1["pool"].new_empty((2, *c1["pool"].shape[1:]))
+
+    def config1_step():  # conv through torch's conv1d (groups = channels), then the shift
+        window = conv_state[1:2]
+        c1_args[0] = conv_oracle.conv_update_reference_form(pre_conv, window, conv_weight)
+        conv_state[1:2] = torch.cat([window[..., 1:], pre_conv[..., None]], -1)
+        packed_reference_step(*c1_args, 1e-6, scratch=c1_scratch)
+
+    median1, count1 = _time_cpu(config1_step, seconds * 0.25)
     return {
         "value": round(1.0 / median, 3),
         "unit": "steps/s",
-        "cores": threads,
+        "cores": cores,
         "kind": "port",
-        "sample": f"{len(times)} steps of the packed Torch reference path (index_select gather, "
+        "sample": f"{count} steps of the packed Torch reference path (index_select gather, "
                   f"unfused GDN, index_copy_ write-back) at B=32, 16/32 heads, 256-slot pool; "
-                  f"median step {median * 1e3:.1f} ms; {cpu}",
+                  f"median step {median * 1e3:.2f} ms; torch threads {cores}; {_cpu_model()}",
+        "config1": {
+            "value": round(1.0 / median1, 2),
+            "unit": "steps/s",
+            "us_per_step": round(median1 * 1e6, 1),
+            "sample": f"{count1} steps at B=1, 4/8 heads: width-4 causal conv + SiLU from a "
+                      f"zero conv state, then the packed Torch path",
+        },
     }
+
+
+def _graph_us(fn, steps):
+    """us per call of `steps` calls of fn captured in one HIP graph, one timed replay."""
+    import torch
+
+    graph = capture(fn, steps)
+    graph.replay()
+    torch.cuda.synchronize()
+    return timed_replay(graph) * 1e6 / steps
 
 
 def conv_fused(case, op_args, steps, device):
-    """The same step with the causal conv1d (width 4, SiLU, conv state of 3 columns, bf16
-    pool of 256 slots x 8192 channels) fused in front: one decode_conv launch per step on the
-    pre-conv activations."""
+    """The step with the causal conv1d (width 4, SiLU, bf16 conv pool of 8192 channels, no
+    bias) fused in front, one decode_conv launch per step on the pre-conv activations:
+    `hot` (B=32, the same 32 slots, keep policy), `cold` (B=32, 16 disjoint slot sets
+    rotated through 2048-slot SSM and conv pools, stream policy) and `verify` (B=64, T=4
+    speculative verify with a 6-column conv state and random accepted counts, hot)."""
     import torch
+
+    from lightdelta_amd import ops
+    from lightdelta_amd.workloads import decode_case
 
     conv_dim = case["qkv"].shape[1]
     gen = torch.Generator().manual_seed(1)
-    conv_state = torch.randn(POOL, conv_dim, 3, generator=gen).bfloat16().to(device)
     conv_weight = (torch.randn(conv_dim, 4, generator=gen) / 2).bfloat16().to(device)
-    rest = op_args[1:]
+    saved = ops.state_cache_policy()
+    result = {"workload": "decode_conv: width-4 causal conv1d + SiLU fused in front of the "
+                          "GDN step, bf16 conv pool of 8192 channels, no bias"}
+    try:
+        ops.set_state_cache_policy("keep")
+        conv_state = torch.randn(POOL, conv_dim, 3, generator=gen).bfloat16().to(device)
+        rest = op_args[1:]
+        hot = lambda: torch.ops.lightdelta.decode_conv(  # noqa: E731
+            case["qkv"], conv_state, conv_weight, None, *rest, 1e-6)
+        us = _graph_us(hot, steps)
+        conv_bytes = BATCH * conv_dim * 3 * 2 * 2  # conv state columns read + written
+        result["hot"] = {
+            "us_per_step": round(us, 3), "steps_per_s": round(1e6 / us, 1),
+            "state_TBps": round(STATE_BYTES / us / 1e6, 3),
+            "frac": round((STATE_BYTES + conv_bytes) / us / 1e3 / HBM_PEAK_GBS, 4),
+            "cache_policy": "keep"}
+        del conv_state
+
+        ops.set_state_cache_policy("stream")
+        big = torch.empty(2049, HV, DIM, DIM, device=device).normal_(0.0, 0.02)
+        big_conv = torch.zeros(2049, conv_dim, 3, dtype=torch.bfloat16, device=device)
+        perm = torch.randperm(2048, device=device)[: 16 * BATCH] + 1
+        sets = [perm[i * BATCH:(i + 1) * BATCH].to(torch.int32).view(BATCH, 1) for i in range(16)]
+        cold_args = list(rest)
+        pool_at, slots_at = ORDER.index("pool") - 1, ORDER.index("slots") - 1
+        cold_args[pool_at] = big
+
+        def cold_pass():
+            for slots in sets:
+                cold_args[slots_at] = slots
+                torch.ops.lightdelta.decode_conv(case["qkv"], big_conv, conv_weight, None,
+                                                 *cold_args, 1e-6)
+
+        us = _graph_us(cold_pass, max(1, steps // 16)) / 16
+        result["cold"] = {
+            "us_per_step": round(us, 3), "steps_per_s": round(1e6 / us, 1),
+            "frac": round((STATE_BYTES + conv_bytes) / us / 1e3 / HBM_PEAK_GBS, 4),
+            "cache_policy": "stream"}
+        del big, big_conv
+
+        ops.set_state_cache_policy("keep")
+        batch, width = 64, 4
+        v = decode_case(batch, width, num_k_heads=H, num_v_heads=HV,
+                        pool_slots=batch * width + 2, seed=5, device=device)
+        v["accepted"].copy_(torch.randint(1, width + 1, (batch,), generator=gen).int())
+        v_conv = torch.randn(batch * width + 2, conv_dim, 3 + width - 1, generator=gen
+                             ).bfloat16().to(device)
+        v_args = [v[k] for k in ORDER[1:]]
+        verify = lambda: torch.ops.lightdelta.decode_conv(  # noqa: E731
+            v["qkv"], v_conv, conv_weight, None, *v_args, 1e-6)
+        us = _graph_us(verify, steps)
+        v_bytes = batch * HV * 65536 * (1 + width) + batch * conv_dim * 6 * 2 * 2
+        result["verify_b64_t4"] = {
+            "us_per_step": round(us, 3), "tokens_per_s": round(batch * width * 1e6 / us, 1),
+            "TBps": round(v_bytes / us / 1e6, 3), "cache_policy": "keep",
+            "accepted": "random in 1..4 per request, conv state of 6 columns"}
+    finally:
+        ops.set_state_cache_policy(saved)
+    return result
+
+
+def operator_table(device, iterations=30):
+    """The reference's operator benchmark, same shapes and method (benchmarks/gdn.py:13-94 of
+    the reference): 16 qk / 48 v heads, B in {1, 4, 8} x T in {1..4}, its seeded inputs
+    (qkv and gate bf16 0.2 N(0,1), pool 0.1 N(0,1) over slots 1..B*T, bf16 dt_bias and norm
+    weight), five warm-up calls on a side stream, then `iterations` samples that each restore
+    the pool outside the timed interval and time one call with HIP events: `indexed` an eager
+    GDNBackend call (indexed state access, host dispatch included), `graph` the replay of
+    that call captured in a HIP graph.  Medians in us, beside the reference's H100 medians
+    (docs/performance.md:12-25 of the reference)."""
+    import statistics
+
+    import torch
+
+    from lightdelta_amd import ops
+    from lightdelta_amd.backend import GDNBackend
+    from lightdelta_amd.config import BackendConfig
+
+    saved = ops.state_cache_policy()
+    ops.set_state_cache_policy("keep")  # the pool is restored (written) right before each call
+    rows = {}
+    try:
+        for batch in (1, 4, 8):
+            for width in (1, 2, 3, 4):
+                torch.manual_seed(42)
+                n = batch * width
+                qkvz = torch.randn(n, 16384, device=device, dtype=torch.bfloat16) * 0.2
+                ba = torch.randn(n, 96, device=device, dtype=torch.bfloat16)
+                pool = torch.randn(n + 1, 48, 128, 128, device=device) * 0.1
+                state = pool.clone()
+                case = dict(
+                    qkv=qkvz[:, :10240], a=ba[:, 48:], b=ba[:, :48],
+                    a_log=torch.randn(48, device=device),
+                    dt_bias=torch.randn(48, device=device, dtype=torch.bfloat16),
+                    slots=torch.arange(1, n + 1, device=device, dtype=torch.int32).view(batch, width),
+                    cu=torch.arange(0, n + 1, width, device=device, dtype=torch.int32),
+                    accepted=torch.ones(batch, device=device, dtype=torch.int32),
+                    pool=pool, gate=qkvz[:, 10240:].view(n, 48, 128),
+                    weight=torch.randn(128, device=device, dtype=torch.bfloat16),
+                    out=torch.empty(n, 48, 128, device=device, dtype=torch.bfloat16),
+                )
+                backend = GDNBackend(BackendConfig(compute="cuda_fused", state_io="indexed"))
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    for _ in range(5):
+                        pool.copy_(state)
+                        backend(**case)
+                torch.cuda.current_stream().wait_stream(side)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    backend(**case)
+                cell = {}
+                for name, execute in (("indexed", lambda: backend(**case)),
+                                      ("graph", graph.replay)):
+                    timers = []
+                    for _ in range(iterations):
+                        start, end = events()
+                        pool.copy_(state)
+                        start.record()
+                        execute()
+                        end.record()
+                        timers.append((start, end))
+                    torch.cuda.synchronize()
+                    cell[f"{name}_us"] = round(statistics.median(
+                        a.elapsed_time(b) * 1000 for a, b in timers), 2)
+                ref_indexed, ref_graph = REF_H100_US[(batch, width)]
+                cell["h100_indexed_us"], cell["h100_graph_us"] = ref_indexed, ref_graph
+                cell["speedup_indexed"] = round(ref_indexed / cell["indexed_us"], 2)
+                cell["speedup_graph"] = round(ref_graph / cell["graph_us"], 2)
+                rows[f"B{batch}_T{width}"] = cell
+                del graph, case, pool, state, qkvz, ba
+    finally:
+        ops.set_state_cache_policy(saved)
+    rows["workload"] = ("the reference's operator benchmark: 16 qk / 48 v heads, indexed state "
+                        "access, eager (host dispatch included) and HIP-graph replay, median of "
+                        f"{iterations} samples, pool restored outside the timed interval; "
+                        "h100_* = the reference's published H100 medians")
+    return rows
+
+
+def config1(device, steps):
+    """The first workload configuration on the GPU: B=1, 4 qk / 8 v heads, the conv-fused
+    step (width-4 conv from a zero conv state, SiLU) on one layer, `steps` consecutive
+    in-place steps: graph replay (us per step) and eager calls (HIP events around each call,
+    host dispatch included, median)."""
+    import statistics
+
+    import torch
+
+    from lightdelta_amd.workloads import decode_case
+
+    case = decode_case(1, 1, num_k_heads=4, num_v_heads=8, pool_slots=3, seed=0, device=device)
+    conv_dim = case["qkv"].shape[1]
+    conv_state = torch.zeros(3, conv_dim, 3, dtype=torch.bfloat16, device=device)
+    conv_weight = (torch.randn(conv_dim, 4, generator=torch.Generator().manual_seed(1)) / 2
+                   ).bfloat16().to(device)
+    rest = [case[k] for k in ORDER[1:]]
     step = lambda: torch.ops.lightdelta.decode_conv(  # noqa: E731
         case["qkv"], conv_state, conv_weight, None, *rest, 1e-6)
-    for _ in range(4):
+    graph_us = _graph_us(step, steps)
+    timers = []
+    for _ in range(50):
+        start, end = events()
+        start.record()
         step()
-    graph = capture(step, steps)
-    graph.replay()
+        end.record()
+        timers.append((start, end))
     torch.cuda.synchronize()
-    elapsed = timed_replay(graph)
-    rate = steps / elapsed
-    conv_bytes = BATCH * conv_dim * 3 * 2 * 2  # conv state columns read + written
+    eager = statistics.median(a.elapsed_time(b) * 1000 for a, b in timers)
     return {
-        "workload": "same step with the width-4 causal conv1d + SiLU fused in front "
-                    "(bf16 conv pool 256 x 8192 x 3, no bias)",
-        "steps_per_s": round(rate, 1),
-        "us_per_step": round(elapsed * 1e6 / steps, 3),
-        "state_TBps": round(STATE_BYTES * rate / 1e12, 3),
-        "frac": round((STATE_BYTES + conv_bytes) * rate / 1e9 / HBM_PEAK_GBS, 4),
+        "workload": "B=1, 4 qk / 8 v heads, dk=dv=128, conv-fused decode step from a zero conv "
+                    "state, in place",
+        "graph_us_per_step": round(graph_us, 3),
+        "steps_per_s": round(1e6 / graph_us, 1),
+        "eager_us_per_step": round(eager, 2),
     }
+
+
+def host_cost(device, calls=2000):
+    """Host time of one eager GDNBackend call (indexed, T=1, 16/48 heads) at B=1 and B=8:
+    `calls` back-to-back calls timed with the host clock, no synchronisation between them."""
+    import torch
+
+    from lightdelta_amd.backend import GDNBackend
+    from lightdelta_amd.config import BackendConfig
+    from lightdelta_amd.workloads import decode_case
+
+    backend = GDNBackend(BackendConfig(compute="cuda_fused", state_io="indexed"))
+    result = {}
+    for batch in (1, 8):
+        case = decode_case(batch, 1, num_k_heads=16, num_v_heads=48, pool_slots=batch + 2,
+                           seed=0, device=device)
+        args = [case[k] for k in ORDER]
+        for _ in range(50):
+            backend(*args, 1e-6)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            backend(*args, 1e-6)
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        result[f"B{batch}_us_per_call"] = round((t1 - t0) / calls * 1e6, 2)
+    result["workload"] = ("host time per eager GDNBackend call (validation, argument packing, "
+                          "launch), 16/48 heads, T=1")
+    return result
 
 
 def prefill(device):
@@ -380,6 +640,50 @@ def mtp_verify(steps, device):
     }
 
 
+def mtp_verify_cold(device, passes=4):
+    """The B=64, T=4 verify step cache-cold: 8 disjoint sets of 256 slots (home + 3 per
+    sequence) rotated through a 2049-slot (4 GiB) pool, stream policy, `passes` rounds of the
+    8 sets captured in one HIP graph; one read and 4 writes of every tile (the commit is not
+    part of this figure)."""
+    import torch
+
+    from lightdelta_amd import ops
+    from lightdelta_amd.workloads import decode_case
+
+    batch, width = 64, 4
+    case = decode_case(batch, width, num_k_heads=H, num_v_heads=HV, pool_slots=8, seed=5,
+                       device=device)
+    big = torch.empty(2049, HV, DIM, DIM, device=device).normal_(0.0, 0.02)
+    perm = torch.randperm(2048, device=device)[: 8 * batch * width] + 1
+    sets = [perm[i * batch * width:(i + 1) * batch * width].to(torch.int32).view(batch, width)
+            for i in range(8)]
+    args = [case[k] for k in ORDER]
+    args[ORDER.index("pool")] = big
+
+    def rounds():
+        for slots in sets:
+            args[ORDER.index("slots")] = slots
+            torch.ops.lightdelta.decode(*args, 1e-6)
+
+    saved = ops.state_cache_policy()
+    ops.set_state_cache_policy("stream")
+    try:
+        us = _graph_us(rounds, passes) / 8
+    finally:
+        ops.set_state_cache_policy(saved)
+    nbytes = batch * HV * 65536 * (1 + width)
+    del big
+    return {
+        "workload": "MTP verify B=64, T=4, 16 qk / 32 v heads, 8 disjoint slot sets rotated "
+                    "through a 4 GiB pool (cache-cold), stream policy",
+        "us_per_step": round(us, 2),
+        "tokens_per_s": round(batch * width * 1e6 / us, 1),
+        "bytes_per_step": nbytes,
+        "TBps": round(nbytes / us / 1e6, 3),
+        "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+    }
+
+
 def stack48(steps, device):
     """48 GDN decode layers captured as one HIP graph, batch 128, 16 qk / 32 v heads, 1024
     slots per layer (96 GiB fp32 state), stream cache policy; the slot ids (shared by every
@@ -536,6 +840,9 @@ def main():
             "kernel_mean_us": round(launch_us, 3),
             "algorithmic_bytes": STATE_BYTES,
             "cache_policy": ops.state_cache_policy(),
+            "regime": "Infinity-Cache resident: the workload steps the same 32 slots (64 MiB) in "
+                      "place, which stay in the 256 MB Infinity Cache between steps; the "
+                      "HBM-bound figures are `cold` and `stack48`",
         },
     }
 
@@ -572,12 +879,18 @@ def main():
 
     if not args.no_conv:
         result["conv_fused"] = conv_fused(case, op_args, args.steps, device)
+        result["config1"] = config1(device, args.steps)
+
+    if not args.no_table:
+        result["operator_table"] = operator_table(device)
+        result["host_cost"] = host_cost(device)
 
     if not args.no_prefill:
         result["prefill"] = prefill(device)
 
     if not args.no_mtp:
         result["mtp_verify"] = mtp_verify(args.steps, device)
+        result["mtp_verify_cold"] = mtp_verify_cold(device)
 
     if not args.no_copies:
         result["copies"] = copies(device)

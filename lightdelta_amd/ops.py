@@ -107,11 +107,25 @@ def _require(condition: bool, message: str) -> None:
 
 
 def _is_gpu(t: torch.Tensor) -> bool:
-    return t.device.type == "cuda"
+    return t.is_cuda
 
 
-def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+_BF16, _F32, _I32 = torch.bfloat16, torch.float32, torch.int32
+
+# The calling thread's current device and a device's current stream as plain integers:
+# torch's raw accessors where this build has them (torch.cuda.current_stream() builds a Stream
+# object, ~2 us per call), the public API otherwise.
+_current_device = getattr(torch._C, "_cuda_getDevice", torch.cuda.current_device)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(device) -> int:
+    index = device if isinstance(device, int) else device.index
+    if index is None:
+        index = _current_device()
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 class _DeviceGuard:
@@ -119,12 +133,13 @@ class _DeviceGuard:
 
     __slots__ = ("index", "previous")
 
-    def __init__(self, device: torch.device):
-        self.index = device.index if device.index is not None else torch.cuda.current_device()
+    def __init__(self, device):
+        index = device if isinstance(device, int) else device.index
+        self.index = index if index is not None else _current_device()
         self.previous = None
 
     def __enter__(self):
-        current = torch.cuda.current_device()
+        current = _current_device()
         if current != self.index:
             self.previous = current
             torch.cuda.set_device(self.index)
@@ -155,71 +170,60 @@ def decode_geometry(qkv: torch.Tensor, state: torch.Tensor) -> tuple[int, int]:
     return (h, hv) if valid else (0, hv)
 
 
-def check_decode(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out, eps):
-    """Validation of lightdelta::decode (reference csrc/gdn_decode.cu:366-403)."""
-    _require(_is_gpu(qkv) and qkv.dtype == torch.bfloat16, "qkv must be CUDA BF16")
-    device = qkv.device
+def _decode_layout(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out,
+                   eps):
+    """Validation of lightdelta::decode (reference csrc/gdn_decode.cu:366-403), reading each
+    tensor property once: returns (H, HV, device index, requests, width) and the row strides
+    of qkv, a, b, state and gate, which the launch needs."""
+    if not (_is_gpu(qkv) and qkv.dtype is _BF16):
+        raise RuntimeError("qkv must be CUDA BF16")
+    dev = qkv.get_device()
     for t in (a, b, gate, out):
-        _require(
-            t.device == device and t.dtype == torch.bfloat16 and t.dim() > 0 and t.stride(-1) == 1,
-            "activations must be BF16 with dense rows",
-        )
+        if not (t.get_device() == dev and t.dtype is _BF16 and t.dim() > 0 and t.stride(-1) == 1):
+            raise RuntimeError("activations must be BF16 with dense rows")
     for t in (a_log, state):
-        _require(
-            t.device == device and t.dtype == torch.float32 and t.dim() > 0 and t.stride(-1) == 1,
-            "state and A_log must be CUDA FP32 with dense rows",
-        )
+        if not (t.get_device() == dev and t.dtype is _F32 and t.dim() > 0 and t.stride(-1) == 1):
+            raise RuntimeError("state and A_log must be CUDA FP32 with dense rows")
     for t in (indices, cu, accepted):
-        _require(
-            t.device == device and t.dtype == torch.int32 and t.is_contiguous(),
-            "metadata must be contiguous CUDA int32",
-        )
+        if not (t.get_device() == dev and t.dtype is _I32 and t.is_contiguous()):
+            raise RuntimeError("metadata must be contiguous CUDA int32")
     for t in (dt_bias, weight):
-        _require(
-            t.device == device and t.is_contiguous() and t.dtype in _FLOATS,
-            "weights must be contiguous FP32/BF16",
-        )
+        if not (t.get_device() == dev and t.is_contiguous() and t.dtype in _FLOATS):
+            raise RuntimeError("weights must be contiguous FP32/BF16")
+    qkv_shape, qkv_stride = qkv.shape, qkv.stride()
+    state_shape, state_stride = state.shape, state.stride()
     h, hv = decode_geometry(qkv, state)
-    _require(
-        qkv.dim() == 2 and h > 0 and qkv.stride(1) == 1,
-        "qkv must be [tokens,(2*H+HV)*128] with HV a multiple of H",
-    )
-    _require(
-        state.dim() == 4
-        and state.shape[2] == HEAD_DIM
-        and state.shape[3] == HEAD_DIM
-        and state.stride(2) == HEAD_DIM
-        and state.stride(1) == HEAD_DIM * HEAD_DIM,
-        "state must be [slots,HV,128,128]",
-    )
-    _require(
-        indices.dim() == 2 and 1 <= indices.shape[1] <= _lib.MAX_TOKENS,
-        "decode/MTP supports 1 through 4 tokens per request",
-    )
-    n = qkv.shape[0]
-    _require(
-        tuple(a.shape) == (n, hv)
-        and tuple(b.shape) == (n, hv)
-        and tuple(gate.shape) == (n, hv, HEAD_DIM)
-        and tuple(out.shape) == (n, hv, HEAD_DIM)
-        and out.is_contiguous()
-        and gate.stride(1) == HEAD_DIM,
-        "invalid activation shape or output layout",
-    )
-    _require(
-        a_log.numel() == hv and dt_bias.numel() == hv and weight.numel() == HEAD_DIM,
-        "invalid weight shapes",
-    )
-    requests = indices.shape[0]
-    _require(
-        cu.dim() == 1
-        and cu.numel() == requests + 1
-        and accepted.dim() == 1
-        and accepted.numel() == requests,
-        "invalid request metadata shapes",
-    )
-    _require(eps > 0, "norm epsilon must be positive")
-    return h, hv
+    if not (len(qkv_shape) == 2 and h > 0 and qkv_stride[1] == 1):
+        raise RuntimeError("qkv must be [tokens,(2*H+HV)*128] with HV a multiple of H")
+    if not (len(state_shape) == 4 and state_shape[2] == HEAD_DIM and state_shape[3] == HEAD_DIM
+            and state_stride[2] == HEAD_DIM and state_stride[1] == HEAD_DIM * HEAD_DIM):
+        raise RuntimeError("state must be [slots,HV,128,128]")
+    indices_shape = indices.shape
+    if not (len(indices_shape) == 2 and 1 <= indices_shape[1] <= _lib.MAX_TOKENS):
+        raise RuntimeError("decode/MTP supports 1 through 4 tokens per request")
+    n = qkv_shape[0]
+    gate_stride = gate.stride()
+    if not (a.shape == (n, hv) and b.shape == (n, hv) and gate.shape == (n, hv, HEAD_DIM)
+            and out.shape == (n, hv, HEAD_DIM) and out.is_contiguous()
+            and gate_stride[1] == HEAD_DIM):
+        raise RuntimeError("invalid activation shape or output layout")
+    if not (a_log.numel() == hv and dt_bias.numel() == hv and weight.numel() == HEAD_DIM):
+        raise RuntimeError("invalid weight shapes")
+    requests = indices_shape[0]
+    if not (cu.dim() == 1 and cu.numel() == requests + 1 and accepted.dim() == 1
+            and accepted.numel() == requests):
+        raise RuntimeError("invalid request metadata shapes")
+    if not eps > 0:
+        raise RuntimeError("norm epsilon must be positive")
+    return (h, hv, dev, requests, indices_shape[1], qkv_stride[0], a.stride(0), b.stride(0),
+            state_stride[0], gate_stride[0])
+
+
+def check_decode(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out, eps):
+    """Validation of lightdelta::decode (reference csrc/gdn_decode.cu:366-403); returns
+    (H, HV)."""
+    return _decode_layout(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight,
+                          out, eps)[:2]
 
 
 def check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state, gate,
@@ -299,43 +303,25 @@ def _dtype_code(t: torch.Tensor) -> int:
 
 
 def _decode_impl(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out, eps):
-    h, hv = check_decode(
-        qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out, eps
-    )
-    requests = indices.shape[0]
+    (h, hv, dev, requests, width, qkv_row, a_row, b_row, slot_stride,
+     gate_row) = _decode_layout(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate,
+                                weight, out, eps)
     if requests == 0:
         return
-    args = _lib.DecodeArgs(
-        qkv.data_ptr(),
-        qkv.stride(0),
-        a.data_ptr(),
-        a.stride(0),
-        b.data_ptr(),
-        b.stride(0),
-        a_log.data_ptr(),
-        dt_bias.data_ptr(),
-        _dtype_code(dt_bias),
-        _dtype_code(weight),
-        indices.data_ptr(),
-        cu.data_ptr(),
-        accepted.data_ptr(),
-        state.data_ptr(),
-        state.stride(0),
-        gate.data_ptr(),
-        gate.stride(0),
-        weight.data_ptr(),
-        out.data_ptr(),
-        requests,
-        indices.shape[1],
-        h,
-        hv,
-        QK_SCALE,
-        eps,
-        _cache_policy,
-    )
-    lib = _lib.load()
-    with _DeviceGuard(qkv.device):
-        _lib.check(lib.ld_gdn_decode(args, _stream(qkv.device)))
+    args = _lib.DECODE_ARGS.pack(
+        qkv.data_ptr(), qkv_row, a.data_ptr(), a_row, b.data_ptr(), b_row, a_log.data_ptr(),
+        dt_bias.data_ptr(), _lib.DTYPE_BF16 if dt_bias.dtype is _BF16 else _lib.DTYPE_F32,
+        _lib.DTYPE_BF16 if weight.dtype is _BF16 else _lib.DTYPE_F32, indices.data_ptr(),
+        cu.data_ptr(), accepted.data_ptr(), state.data_ptr(), slot_stride, gate.data_ptr(),
+        gate_row, weight.data_ptr(), out.data_ptr(), requests, width, h, hv, QK_SCALE, eps,
+        _cache_policy)
+    launch = _lib.packed("ld_gdn_decode")
+    current = _current_device()
+    if current == dev:
+        _lib.check(launch(args, _stream(dev)))
+        return
+    with _DeviceGuard(dev):
+        _lib.check(launch(args, _stream(dev)))
 
 
 def check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log, dt_bias,
