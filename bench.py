@@ -388,10 +388,32 @@ def operator_table(device, iterations=30):
                 del graph, case, pool, state, qkvz, ba
     finally:
         ops.set_state_cache_policy(saved)
+    # The same method on a one-kernel graph of a trivial torch op: what a HIP graph replay
+    # costs on this platform before any work of ours.
+    x = torch.zeros(1, device=device)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        x.add_(1)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        x.add_(1)
+    timers = []
+    for _ in range(iterations):
+        start, end = events()
+        start.record()
+        graph.replay()
+        end.record()
+        timers.append((start, end))
+    torch.cuda.synchronize()
+    rows["graph_replay_floor_us"] = round(statistics.median(
+        a.elapsed_time(b) * 1000 for a, b in timers), 2)
     rows["workload"] = ("the reference's operator benchmark: 16 qk / 48 v heads, indexed state "
                         "access, eager (host dispatch included) and HIP-graph replay, median of "
                         f"{iterations} samples, pool restored outside the timed interval; "
-                        "h100_* = the reference's published H100 medians")
+                        "h100_* = the reference's published H100 medians; graph_replay_floor_us "
+                        "= the replay of a one-kernel graph of torch's x.add_(1), same method")
     return rows
 
 

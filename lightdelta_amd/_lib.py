@@ -9,7 +9,6 @@ process).  There is no fallback: a missing or unloadable library raises.
 from __future__ import annotations
 
 import ctypes
-import struct
 import threading
 from pathlib import Path
 
@@ -117,11 +116,6 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
-# ld_gdn_decode_args packed without ctypes objects (the fields of DecodeArgs in order, native
-# alignment, padded to the struct's 176 bytes): the per-call path of the decode op, ~1 us
-# cheaper than building a DecodeArgs.
-DECODE_ARGS = struct.Struct("@PqPqPqPPiiPPPPqPqPPiiiiffi4x")
-
 PREFILL_AUTO, PREFILL_TOKEN_SERIAL, PREFILL_CHUNKED = 0, 1, 2
 PREFILL_STATIC_SCRATCH_BYTES = 64 << 20
 
@@ -177,23 +171,6 @@ def load() -> ctypes.CDLL:
                 raise RuntimeError(f"{LIBRARY_PATH.name} ABI {version}, expected {ABI_VERSION}")
             _lib = lib
     return _lib
-
-
-_packed: dict = {}
-
-
-def packed(name: str):
-    """Entry point `name` taking its argument struct as packed bytes (e.g. DECODE_ARGS.pack)
-    and the stream as an integer: a function object of its own, so the argtypes of
-    load().<name> (the ctypes structure pointer) stay as they are."""
-    fn = _packed.get(name)
-    if fn is None:
-        lib = load()
-        fn = lib._FuncPtr((name, lib))
-        fn.argtypes = [ctypes.c_char_p, ctypes.c_void_p]
-        fn.restype = ctypes.c_int
-        _packed[name] = fn
-    return fn
 
 
 def check(code: int) -> None:

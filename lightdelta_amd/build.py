@@ -18,6 +18,8 @@ ROOT = PACKAGE.parent
 CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "liblightdelta_hip.so"
+# torch.ops.lightdelta dispatcher kernels (host C++ over the C ABI; see csrc/torch_ops.cpp)
+TORCH_LIBRARY = PACKAGE / "liblightdelta_torch.so"
 SOURCES = ("abi.hip", "gdn_decode.hip", "prefill_serial.hip", "prefill_chunked.hip",
            "state_io.hip")
 ARCH = "gfx950"
@@ -45,6 +47,10 @@ HIPCC_FLAGS = [
 # and the head count as its first 7 argument dwords, which the hardware then preloads into
 # SGPRs at launch (kernels without such leading scalar arguments preload nothing).
 EXTRA_FLAGS = {"gdn_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=7"]}
+
+
+def _rocm() -> Path:
+    return Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 
 def _hipcc() -> str:
@@ -77,11 +83,34 @@ def build(verbose: bool = False) -> Path:
         list(pool.map(_run, commands))
     tmp = LIBRARY.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-          *map(str, objects)])
+          f"-Wl,-soname,{LIBRARY.name}", *map(str, objects)])
     os.replace(tmp, LIBRARY)
+    build_torch_ops()
     if verbose:
-        print(f"built {LIBRARY}", file=sys.stderr)
+        print(f"built {LIBRARY} and {TORCH_LIBRARY}", file=sys.stderr)
     return LIBRARY
+
+
+def build_torch_ops() -> Path:
+    """liblightdelta_torch.so: csrc/torch_ops.cpp compiled by the host compiler against
+    torch's headers and libraries (c10, c10_hip, torch_cpu) and linked to
+    liblightdelta_hip.so, found next to it at load time."""
+    import torch
+
+    torch_dir = Path(torch.__file__).resolve().parent
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler (g++) for the torch.ops kernels")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = TORCH_LIBRARY.with_suffix(".so.tmp")
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+          "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", f"-I{torch_dir / 'include'}",
+          f"-I{torch_dir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+          f"-I{_rocm() / 'include'}", f"-I{ROOT / 'include'}", str(CSRC / "torch_ops.cpp"),
+          "-o", str(tmp), f"-L{torch_dir / 'lib'}", "-lc10", "-lc10_hip", "-ltorch_cpu",
+          f"-L{PACKAGE}", "-llightdelta_hip", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, TORCH_LIBRARY)
+    return TORCH_LIBRARY
 
 
 if __name__ == "__main__":

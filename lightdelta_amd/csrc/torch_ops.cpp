@@ -1,0 +1,201 @@
+// Dispatcher kernels of torch.ops.lightdelta.decode and decode_conv (CUDA key, under which
+// HIP tensors dispatch on PyTorch-ROCm): the argument checks of the reference's launcher
+// (csrc/gdn_decode.cu:366-403), generalised to any H, HV with HV % H == 0, with its
+// messages, then the C ABI of liblightdelta_hip.so on the current HIP stream of the
+// tensors' device.  The schemas are defined by lightdelta_amd/ops.py, which loads this
+// library; the other ops keep their Python kernels.  Host-only C++ (no device code): one
+// eager call costs a few microseconds of host time, as the reference's C++ launcher does,
+// where a Python kernel costs about twelve.
+#include <ATen/core/Tensor.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <atomic>
+#include <optional>
+
+#include "lightdelta_hip.h"
+
+namespace {
+
+constexpr int64_t kDim = LD_HEAD_DIM;
+
+std::atomic<int> g_cache_policy{LD_CACHE_STREAM};
+
+bool floats(const at::Tensor& t) {
+  return t.scalar_type() == at::kFloat || t.scalar_type() == at::kBFloat16;
+}
+
+int32_t dtype_code(const at::Tensor& t) {
+  return t.scalar_type() == at::kBFloat16 ? LD_DTYPE_BF16 : LD_DTYPE_F32;
+}
+
+// The decode step's checks (ops.py _decode_layout has the same ones for the Python-side
+// callers); returns H, HV.
+std::pair<int64_t, int64_t> check_decode(const at::Tensor& qkv, const at::Tensor& a,
+                                         const at::Tensor& b, const at::Tensor& a_log,
+                                         const at::Tensor& dt_bias, const at::Tensor& indices,
+                                         const at::Tensor& cu, const at::Tensor& accepted,
+                                         const at::Tensor& state, const at::Tensor& gate,
+                                         const at::Tensor& weight, const at::Tensor& out,
+                                         double eps) {
+  TORCH_CHECK(qkv.is_cuda() && qkv.scalar_type() == at::kBFloat16, "qkv must be CUDA BF16");
+  const c10::Device device = qkv.device();
+  for (const at::Tensor* t : {&a, &b, &gate, &out})
+    TORCH_CHECK(t->device() == device && t->scalar_type() == at::kBFloat16 && t->dim() > 0 &&
+                    t->stride(-1) == 1,
+                "activations must be BF16 with dense rows");
+  for (const at::Tensor* t : {&a_log, &state})
+    TORCH_CHECK(t->device() == device && t->scalar_type() == at::kFloat && t->dim() > 0 &&
+                    t->stride(-1) == 1,
+                "state and A_log must be CUDA FP32 with dense rows");
+  for (const at::Tensor* t : {&indices, &cu, &accepted})
+    TORCH_CHECK(t->device() == device && t->scalar_type() == at::kInt && t->is_contiguous(),
+                "metadata must be contiguous CUDA int32");
+  for (const at::Tensor* t : {&dt_bias, &weight})
+    TORCH_CHECK(t->device() == device && t->is_contiguous() && floats(*t),
+                "weights must be contiguous FP32/BF16");
+  // H and HV from qkv's width (2H + HV) * 128 and the state's head count
+  const int64_t hv = state.dim() == 4 ? state.size(1) : 0;
+  const int64_t cols = qkv.dim() == 2 ? qkv.size(1) : 0;
+  const int64_t h2 = cols / kDim - hv;
+  const int64_t h = h2 / 2;
+  const bool geometry = hv > 0 && cols % kDim == 0 && h2 > 0 && h2 % 2 == 0 && hv % h == 0;
+  TORCH_CHECK(qkv.dim() == 2 && geometry && qkv.stride(1) == 1,
+              "qkv must be [tokens,(2*H+HV)*128] with HV a multiple of H");
+  TORCH_CHECK(state.dim() == 4 && state.size(2) == kDim && state.size(3) == kDim &&
+                  state.stride(2) == kDim && state.stride(1) == kDim * kDim,
+              "state must be [slots,HV,128,128]");
+  TORCH_CHECK(indices.dim() == 2 && indices.size(1) >= 1 && indices.size(1) <= LD_MAX_TOKENS,
+              "decode/MTP supports 1 through 4 tokens per request");
+  const int64_t n = qkv.size(0);
+  TORCH_CHECK(a.dim() == 2 && a.size(0) == n && a.size(1) == hv && b.dim() == 2 &&
+                  b.size(0) == n && b.size(1) == hv && gate.dim() == 3 && gate.size(0) == n &&
+                  gate.size(1) == hv && gate.size(2) == kDim && out.dim() == 3 &&
+                  out.size(0) == n && out.size(1) == hv && out.size(2) == kDim &&
+                  out.is_contiguous() && gate.stride(1) == kDim,
+              "invalid activation shape or output layout");
+  TORCH_CHECK(a_log.numel() == hv && dt_bias.numel() == hv && weight.numel() == kDim,
+              "invalid weight shapes");
+  const int64_t requests = indices.size(0);
+  TORCH_CHECK(cu.dim() == 1 && cu.numel() == requests + 1 && accepted.dim() == 1 &&
+                  accepted.numel() == requests,
+              "invalid request metadata shapes");
+  TORCH_CHECK(eps > 0, "norm epsilon must be positive");
+  return {h, hv};
+}
+
+ld_gdn_decode_args decode_args(const at::Tensor& qkv, const at::Tensor& a,
+                               const at::Tensor& b, const at::Tensor& a_log,
+                               const at::Tensor& dt_bias, const at::Tensor& indices,
+                               const at::Tensor& cu, const at::Tensor& accepted,
+                               const at::Tensor& state, const at::Tensor& gate,
+                               const at::Tensor& weight, const at::Tensor& out, double eps,
+                               std::pair<int64_t, int64_t> heads) {
+  ld_gdn_decode_args args{};
+  args.qkv = qkv.data_ptr();
+  args.qkv_row_stride = qkv.stride(0);
+  args.a = a.data_ptr();
+  args.a_row_stride = a.stride(0);
+  args.b = b.data_ptr();
+  args.b_row_stride = b.stride(0);
+  args.a_log = static_cast<const float*>(a_log.data_ptr());
+  args.dt_bias = dt_bias.data_ptr();
+  args.dt_bias_dtype = dtype_code(dt_bias);
+  args.norm_weight_dtype = dtype_code(weight);
+  args.indices = static_cast<const int32_t*>(indices.data_ptr());
+  args.cu = static_cast<const int32_t*>(cu.data_ptr());
+  args.accepted = static_cast<const int32_t*>(accepted.data_ptr());
+  args.state = static_cast<float*>(state.data_ptr());
+  args.state_slot_stride = state.stride(0);
+  args.gate = gate.data_ptr();
+  args.gate_row_stride = gate.stride(0);
+  args.norm_weight = weight.data_ptr();
+  args.out = out.data_ptr();
+  args.num_requests = static_cast<int32_t>(indices.size(0));
+  args.width = static_cast<int32_t>(indices.size(1));
+  args.num_k_heads = static_cast<int32_t>(heads.first);
+  args.num_v_heads = static_cast<int32_t>(heads.second);
+  args.scale = static_cast<float>(0.08838834764831845);  // 128^-0.5 (reference csrc/gdn_decode.cu:417)
+  args.eps = static_cast<float>(eps);
+  args.cache_policy = g_cache_policy.load(std::memory_order_relaxed);
+  return args;
+}
+
+void decode(const at::Tensor& qkv, const at::Tensor& a, const at::Tensor& b,
+            const at::Tensor& a_log, const at::Tensor& dt_bias, const at::Tensor& indices,
+            const at::Tensor& cu, const at::Tensor& accepted, at::Tensor state,
+            const at::Tensor& gate, const at::Tensor& weight, at::Tensor out, double eps) {
+  const auto heads = check_decode(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate,
+                                  weight, out, eps);
+  if (indices.size(0) == 0) return;
+  const ld_gdn_decode_args args = decode_args(qkv, a, b, a_log, dt_bias, indices, cu, accepted,
+                                              state, gate, weight, out, eps, heads);
+  const c10::DeviceGuard guard(qkv.device());
+  const int rc = ld_gdn_decode(&args, c10::hip::getCurrentHIPStream(qkv.get_device()).stream());
+  TORCH_CHECK(rc == LD_OK, ld_last_error());
+}
+
+void decode_conv(const at::Tensor& mixed_qkv, at::Tensor conv_state, const at::Tensor& conv_weight,
+                 const std::optional<at::Tensor>& conv_bias, const at::Tensor& a,
+                 const at::Tensor& b, const at::Tensor& a_log, const at::Tensor& dt_bias,
+                 const at::Tensor& indices, const at::Tensor& cu, const at::Tensor& accepted,
+                 at::Tensor state, const at::Tensor& gate, const at::Tensor& weight,
+                 at::Tensor out, double eps) {
+  const auto heads = check_decode(mixed_qkv, a, b, a_log, dt_bias, indices, cu, accepted, state,
+                                  gate, weight, out, eps);
+  const int64_t conv_dim = mixed_qkv.size(1);
+  TORCH_CHECK(conv_state.device() == mixed_qkv.device() &&
+                  conv_state.scalar_type() == at::kBFloat16 && conv_state.dim() == 3 &&
+                  conv_state.size(1) == conv_dim && conv_state.size(2) >= 3 &&
+                  conv_state.size(2) <= 8,
+              "conv_state must be CUDA BF16 [slots, conv_dim, 3..8]");
+  TORCH_CHECK(conv_weight.device() == mixed_qkv.device() &&
+                  conv_weight.scalar_type() == at::kBFloat16 && conv_weight.dim() == 2 &&
+                  conv_weight.size(0) == conv_dim && conv_weight.size(1) == 4 &&
+                  conv_weight.is_contiguous() &&
+                  reinterpret_cast<uintptr_t>(conv_weight.data_ptr()) % 8 == 0,
+              "conv_weight must be contiguous CUDA BF16 [conv_dim, 4]");
+  const at::Tensor* bias = conv_bias.has_value() ? &*conv_bias : nullptr;
+  if (bias != nullptr)
+    TORCH_CHECK(bias->device() == mixed_qkv.device() && bias->scalar_type() == at::kBFloat16 &&
+                    bias->numel() == conv_dim && bias->is_contiguous(),
+                "conv_bias must be contiguous CUDA BF16 [conv_dim]");
+  ld_gdn_decode_args args = decode_args(mixed_qkv, a, b, a_log, dt_bias, indices, cu, accepted,
+                                        state, gate, weight, out, eps, heads);
+  args.qkv = nullptr;  // the post-conv activations are the kernel's own
+  args.qkv_row_stride = 0;
+  ld_conv_args conv{};
+  conv.x = mixed_qkv.data_ptr();
+  conv.x_row_stride = mixed_qkv.stride(0);
+  conv.state = conv_state.data_ptr();
+  conv.state_slots = conv_state.size(0);
+  conv.state_slot_stride = conv_state.stride(0);
+  conv.state_dim_stride = conv_state.stride(1);
+  conv.state_len_stride = conv_state.stride(2);
+  conv.state_len = static_cast<int32_t>(conv_state.size(2));
+  conv.width = 4;
+  conv.weight = conv_weight.data_ptr();
+  conv.weight_dtype = LD_DTYPE_BF16;
+  conv.bias_dtype = LD_DTYPE_BF16;
+  conv.bias = bias != nullptr ? bias->data_ptr() : nullptr;
+  const c10::DeviceGuard guard(mixed_qkv.device());
+  const int rc = ld_gdn_decode_conv(
+      &args, &conv, c10::hip::getCurrentHIPStream(mixed_qkv.get_device()).stream());
+  TORCH_CHECK(rc == LD_OK, ld_last_error());
+}
+
+}  // namespace
+
+TORCH_LIBRARY_IMPL(lightdelta, CUDA, m) {
+  m.impl("decode", &decode);
+  m.impl("decode_conv", &decode_conv);
+}
+
+// The state cache policy these kernels pass (LD_CACHE_KEEP / LD_CACHE_STREAM), set from
+// lightdelta_amd.ops.set_state_cache_policy.
+extern "C" int ld_torch_set_cache_policy(int policy) {
+  if (policy != LD_CACHE_KEEP && policy != LD_CACHE_STREAM) return LD_ERR_INVALID_ARGUMENT;
+  g_cache_policy.store(policy, std::memory_order_relaxed);
+  return LD_OK;
+}

@@ -34,7 +34,9 @@ memory on the host, so it can be captured in a HIP graph.
 
 from __future__ import annotations
 
+import ctypes
 import os
+from pathlib import Path
 
 import torch
 
@@ -93,6 +95,8 @@ def set_state_cache_policy(policy: str) -> None:
     if policy not in _POLICIES:
         raise ValueError(f"state cache policy must be one of {sorted(_POLICIES)}")
     _cache_policy = _POLICIES[policy]
+    if _TORCH_KERNELS is not None:
+        _TORCH_KERNELS.ld_torch_set_cache_policy(_cache_policy)
 
 
 def state_cache_policy() -> str:
@@ -302,28 +306,6 @@ def _dtype_code(t: torch.Tensor) -> int:
     return _lib.DTYPE_BF16 if t.dtype == torch.bfloat16 else _lib.DTYPE_F32
 
 
-def _decode_impl(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate, weight, out, eps):
-    (h, hv, dev, requests, width, qkv_row, a_row, b_row, slot_stride,
-     gate_row) = _decode_layout(qkv, a, b, a_log, dt_bias, indices, cu, accepted, state, gate,
-                                weight, out, eps)
-    if requests == 0:
-        return
-    args = _lib.DECODE_ARGS.pack(
-        qkv.data_ptr(), qkv_row, a.data_ptr(), a_row, b.data_ptr(), b_row, a_log.data_ptr(),
-        dt_bias.data_ptr(), _lib.DTYPE_BF16 if dt_bias.dtype is _BF16 else _lib.DTYPE_F32,
-        _lib.DTYPE_BF16 if weight.dtype is _BF16 else _lib.DTYPE_F32, indices.data_ptr(),
-        cu.data_ptr(), accepted.data_ptr(), state.data_ptr(), slot_stride, gate.data_ptr(),
-        gate_row, weight.data_ptr(), out.data_ptr(), requests, width, h, hv, QK_SCALE, eps,
-        _cache_policy)
-    launch = _lib.packed("ld_gdn_decode")
-    current = _current_device()
-    if current == dev:
-        _lib.check(launch(args, _stream(dev)))
-        return
-    with _DeviceGuard(dev):
-        _lib.check(launch(args, _stream(dev)))
-
-
 def check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log, dt_bias,
                       indices, cu, accepted, state, gate, weight, out, eps):
     """Validation of decode_conv: decode's checks on the pre-conv activations, plus the conv
@@ -356,29 +338,6 @@ def check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log
             "conv_bias must be contiguous CUDA BF16 [conv_dim]",
         )
     return h, hv
-
-
-def _decode_conv_impl(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log, dt_bias,
-                      indices, cu, accepted, state, gate, weight, out, eps):
-    h, hv = check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log,
-                              dt_bias, indices, cu, accepted, state, gate, weight, out, eps)
-    requests, width = indices.shape
-    args = _lib.DecodeArgs(
-        0, 0, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), a_log.data_ptr(),
-        dt_bias.data_ptr(), _dtype_code(dt_bias), _dtype_code(weight), indices.data_ptr(),
-        cu.data_ptr(), accepted.data_ptr(), state.data_ptr(), state.stride(0),
-        gate.data_ptr(), gate.stride(0), weight.data_ptr(), out.data_ptr(), requests, width, h,
-        hv, QK_SCALE, eps, _cache_policy,
-    )
-    conv = _lib.ConvArgs(
-        mixed_qkv.data_ptr(), mixed_qkv.stride(0), conv_state.data_ptr(), conv_state.shape[0],
-        conv_state.stride(0), conv_state.stride(1), conv_state.stride(2), conv_state.shape[2], 4,
-        conv_weight.data_ptr(), _lib.DTYPE_BF16, _lib.DTYPE_BF16,
-        None if conv_bias is None else conv_bias.data_ptr(),
-    )
-    lib = _lib.load()
-    with _DeviceGuard(mixed_qkv.device):
-        _lib.check(lib.ld_gdn_decode_conv(args, conv, _stream(mixed_qkv.device)))
 
 
 # ---------------------------------------------------------------------------------------
@@ -577,14 +536,15 @@ def _zero_slots_impl(pool, slots):
 # registration
 # ---------------------------------------------------------------------------------------
 
+# decode and decode_conv have C++ kernels (csrc/torch_ops.cpp, liblightdelta_torch.so): their
+# host path is on every decode step.  The other ops' kernels are these Python functions.
+_CXX_KERNELS = ("decode", "decode_conv")
 _IMPLS = {
-    "decode": _decode_impl,
     "gather_state": _gather_state_impl,
     "scatter_state": _scatter_state_impl,
     "copy_state": _copy_state_impl,
     "zero_slots": _zero_slots_impl,
     "prefill": _prefill_impl,
-    "decode_conv": _decode_conv_impl,
     "gather_slots": _gather_slots_impl,
     "scatter_slots": _scatter_slots_impl,
 }
@@ -594,13 +554,36 @@ def _fake(*args, **kwargs):
     return None
 
 
-def _register() -> torch.library.Library:
+TORCH_KERNELS_PATH = Path(__file__).resolve().with_name("liblightdelta_torch.so")
+
+
+def _not_built(*args, **kwargs):
+    raise RuntimeError(f"{TORCH_KERNELS_PATH.name} is not built; run `python -m "
+                       "lightdelta_amd.build` (hipcc, gfx950, and g++ against torch) before "
+                       "using the lightdelta ops")
+
+
+def _register():
+    """Defines the ops, registers their fakes and their CUDA-key kernels: the C++ ones by
+    loading liblightdelta_torch.so (with its liblightdelta_hip.so), the others from _IMPLS.
+    Without the C++ library, decode and decode_conv raise."""
     library = torch.library.Library("lightdelta", "DEF")
     for name, schema in SCHEMAS.items():
         library.define(schema)
-        library.impl(name, _IMPLS[name], "CUDA")
         torch.library.register_fake(f"lightdelta::{name}", _fake, lib=library)
-    return library
+        if name in _IMPLS:
+            library.impl(name, _IMPLS[name], "CUDA")
+    kernels = None
+    if TORCH_KERNELS_PATH.exists():
+        torch.ops.load_library(str(TORCH_KERNELS_PATH))
+        kernels = ctypes.CDLL(str(TORCH_KERNELS_PATH))
+        kernels.ld_torch_set_cache_policy.argtypes = [ctypes.c_int]
+        kernels.ld_torch_set_cache_policy.restype = ctypes.c_int
+        kernels.ld_torch_set_cache_policy(_cache_policy)
+    else:
+        for name in _CXX_KERNELS:
+            library.impl(name, _not_built, "CUDA")
+    return library, kernels
 
 
-_LIBRARY = _register()
+_LIBRARY, _TORCH_KERNELS = _register()

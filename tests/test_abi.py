@@ -175,14 +175,3 @@ def test_static_prefill_rejects_without_launching():
     assert need > _lib.PREFILL_STATIC_SCRATCH_BYTES
     assert lib.ld_gdn_prefill_static(args, None) == 1
     assert b"static scratch" in lib.ld_last_error()
-
-
-def test_packed_decode_args_match_the_struct():
-    """The decode op's per-call argument bytes (DECODE_ARGS) are byte for byte the
-    ld_gdn_decode_args that the ctypes mirror lays out."""
-    import ctypes
-
-    values = (1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21,
-              0.5, 1e-6, 1)
-    assert _lib.DECODE_ARGS.size == ctypes.sizeof(_lib.DecodeArgs)
-    assert _lib.DECODE_ARGS.pack(*values) == bytes(_lib.DecodeArgs(*values))

@@ -42,7 +42,9 @@ def test_valid_geometries(meta):
     assert check(decode_args(meta, h=4, hv=8, width=4)) == (4, 8)
 
 
-@pytest.mark.parametrize("mutate,message", [
+# Invalid decode arguments and the message each must raise: mutate(args, device) edits the
+# valid arguments of decode_args(device).
+DECODE_CASES = [
     (lambda d, m: d.update(qkv=d["qkv"].float()), "qkv must be CUDA BF16"),
     (lambda d, m: d.update(qkv=torch.empty(4, 8192, dtype=torch.bfloat16)), "qkv must be CUDA BF16"),
     (lambda d, m: d.update(a=d["a"].float()), "activations must be BF16"),
@@ -73,7 +75,10 @@ def test_valid_geometries(meta):
     (lambda d, m: d.update(cu=torch.empty(4, dtype=torch.int32, device=m)),
      "invalid request metadata shapes"),
     (lambda d, m: d.update(eps=0.0), "norm epsilon must be positive"),
-])
+]
+
+
+@pytest.mark.parametrize("mutate,message", DECODE_CASES)
 def test_decode_validation_messages(meta, mutate, message):
     args = decode_args(meta)
     mutate(args, meta)
@@ -109,6 +114,18 @@ def test_state_io_validation_messages(meta):
         ops.check_zero(pool, slots.long())
     with pytest.raises(RuntimeError, match="dense inner dimensions"):
         ops.check_zero(torch.empty(8, 4, 128, 256, device=meta)[..., :128], slots)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mutate,message", DECODE_CASES + [
+    (lambda d, m: d.update(qkv=d["qkv"].cpu()), "qkv must be CUDA BF16")])
+def test_decode_kernel_validation_messages(gpu, mutate, message):
+    """The same cases through torch.ops.lightdelta.decode on the GPU: the C++ kernel
+    (csrc/torch_ops.cpp) raises the same messages, before any launch."""
+    args = decode_args(gpu)
+    mutate(args, gpu)
+    with pytest.raises(RuntimeError, match=message):
+        torch.ops.lightdelta.decode(*args.values())
 
 
 def test_cpu_tensors_are_rejected():
