@@ -137,9 +137,12 @@ typedef struct ld_conv_args {
  * is the plain one-column shift); then the GDN step of ld_gdn_decode runs.  Requests that
  * are invalid for the GDN step, or whose conv columns would fall outside the state
  * (accepted - 1 + 2 > state_len - 1, or accepted > n < state_len), or whose conv slot
- * indices[r, 0] is padding, get zero outputs and leave both pools untouched.  Launches that
- * touch the same slots must be stream-ordered (they share one ticket per (slot, k-head) in
- * library-owned device memory; at most 2^20).
+ * indices[r, 0] is padding, get zero outputs and leave both pools untouched.  Conv slots
+ * must be distinct within one launch, and launches that touch the same slots must be
+ * stream-ordered: the v-heads of a k-head group decide which of them writes the shared q/k
+ * conv state with one ticket per (slot, k-head) in library-owned device memory (slots x
+ * k-heads at most 2^20).  Either violation makes that launch's conv states undefined; the
+ * tickets themselves return to their state, so later launches are unaffected.
  * No counterpart in the reference, whose conv is vLLM's causal_conv1d_update run before
  * lightdelta::decode (python/lightdelta/integration/vllm_layer.py:150-172, 199-220).
  */
@@ -267,7 +270,11 @@ int ld_state_scatter(const void* packed, int64_t packed_row_stride_bytes,
 /*
  * Slot-to-slot copy inside one pool for `pairs` (src, dst) pairs:
  *   if src_slots[p] > 0 && dst_slots[p] > 0: pool[dst_slots[p]] = pool[src_slots[p]]
- * Pairs must not write the same destination twice or read a slot another pair writes.
+ * A pair whose slots overlap another live pair's -- its source is another pair's
+ * destination (a chain a->b, b->c), or its destination is another pair's source or
+ * destination -- is rejected and writes nothing; every other pair is copied from the pool
+ * as it was before the call.  Each workgroup scans the pair list for its own pair, so the
+ * cost grows with pairs^2 / 256 (a few percent at 1024 pairs of 2 MiB).
  * No counterpart in the reference (which commits MTP states implicitly through the
  * next step's `accepted`, csrc/gdn_decode.cu:154-158); it is the explicit commit /
  * slot-lifecycle copy, with the reference's padding convention (slot <= 0).

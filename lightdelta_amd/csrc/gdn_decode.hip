@@ -58,6 +58,19 @@ __device__ __forceinline__ TokenIn conv_token(const uint16_t* conv, int kq) {
   return in;
 }
 
+// Counts a workgroup in on a conv ticket of a k-head group of `group` workgroups: a wrapping
+// increment (global_atomic_inc: the ticket becomes 0 when it held group - 1, else its value
+// + 1) that returns the previous count, so the workgroup that counts in last receives
+// group - 1 and leaves the ticket at 0 for the next launch, with no store of its own.  Any
+// sequence of arrivals whose number is a multiple of `group` (every launch: each valid
+// request counts its group in once per k-head, a repeated conv slot in one batch twice)
+// returns the ticket to where it was.  Relaxed, agent scope: the count orders nothing; the
+// conv-state reads it follows were consumed before it is issued.
+__device__ __forceinline__ uint32_t count_in(uint32_t* ticket, int group) {
+  return __builtin_amdgcn_atomic_inc32(ticket, static_cast<uint32_t>(group - 1), __ATOMIC_RELAXED,
+                                       "agent");
+}
+
 template <typename T>
 __device__ __forceinline__ void pin_sgpr(const T& x) {
   asm volatile("" ::"s"(x));
@@ -188,11 +201,11 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 // streams in, several (speculative verify, W > 1) before the tile loads.  Its own v
 // channels' conv state is updated in place.  The q/k channels are shared by the
 // HV/H workgroups of a k-head group, so their shifted state is written only after all of
-// them have read it: every workgroup counts itself in (relaxed atomic add on
-// g_conv_ticket[slot*H + kh], returning the previous count) after its reads; the one that
-// receives HV/H - 1 counted in last, writes the shifted state at its end and resets the
-// count to 0.  Nothing waits on another workgroup, and every launch leaves the counts at
-// zero.  ConvCols: conv-state columns held per channel (4 for states of 3..4 columns, 8 for
+// them have read it: every workgroup counts itself in (count_in, a wrapping increment of
+// g_conv_ticket[slot*H + kh] that returns the previous count) after its reads; the one that
+// receives HV/H - 1 counted in last and writes the shifted state at its end; its increment
+// returned the ticket to 0.  Nothing waits on another workgroup, and every launch leaves the
+// tickets as it found them.  ConvCols: conv-state columns held per channel (4 for states of 3..4 columns, 8 for
 // up to 8; 0 = no conv).
 //
 // Waves: 4 (32 V rows and 16 tile pieces per wave), or 16 (8 rows, 4 pieces) for the
@@ -364,9 +377,8 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     for (int k = 0; k < kCols; ++k)
       p.conv_state[cs_v_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new[k];
     if (p.group > 1 && tid == 0)
-      arrived = __hip_atomic_fetch_add(
-          &g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head], 1u,
-          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      arrived = count_in(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
+                         p.group);
     in0.a = p.a[static_cast<int64_t>(bos) * p.a_row + head];
     in0.b = p.b[static_cast<int64_t>(bos) * p.b_row + head];
   } else if constexpr (kConvLate) {
@@ -470,9 +482,8 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     // The returned count is first used at the kernel's end, by which time it has long
     // arrived: no wait on the tile stream here, and no extra round trip there.
     if (p.group > 1 && tid == 0)
-      arrived = __hip_atomic_fetch_add(
-          &g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head], 1u,
-          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      arrived = count_in(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
+                         p.group);
   }
   if constexpr (Conv) {  // token 0 after the conv, from LDS
     const TokenIn c = conv_token(s_conv[0], kq);
@@ -588,7 +599,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
 
   // ---- conv variant: the only workgroup of its k-head (HV == H), or the one that counted
   // in last (all HV/H of the k-head group had read the q/k conv state before it), writes the
-  // shifted q/k conv state and returns the count to zero for the next launch ----
+  // shifted q/k conv state (its count_in already returned the count to zero) ----
   if constexpr (Conv) {
     if (p.group == 1 || s_arrived == static_cast<uint32_t>(p.group - 1)) {
       const int64_t slot_at = static_cast<int64_t>(slot[0]) * p.conv_slot;
@@ -597,9 +608,6 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
         const int64_t at = slot_at + ch * p.conv_dim_stride;
         for (int j = 0; j < p.conv_len; ++j) p.conv_state[at + j * p.conv_len_stride] = s_conv_new[c][j];
       }
-      if (p.group > 1 && tid == 0)
-        __hip_atomic_store(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
-                           0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }

@@ -28,6 +28,7 @@ struct CopyParams {
   int64_t slot_stride;    // elements between consecutive slots entries (gather/scatter)
   const int32_t* dst_slots;  // copy only
   const uint8_t* valid;   // gather only; NULL = all valid
+  int64_t rows;           // rows (copy: pairs)
   int64_t vecs;           // 16-byte vectors per row
   uint32_t chunks;        // chunks per row
 };
@@ -50,6 +51,23 @@ __device__ __forceinline__ void store_row(u32x4 v, u32x4* dst) {
     *dst = v;
   else
     __builtin_nontemporal_store(v, dst);
+}
+
+// Copy: whether live pair `row` (source `from`, destination `to`, both > 0) conflicts with
+// another live pair -- its source is another pair's destination, or its destination is
+// another pair's source or destination.  Such pairs are rejected (nothing is written for
+// them); the remaining pairs read slots no pair writes and write slots no other pair
+// touches, so their copies are independent of the order of all reads and writes.  Every
+// thread scans a share of the pairs; the verdict is the workgroup's OR (uniform).
+__device__ __forceinline__ bool copy_conflicts(const CopyParams& p, uint32_t row, int from,
+                                               int to) {
+  bool conflict = false;
+  for (int64_t q = threadIdx.x; q < p.rows; q += kThreads) {
+    const int s = p.slots[q];
+    const int d = p.dst_slots[q];
+    conflict |= q != row && s > 0 && d > 0 && (d == from || s == to || d == to);
+  }
+  return __syncthreads_or(conflict);
 }
 
 // One workgroup moves one 16 KiB chunk of one row: 4 128-bit loads per thread in flight,
@@ -102,6 +120,9 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i)
       v[i] = load_row<M>(src + first + i * kThreads);
+    // copy: the pair-conflict scan's loads go out right behind the chunk's (L2 hits), so the
+    // scan adds little to the time the stores wait for the chunk anyway
+    if (M == kCopy && copy_conflicts(p, row, p.slots[row], p.dst_slots[row])) return;
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i)
       store_row<M>(v[i], dst + first + i * kThreads);
@@ -113,6 +134,7 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
     const int64_t idx = first + i * kThreads;
     v[i] = load_row<M>(src + (idx < p.vecs ? idx : 0));
   }
+  if (M == kCopy && copy_conflicts(p, row, p.slots[row], p.dst_slots[row])) return;
 #pragma unroll
   for (int i = 0; i < kVecsPerThread; ++i) {
     const int64_t idx = first + i * kThreads;
@@ -128,6 +150,7 @@ int launch(const char* what, int mode, CopyParams p, int64_t rows, int64_t row_b
       (mode != kZero && !aligned16(p.src)) || !aligned16(p.dst))
     return fail(LD_ERR_INVALID_ARGUMENT,
                 "state rows, strides and base pointers must be 16-byte aligned");
+  p.rows = rows;
   p.vecs = row_bytes / 16;
   const int64_t chunks = (p.vecs + kVecsPerChunk - 1) / kVecsPerChunk;
   p.chunks = static_cast<uint32_t>(chunks);

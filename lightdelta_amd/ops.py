@@ -9,7 +9,10 @@ Argument validation raises RuntimeError with the reference's messages
 
 Additive ops (no reference counterpart):
   copy_state(pool, src, dst)            slot -> slot copy inside one pool (MTP commit,
-                                        slot reuse), any dtype, padding slot <= 0 skipped
+                                        slot reuse), any dtype, padding slot <= 0 skipped;
+                                        a pair that overlaps another (its source another's
+                                        destination, its destination another's source or
+                                        destination) is rejected and writes nothing
   zero_slots(pool, slots)               zero whole slots in place (a slot reused by a new
                                         sequence), any dtype, padding slot <= 0 skipped
   decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, <decode args without qkv>)

@@ -105,9 +105,9 @@ def test_state_io_oracle_against_brute_force():
             assert np.array_equal(result[d], packed[r])
     untouched = [s for s in range(7) if s not in (1, 2, 5)]
     assert np.array_equal(result[untouched], pool[untouched])
-    src, dst = np.array([1, 2, -1, 4]), np.array([2, 3, 5, 0])
+    src, dst = np.array([1, 5, -1, 4]), np.array([2, 3, 5, 0])
     copied = state_io.copy(pool, src, dst)
-    assert np.array_equal(copied[2], pool[1]) and np.array_equal(copied[3], pool[2])
+    assert np.array_equal(copied[2], pool[1]) and np.array_equal(copied[3], pool[5])
     assert np.array_equal(copied[[0, 1, 4, 5, 6]], pool[[0, 1, 4, 5, 6]])
     zeroed = state_io.zero(pool, np.array([6, -1, 0, 2]))
     assert not zeroed[[2, 6]].any()
@@ -116,3 +116,70 @@ def test_state_io_oracle_against_brute_force():
     via_gather = state_io.scatter(state_io.gather(pool, np.array([6, 2]), np.array([0, 0], bool)),
                                   np.array([6, 2]), pool)
     assert np.array_equal(via_gather, zeroed)
+
+
+def test_copy_rejects_overlapping_pairs():
+    """A chain (1->2, 2->3), a cycle (4->5->6->4) and two writes of one slot (1->0 padding
+    aside, 3->7 and 2->7) overlap: every pair involved is rejected and writes nothing; the
+    independent pair 8->9 and a self pair 10->10 are applied; a pair with a padding slot
+    takes no part in any overlap."""
+    rng = np.random.default_rng(3)
+    pool = rng.standard_normal((12, 2, 3)).astype(np.float32)
+    src = np.array([1, 2, 4, 5, 6, 8, 10, 11, -1])
+    dst = np.array([2, 3, 5, 6, 4, 9, 10, -1, 8])
+    assert list(state_io.copy_rejected(src, dst)) == [True, True, True, True, True, False,
+                                                      False, False, False]
+    copied = state_io.copy(pool, src, dst)
+    assert np.array_equal(copied[9], pool[8])
+    assert np.array_equal(copied[[s for s in range(12) if s != 9]],
+                          pool[[s for s in range(12) if s != 9]])
+    twice = state_io.copy(pool, np.array([3, 2, 8]), np.array([7, 7, 9]))
+    assert np.array_equal(twice[7], pool[7]) and np.array_equal(twice[9], pool[8])
+
+
+def test_copy_kept_pairs_are_order_independent():
+    """On random pair sets (many overlaps), the pairs the rule keeps can be applied one after
+    another in any order with the same result, which equals the oracle's; and every
+    rejected pair shares a slot with another live pair in a way that makes the order matter
+    (its source written, or its destination read or written, by another pair)."""
+    rng = np.random.default_rng(4)
+    for trial in range(200):
+        slots, pairs = 12, int(rng.integers(1, 9))
+        pool = rng.standard_normal((slots, 4)).astype(np.float32)
+        src = rng.integers(-1, slots, pairs)
+        dst = rng.integers(-1, slots, pairs)
+        rejected = state_io.copy_rejected(src, dst)
+        expected = state_io.copy(pool, src, dst)
+        kept = [p for p in range(pairs) if src[p] > 0 and dst[p] > 0 and not rejected[p]]
+        for _ in range(3):
+            result = pool.copy()
+            for p in rng.permutation(kept):
+                result[dst[p]] = result[src[p]]
+            assert np.array_equal(result, expected), trial
+        live = [p for p in range(pairs) if src[p] > 0 and dst[p] > 0]
+        for p in live:
+            others = [q for q in live if q != p]
+            touches = any(dst[q] == src[p] or src[q] == dst[p] or dst[q] == dst[p] for q in others)
+            assert touches == bool(rejected[p]), trial
+
+
+def test_copy_rule_catches_a_dropped_condition(monkeypatch):
+    """Planted mistake: an oracle that does not reject two writes of one slot keeps a pair the
+    order-independence property then fails on."""
+    def lenient(src, dst):
+        live = [(s, d) if s > 0 and d > 0 else None for s, d in zip(src, dst)]
+        return np.array([pair is not None and any(
+            q != p and o is not None and (o[1] == pair[0] or o[0] == pair[1])
+            for q, o in enumerate(live)) for p, pair in enumerate(live)])
+
+    monkeypatch.setattr(state_io, "copy_rejected", lenient)
+    pool = np.arange(10, dtype=np.float32)[:, None]
+    src, dst = np.array([3, 2]), np.array([7, 7])
+    results = set()
+    for order in ([0, 1], [1, 0]):
+        result = pool.copy()
+        for p in order:
+            if not state_io.copy_rejected(src, dst)[p]:
+                result[dst[p]] = result[src[p]]
+        results.add(float(result[7, 0]))
+    assert len(results) == 2  # the lenient rule leaves the outcome order-dependent

@@ -77,6 +77,24 @@ def test_gather_scatter_copy_match_numpy(gpu, dtype):
     assert np.array_equal(row_bytes(pool), oracle.zero(copied, reset.numpy()))
 
 
+def test_copy_state_overlapping_pairs(gpu):
+    """Pair sets with a chain, a cycle, two writes of one slot, a self pair, padding and
+    independent pairs, on a pool of 2 MiB slots (every chunk of a row must agree): bit-exact
+    against the oracle, which rejects every overlapping pair."""
+    announce(test="copy_state_overlapping_pairs")
+    gen = torch.Generator().manual_seed(5)
+    pool = torch.randn(24, 32, 128, 128, generator=gen).to(gpu)
+    host = row_bytes(pool)
+    src = torch.tensor([1, 2, 4, 5, 6, 8, 10, 11, -1, 13, 14, 16, 20], dtype=torch.int32)
+    dst = torch.tensor([2, 3, 5, 6, 4, 9, 10, -1, 8, 12, 12, 17, 21], dtype=torch.int32)
+    torch.ops.lightdelta.copy_state(pool, src.to(gpu), dst.to(gpu))
+    torch.cuda.synchronize()
+    expected = oracle.copy(host, src.numpy(), dst.numpy())
+    assert np.array_equal(row_bytes(pool), expected)
+    assert not np.array_equal(expected[[9, 17, 21]], host[[9, 17, 21]])  # some pairs applied
+    assert np.array_equal(expected[[2, 3, 4, 5, 6, 12]], host[[2, 3, 4, 5, 6, 12]])
+
+
 def test_gather_into_strided_rows(gpu):
     """The packed backend gathers into scratch[1:].view(B, W, ...)[:, 0] (row stride W)."""
     announce(test="gather_strided_rows")
