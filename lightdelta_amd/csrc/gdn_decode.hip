@@ -269,24 +269,31 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   pin_sgpr(bos);
   pin_sgpr(eos);
   pin_sgpr(accepted);
-  pin_sgpr(p.qkv);
-  pin_sgpr(p.qkv_row);
-  pin_sgpr(p.a);
-  pin_sgpr(p.a_row);
-  pin_sgpr(p.b);
-  pin_sgpr(p.b_row);
-  pin_sgpr(p.a_log);
-  pin_sgpr(p.dt_bias);
-  pin_sgpr(p.state);
-  pin_sgpr(p.state_slot);
-  pin_sgpr(p.gate);
-  pin_sgpr(p.gate_row);
-  pin_sgpr(p.norm_weight);
-  pin_sgpr(p.out);
-  pin_sgpr(p.num_k_heads);
-  pin_sgpr(p.group);
-  pin_sgpr(p.scale);
-  pin_sgpr(p.eps);
+  // The step's arguments too -- except where the conv runs to completion before the tile
+  // loads (several tokens, or a long conv state): those have no loads to get ahead of, and
+  // holding every argument through the conv would exceed the 102 SGPRs.
+  if constexpr (!kConvFirst) {
+    if constexpr (!Conv) {  // the conv variant reads its activations from conv_x
+      pin_sgpr(p.qkv);
+      pin_sgpr(p.qkv_row);
+    }
+    pin_sgpr(p.a);
+    pin_sgpr(p.a_row);
+    pin_sgpr(p.b);
+    pin_sgpr(p.b_row);
+    pin_sgpr(p.a_log);
+    pin_sgpr(p.dt_bias);
+    pin_sgpr(p.state);
+    pin_sgpr(p.state_slot);
+    pin_sgpr(p.gate);
+    pin_sgpr(p.gate_row);
+    pin_sgpr(p.norm_weight);
+    pin_sgpr(p.out);
+    pin_sgpr(p.num_k_heads);
+    pin_sgpr(p.group);
+    pin_sgpr(p.scale);
+    pin_sgpr(p.eps);
+  }
   const int num_tokens = eos - bos;
   if (num_tokens <= 0) return;
   int source = 0;

@@ -277,6 +277,30 @@ def prefill_algorithm() -> str:
     return next(k for k, v in _PREFILL_ALGORITHMS.items() if v == _prefill_algorithm)
 
 
+# Chunked-prefill workspaces, one per (device, stream), kept and grown to the largest prefill
+# seen (ld_gdn_prefill_workspace_bytes: 115,712 bytes per 64-token chunk and v-head, e.g.
+# 2.0 GB for 32 x 1024 tokens at 32 v-heads).  Calls on one stream run in order, so they can
+# share one; the buffer comes from torch's allocator once (under a graph capture, from the
+# graph's pool) instead of on every call.  release_prefill_workspaces() drops them.
+_workspaces: dict = {}
+
+
+def _prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    key = (device.index, _stream(device))
+    buffer = _workspaces.get(key)
+    if buffer is None or buffer.numel() < nbytes:
+        _workspaces.pop(key, None)
+        buffer = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _workspaces[key] = buffer
+    return buffer
+
+
+def release_prefill_workspaces() -> None:
+    """Frees the cached chunked-prefill workspaces (the next chunked prefill allocates
+    again)."""
+    _workspaces.clear()
+
+
 def _prefill_impl(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state, gate,
                   weight, out, eps):
     h, hv = check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, state,
@@ -289,9 +313,9 @@ def _prefill_impl(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, sta
         algorithm == _lib.PREFILL_AUTO
         and lib.ld_gdn_prefill_auto_chunked(qkv.shape[0], slots.numel(), hv) == 1)
     workspace = None
-    if chunked:  # from the caching allocator (graph-capturable)
+    if chunked:
         nbytes = lib.ld_gdn_prefill_workspace_bytes(qkv.shape[0], slots.numel(), hv)
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=qkv.device)
+        workspace = _prefill_workspace(qkv.device, nbytes)
     args = _lib.PrefillArgs(
         qkv.data_ptr(), qkv.stride(0), a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
         a_log.data_ptr(), dt_bias.data_ptr(), _dtype_code(dt_bias), _dtype_code(weight),
