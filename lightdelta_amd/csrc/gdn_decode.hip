@@ -11,7 +11,7 @@
 //
 // Work decomposition (one workgroup = one (request, v-head) 128x128 fp32 state tile):
 //   * 256 threads = 4 wave64s (16 wave64s for the single-token step under the stream
-//     policy).  Inside a wave, the 16 lanes of a DPP row span one 512-byte K row: lane kq
+//     policy and for the verify steps without the conv).  Inside a wave, the 16 lanes of a DPP row span one 512-byte K row: lane kq
 //     holds k = 4kq..4kq+3 and 64+4kq..64+4kq+3 (two 16-byte pieces); the 4 DPP rows of the
 //     wave take 4 consecutive V rows.  Wave w's rows are 4w..4w+3 plus multiples of 4 * waves:
 //     a piece pair of all waves covers one contiguous block of the tile (16 rows = 8 KiB with
@@ -104,10 +104,6 @@ __device__ __forceinline__ uint16_t silu_bf16(float x) {
   return f32_to_bf16(y);
 }
 
-// One decode-token output of the causal depthwise conv (width 4) plus SiLU, rounded to bf16:
-//   bf16(silu(bias + sum_j w[j] * [state[len-3], state[len-2], state[len-1], x][j]))
-// with the fp32 accumulation running from the oldest tap to the newest (one rounding per
-// fused multiply-add) and the SiLU correctly rounded to bf16.
 // bf16(silu(bias + w0*t0 + w1*t1 + w2*t2 + w3*t3)): one causal conv output from its four
 // taps, oldest first, with the fp32 accumulation running from the oldest tap to the newest
 // (one rounding per fused multiply-add) and the SiLU correctly rounded to bf16.
@@ -205,13 +201,14 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 // g_conv_ticket[slot*H + kh] that returns the previous count) after its reads; the one that
 // receives HV/H - 1 counted in last and writes the shifted state at its end; its increment
 // returned the ticket to 0.  Nothing waits on another workgroup, and every launch leaves the
-// tickets as it found them.  ConvCols: conv-state columns held per channel (4 for states of 3..4 columns, 8 for
-// up to 8; 0 = no conv).
+// tickets as it found them.  ConvCols: conv-state columns held per channel (4 for states of
+// 3..4 columns, 8 for up to 8; 0 = no conv).
 //
 // Waves: 4 (32 V rows and 16 tile pieces per wave), or 16 (8 rows, 4 pieces) for the
-// non-conv steps under the stream policy.  A cold in-place read-modify-write of 64 KiB per
-// workgroup in this layout runs at 6.26 TB/s as 1024 threads x 4 pieces against 5.63 as
-// 256 x 16 (B=128 tiles at random slots, non-temporal loads, system-scope stores).
+// single-token step under the stream policy and for every verify step without the conv.  A
+// cold in-place read-modify-write of 64 KiB per workgroup in this layout runs at 6.26 TB/s
+// as 1024 threads x 4 pieces against 5.63 as 256 x 16 (B=128 tiles at random slots,
+// non-temporal loads, system-scope stores).
 template <bool DtBf16, bool WBf16, int LoadPol, int StorePol, int Width, int ConvCols,
           int Waves = kWaves>
 __global__ __launch_bounds__(64 * Waves)
