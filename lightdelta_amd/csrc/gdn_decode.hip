@@ -11,8 +11,8 @@
 //
 // Work decomposition (one workgroup = one (request, v-head) 128x128 fp32 state tile):
 //   * 256 threads = 4 wave64s (16 wave64s for the single-token step under the stream
-//     policy and for the verify steps without the conv).  Inside a wave, the 16 lanes of a DPP row span one 512-byte K row: lane kq
-//     holds k = 4kq..4kq+3 and 64+4kq..64+4kq+3 (two 16-byte pieces); the 4 DPP rows of the
+//     policy and for the verify steps without the conv).  Inside a wave, the 16 lanes of a
+//     DPP row span one 512-byte K row: lane kq holds k = 4kq..4kq+3 and 64+4kq..64+4kq+3 (two 16-byte pieces); the 4 DPP rows of the
 //     wave take 4 consecutive V rows.  Wave w's rows are 4w..4w+3 plus multiples of 4 * waves:
 //     a piece pair of all waves covers one contiguous block of the tile (16 rows = 8 KiB with
 //     4 waves, the whole 32 KiB half tile with 16).  A cold in-place read-modify-write of
@@ -617,43 +617,58 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
 }
 
 
-template <int LoadPol, int StorePol, int Width, int ConvCols, int Waves>
+// Launch shape of one kernel family: cache policy bits of the state loads and stores, waves
+// per workgroup, and whether a workgroup runs alone on its CU.  Solo workgroups ask for
+// kSoloLds bytes of dynamic LDS (they use none of it): more than half of the CU's 160 KiB,
+// so a second workgroup never fits beside one, plus the kernel's static LDS (under 16 KiB),
+// within the 160 KiB a workgroup may hold.
+template <int LoadPol, int StorePol, int Waves, bool Solo = false>
+struct Shape {
+  static constexpr int kLoad = LoadPol;
+  static constexpr int kStore = StorePol;
+  static constexpr int kWaveCount = Waves;
+  static constexpr bool kSolo = Solo;
+};
+constexpr size_t kSoloLds = 96 * 1024;
+
+template <typename S, int Width, int ConvCols>
 void launch_kernel(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
                    hipStream_t stream) {
-  auto kernel =
-      dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, LoadPol, StorePol, Width, ConvCols, Waves>
-                        : gdn_decode_kernel<true, false, LoadPol, StorePol, Width, ConvCols, Waves>)
-              : (w_bf16 ? gdn_decode_kernel<false, true, LoadPol, StorePol, Width, ConvCols, Waves>
-                        : gdn_decode_kernel<false, false, LoadPol, StorePol, Width, ConvCols, Waves>);
-  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * Waves), 0, stream, p.indices, p.cu,
-                     p.accepted, p.num_v_heads, p);
+  constexpr int LP = S::kLoad, SP = S::kStore, W = S::kWaveCount;
+  auto kernel = dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, LP, SP, Width, ConvCols, W>
+                                  : gdn_decode_kernel<true, false, LP, SP, Width, ConvCols, W>)
+                        : (w_bf16 ? gdn_decode_kernel<false, true, LP, SP, Width, ConvCols, W>
+                                  : gdn_decode_kernel<false, false, LP, SP, Width, ConvCols, W>);
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * W), S::kSolo ? kSoloLds : 0, stream,
+                     p.indices, p.cu, p.accepted, p.num_v_heads, p);
 }
 
-// One cache policy: hints and wave count of the single-token step (LP1, SP1, Waves1) and of
-// verify steps (LPn, SPn, WavesN); the conv-fused kernels run 4 waves, with the hints LPc, SPc
-// for one token and LPn, SPn for several.
-template <int LP1, int SP1, int Waves1, int LPn, int SPn, int WavesN, int LPc, int SPc>
+// One cache policy: the shapes of the single-token step (One), of verify steps (Verify), and
+// of the conv-fused single-token (ConvOne) and verify (ConvVerify) steps, which run 4 waves.
+template <typename One, typename Verify, typename ConvOne, typename ConvVerify>
 void launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
                    uint32_t blocks, hipStream_t stream) {
+  static_assert(ConvOne::kWaveCount == kWaves && ConvVerify::kWaveCount == kWaves,
+                "the conv-fused kernels run 4 waves");
   if (conv) {
     switch (p.width) {
       case 1:  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
         if (p.conv_len <= 4)
-          launch_kernel<LPc, SPc, 1, 4, kWaves>(p, dt_bf16, w_bf16, blocks, stream);
+          launch_kernel<ConvOne, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
         else
-          launch_kernel<LPc, SPc, 1, kMaxConvLen, kWaves>(p, dt_bf16, w_bf16, blocks, stream);
+          launch_kernel<ConvOne, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
         break;
-      case 2: launch_kernel<LPn, SPn, 2, kMaxConvLen, kWaves>(p, dt_bf16, w_bf16, blocks, stream); break;
-      case 3: launch_kernel<LPn, SPn, 3, kMaxConvLen, kWaves>(p, dt_bf16, w_bf16, blocks, stream); break;
-      default: launch_kernel<LPn, SPn, 4, kMaxConvLen, kWaves>(p, dt_bf16, w_bf16, blocks, stream); break;
+      case 2: launch_kernel<ConvVerify, 2, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
+      case 3: launch_kernel<ConvVerify, 3, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
+      default: launch_kernel<ConvVerify, 4, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
     }
     return;
   }
   switch (p.width) {
-    case 1: launch_kernel<LP1, SP1, 1, 0, Waves1>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 2: launch_kernel<LPn, SPn, 2, 0, WavesN>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 3: launch_kernel<LPn, SPn, 3, 0, WavesN>(p, dt_bf16, w_bf16, blocks, stream); break;
-    default: launch_kernel<LPn, SPn, 4, 0, WavesN>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 1: launch_kernel<One, 1, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 2: launch_kernel<Verify, 2, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 3: launch_kernel<Verify, 3, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
+    default: launch_kernel<Verify, 4, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
   }
 }
 
@@ -723,18 +738,24 @@ int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, b
   //   one token, stream: 16 waves, non-temporal loads, system-scope stores (B=128 cold
   //                      89.3 us = 6.01 TB/s; with non-temporal stores 90.9, the keep
   //                      kernel 107.6; B=32 cold 24.8 against 29.8).
-  //   verify, either:    16 waves, plain loads, non-temporal stores (B=64, T=4: 99.4 us hot
-  //                      and 125.0 cold, against 105.1 and 138.9 with 4 waves).
+  //   verify, keep:      16 waves, plain loads, non-temporal stores, one workgroup per CU
+  //                      (B=64, T=4: 98.7 us hot, 120.8 cold; two per CU 98.8 and 124.4;
+  //                      4 waves 105.1 and 138.9).
+  //   verify, stream:    16 waves, non-temporal loads, system-scope stores, one workgroup
+  //                      per CU (B=64, T=4 cold: 114.4 us = 5.87 TB/s; two per CU 116.0;
+  //                      the keep kernel 120.8).
   //   conv-fused, one token: 4 waves, plain loads and stores (keep; 22.4 us hot) or
   //                      non-temporal ones (stream; 28.5 us cold, against 30.0 with
   //                      system-scope stores); conv-fused verify: 4 waves, plain loads,
   //                      non-temporal stores.
   const uint32_t n = static_cast<uint32_t>(blocks);
   if (a.cache_policy == LD_CACHE_STREAM)
-    launch_decode<kPolNT, kPolSys, 16, kPolPlain, kPolNT, 16, kPolNT, kPolNT>(p, conv, dt_bf16,
-                                                                             w_bf16, n, s);
+    launch_decode<Shape<kPolNT, kPolSys, 16>, Shape<kPolNT, kPolSys, 16, true>,
+                  Shape<kPolNT, kPolNT, kWaves>, Shape<kPolPlain, kPolNT, kWaves>>(
+        p, conv, dt_bf16, w_bf16, n, s);
   else
-    launch_decode<kPolPlain, kPolPlain, kWaves, kPolPlain, kPolNT, 16, kPolPlain, kPolPlain>(
+    launch_decode<Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, 16, true>,
+                  Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, kWaves>>(
         p, conv, dt_bf16, w_bf16, n, s);
   return check_launch(conv ? "ld_gdn_decode_conv" : "ld_gdn_decode");
 }
