@@ -51,6 +51,7 @@ struct DecodeParams {
   int32_t conv_len;
   const uint16_t* conv_weight;  // [conv_dim, 4]
   const uint16_t* conv_bias;    // [conv_dim] or NULL
+  bool conv_packed;             // host-side: dense dim-first, 16-byte aligned conv pool
 };
 
 // ---- state-tile traffic through buffer resources -------------------------------------------

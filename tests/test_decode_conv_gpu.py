@@ -4,7 +4,7 @@ state is a pure shift of bf16 data and must match bit for bit; SSM states and ou
 the decode tolerances.  Covers the workload's first configuration (B=1, 4/8 heads,
 zero-initialised conv state), the k-head groups 1, 2 and 3 (direct write and the
 last-reader write of the shared q/k conv state), vLLM's dim-first and dim-last conv pools,
-state lengths 3, 4 and 6, bias, padding and zero-token requests, speculative verify with 2
+the kernel's packed conv-state path against its per-element path, state lengths 3, 4 and 6, bias, padding and zero-token requests, speculative verify with 2
 to 4 tokens and random accepted counts over consecutive steps, requests the conv rejects,
 and graph replay."""
 
@@ -181,6 +181,42 @@ def test_ragged_verify_and_rejected_requests(gpu):
         s0 = int(case["slots"][r, 0])
         if s0 > 0:
             assert torch.equal(case["conv_state"][s0].cpu(), before[s0].cpu())
+
+
+@pytest.mark.parametrize("length,heads,bias", [(3, (16, 32), False), (4, (4, 8), True),
+                                                 (3, (16, 48), True)])
+def test_packed_and_per_element_conv_paths_agree(gpu, length, heads, bias):
+    """A dense, 16-byte aligned dim-first conv pool takes the kernel's packed path (each wave
+    moves its channels' columns as 16-byte pieces); the same data one element into a larger
+    buffer (2-byte aligned) takes the per-element path.  Over 3 steps both give the same bits
+    for the conv state, the SSM pool and the outputs, and the packed run matches the oracle."""
+    announce(test="conv_packed_vs_per_element", length=length, heads=heads, bias=bias)
+    case = conv_case(gpu, 8, heads, pool_slots=10, length=length, bias=bias, seed=90 + length)
+    dense = case["conv_state"]
+    flat = torch.empty(dense.numel() + 1, dtype=dense.dtype, device=dense.device)
+    shifted = flat[1:].view(dense.shape)
+    shifted.copy_(dense)
+    assert dense.data_ptr() % 16 == 0 and shifted.data_ptr() % 16 != 0
+    pool2, out2 = case["pool"].clone(), case["out"].clone()
+    gen = torch.Generator().manual_seed(93)
+    for step in range(3):
+        case["qkv"].copy_(torch.randn(case["qkv"].shape, generator=gen).bfloat16())
+        expected = expected_decode_conv(
+            case["qkv"], dense, case["conv_weight"], case["conv_bias"],
+            *[case[k] for k in ORDER], 1e-6, return_pre=True)
+        rest = [case[k] for k in ORDER]
+        torch.ops.lightdelta.decode_conv(case["qkv"], dense, case["conv_weight"],
+                                         case["conv_bias"], *rest, 1e-6)
+        rest[ORDER.index("pool")], rest[ORDER.index("out")] = pool2, out2
+        torch.ops.lightdelta.decode_conv(case["qkv"], shifted, case["conv_weight"],
+                                         case["conv_bias"], *rest, 1e-6)
+        torch.cuda.synchronize()
+        assert torch.equal(dense, shifted), f"step {step}: conv states differ between the paths"
+        assert torch.equal(case["pool"], pool2), f"step {step}: SSM pools differ between the paths"
+        assert torch.equal(case["out"], out2), f"step {step}: outputs differ between the paths"
+        check_step(case, expected, f"packed step {step}")
+        case["pool"].copy_(expected[1].to(case["pool"].device))
+        pool2.copy_(case["pool"])
 
 
 def test_single_token_long_conv_state(gpu):
