@@ -155,48 +155,43 @@ constexpr int kPrepThreads = 512;
 constexpr int kPrepWaves = kPrepThreads / 64;
 constexpr int kPrepTokens = kC / kPrepWaves;   // tokens normalised per wave
 
-// ---- phase 1: per (chunk, v-head) ----------------------------------------------------
+// ---- phase 1: per (chunk, k-head), then per v-head of its group -----------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// One workgroup per (chunk, k-head).  What depends on q and k alone -- their loads, inverse
+// norms, the raw q.k and k.k tiles on the bf16 matrix cores -- is done once; then the
+// workgroup runs the group's HV/H v-heads in turn: gates, the scaled A and P, the inverses of
+// I + A's diagonal blocks, the substitution for W and U, and the v-head's record.  (One
+// workgroup per (chunk, v-head) recomputed the q/k part for every v-head of a group: with
+// 16 qk / 32 v heads, about a third of each workgroup's lifetime.)
 template <bool DtBf16>
 __global__ __launch_bounds__(kPrepThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
                        const int32_t* chunk_start, int records) {
-  // Workgroups go to the 8 XCDs round-robin by id.  The v-heads of one k-head group read
-  // the same q and k rows, so they get consecutive ids on one XCD and share its L2:
-  // id = ((unit / 8) * group + g) * 8 + unit % 8 for unit = chunk * H + k-head.
-  const int xcd = blockIdx.x & 7;
-  const int rank = blockIdx.x >> 3;
-  const int64_t unit = static_cast<int64_t>(rank / p.group) * 8 + xcd;
-  const int member = rank - (rank / p.group) * p.group;
+  const int64_t unit = blockIdx.x;   // chunk * H + k-head
   const int g = static_cast<int>(unit / p.num_k_heads);   // global chunk
   if (g >= records) return;
-  const int head = static_cast<int>(unit - static_cast<int64_t>(g) * p.num_k_heads) * p.group + member;
+  const int key_head = static_cast<int>(unit - static_cast<int64_t>(g) * p.num_k_heads);
   int seq = 0, t0 = 0, len = 0;
   if (!find_chunk(p.cu, chunk_start, num_sequences, g, seq, t0, len)) return;
-  float* rec = ws + (static_cast<int64_t>(g) * p.num_v_heads + head) * kRecord;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
   // the wave index in a scalar register: the tile table, the A / P choice and the W / U
   // role are then scalar branches
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const int key_head = head / p.group;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int q_col = key_head * kDim;
   const int k_col = (p.num_k_heads + key_head) * kDim;
-  const int v_col = (2 * p.num_k_heads + head) * kDim;
 
   constexpr int kHRow = kDim + 8;  // padded LDS row of the bf16 q / k (272 bytes)
   constexpr int kRow = kDim + 4;   // padded LDS row of W (floats)
   constexpr int kARow = kC + 4;    // padded LDS row of -A and P
   constexpr int kTRow = 20;        // padded LDS row of a diagonal block's inverse
-  // One 34 KiB region: q and k (the bf16 inputs, [64][136] each) until A and P are formed;
-  // then -A and P ([64][68] fp32 each, in place of q and k); then W ([64][132] fp32) on its
-  // way to the workspace.  The four inverses [4][16][20] have their own 5 KiB.
+  // q and k (the bf16 inputs, [64][136] each) for the whole workgroup; per v-head, -A and P
+  // ([64][68] fp32 each), then W ([64][132] fp32) in their place on its way to the
+  // workspace; the four inverses [4][16][20] have their own 5 KiB.
   constexpr int kHalfBytes = kC * kHRow * 2;
-  static_assert(kC * kARow * 4 <= kHalfBytes && kC * kRow * 4 <= 2 * kHalfBytes, "LDS plan");
-  __shared__ __attribute__((aligned(16))) uint8_t sBuf[2 * kHalfBytes];
+  constexpr int kApBytes = 2 * kC * kARow * 4;
+  static_assert(kC * kRow * 4 <= kApBytes, "LDS plan");
+  __shared__ __attribute__((aligned(16))) uint8_t sQk[2 * kHalfBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t sAp[kApBytes];
   __shared__ __attribute__((aligned(16))) float sT[4 * 16 * kTRow];
   __shared__ float sG[kC];
   __shared__ float sBeta[kC];
@@ -204,15 +199,16 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   __shared__ float sEk[kC];     // exp(G_n-1 - G_i)
   __shared__ float sRq[kC];     // rq_i scale (zero past the end)
   __shared__ float sRk[kC];     // rk_i (zero past the end)
-  uint16_t (*const sQh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sBuf);
-  uint16_t (*const sKh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sBuf + kHalfBytes);
-  float* const sA = reinterpret_cast<float*>(sBuf);
-  float* const sP = reinterpret_cast<float*>(sBuf + kHalfBytes);
-  float* const sW = reinterpret_cast<float*>(sBuf);
+  uint16_t (*const sQh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sQk);
+  uint16_t (*const sKh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sQk + kHalfBytes);
+  float* const sA = reinterpret_cast<float*>(sAp);
+  float* const sP = reinterpret_cast<float*>(sAp + kApBytes / 2);
+  float* const sW = reinterpret_cast<float*>(sAp);
 
   // q and k of the chunk's tokens and their inverse norms (zero rows past its end); wave w
   // does tokens 8w .. 8w+7, all 8 tokens' loads in flight before the first norm
   {
+    const int lane = threadIdx.x & 63;
     uint32_t qr[kPrepTokens], kr[kPrepTokens];
 #pragma unroll
     for (int ii = 0; ii < kPrepTokens; ++ii) {
@@ -239,244 +235,264 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
     }
   }
-  // gates and the in-chunk cumulative log decay (wave 0, lane = token)
-  if (wave == 0) {
-    const bool live = lane < len;
-    const int64_t tok = t0 + min(lane, len - 1);
-    const float dt_bias = load_param(p.dt_bias, head, DtBf16);
-    const float x = bf16_to_f32(p.a[tok * p.a_row + head]) + dt_bias;
-    const float g = live ? -__expf(p.a_log[head]) * softplus(x) : 0.0f;
-    const float beta = live ? sigmoid(bf16_to_f32(p.b[tok * p.b_row + head])) : 0.0f;
-    float G = g;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float up = __shfl_up(G, d);
-      if (lane >= d) G += up;
-    }
-    const float glast = __shfl(G, len - 1);
-    sG[lane] = G;
-    sBeta[lane] = beta;
-    sEg[lane] = __expf(G);
-    sEk[lane] = __expf(glast - G);
-    if (lane == 0) rec[kOffMisc] = __expf(glast);
-  }
   __syncthreads();
 
   // Waves 0-3 solve for W's columns 32w .. 32w + 31, waves 4-7 for U's (2 column tiles
-  // each).  U's right-hand side (beta_i v_i) comes from global memory: its loads go out
-  // before the products.
+  // each).
   constexpr int kNt = 2;   // column tiles per wave
   const bool solves_u = wave >= 4;
   const int n0 = (wave & 3) * 16 * kNt;
-  uint16_t vr[4][kNt][4];   // [row block][column tile][r]
-  if (solves_u) {
+
+  for (int member = 0; member < p.group; ++member) {
+    // The lane coordinates are derived anew in every iteration, through a zero the compiler
+    // cannot see through: the loop's per-lane addresses are then formed in the loop, where
+    // they are used, instead of being hoisted and held in registers across it (which
+    // spilled).
+    int opaque_zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(opaque_zero));
+    const int tid = static_cast<int>(threadIdx.x) + opaque_zero;
+    const int lane = tid & 63;
+    const int li = lane & 15;
+    const int lg = lane >> 4;
+    const int head = key_head * p.group + member;
+    const int v_col = (2 * p.num_k_heads + head) * kDim;
+    float* rec = ws + (static_cast<int64_t>(g) * p.num_v_heads + head) * kRecord;
+
+    // U's right-hand side (beta_i v_i) comes from global memory: its loads go out first
+    uint16_t vr[4][kNt][4];   // [row block][column tile][r]
+    if (solves_u) {
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t tok = t0 + min(16 * rb + 4 * lg + r, len - 1);
+          const uint16_t* row = p.qkv + tok * p.qkv_row + v_col + n0 + li;
+#pragma unroll
+          for (int nt = 0; nt < kNt; ++nt) vr[rb][nt][r] = row[16 * nt];
+        }
+    }
+    // gates and the in-chunk cumulative log decay (wave 0, lane = token)
+    if (wave == 0) {
+      const bool live = lane < len;
+      const int64_t tok = t0 + min(lane, len - 1);
+      const float dt_bias = load_param(p.dt_bias, head, DtBf16);
+      const float x = bf16_to_f32(p.a[tok * p.a_row + head]) + dt_bias;
+      const float gl = live ? -__expf(p.a_log[head]) * softplus(x) : 0.0f;
+      const float beta = live ? sigmoid(bf16_to_f32(p.b[tok * p.b_row + head])) : 0.0f;
+      float G = gl;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float up = __shfl_up(G, d);
+        if (lane >= d) G += up;
+      }
+      const float glast = __shfl(G, len - 1);
+      sG[lane] = G;
+      sBeta[lane] = beta;
+      sEg[lane] = __expf(G);
+      sEk[lane] = __expf(glast - G);
+      if (lane == 0) rec[kOffMisc] = __expf(glast);
+    }
+    __syncthreads();
+
+    // A and P tiles of the raw inputs, q_i . k_m and k_i . k_m: bf16 operands with exact
+    // products and fp32 accumulation (v_mfma_f32_16x16x32_bf16, lane (li, lg) giving
+    // X[row li][32 s + 8 lg + e]), 4 steps of 32 per tile; the third tile for waves 0-3 only
+    // (a uniform branch).  Recomputed for each v-head (12 products), so that no register
+    // carries them from one v-head to the next.
+    const uint32_t codes = prep_tiles(wave);
+    const int tiles = wave < 4 ? 3 : 2;
+    f32x4 prod[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      if (t >= tiles) break;
+      const uint32_t code = (codes >> (5 * t)) & 31u;
+      const int mt = (code >> 2) & 3;
+      const int nt = code & 3;
+      const uint16_t* arow = ((code & 16u) ? &sQh[0][0] : &sKh[0][0]) + (16 * mt + li) * kHRow + 8 * lg;
+      const uint16_t* brow = &sKh[0][0] + (16 * nt + li) * kHRow + 8 * lg;
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + 32 * s4);
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(brow + 32 * s4);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+      }
+      prod[t] = acc;
+    }
+
+    // the right-hand sides in the fragment layout: x[rb][nt][r] = B[16 rb + 4 lg + r][n0 + 16 nt + li]
+    // (one uniform branch around two straight-line loops)
+    f32x4 x[4][kNt];
+    if (solves_u) {
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float beta = sBeta[16 * rb + 4 * lg + r];  // zero past the end
+#pragma unroll
+          for (int nt = 0; nt < kNt; ++nt) x[rb][nt][r] = beta * bf16_to_f32(vr[rb][nt][r]);
+        }
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * rb + 4 * lg + r;
+          const float wscale = sBeta[i] * sEg[i] * sRk[i];
+#pragma unroll
+          for (int nt = 0; nt < kNt; ++nt)
+            x[rb][nt][r] = wscale * bf16_to_f32(sKh[i][n0 + 16 * nt + li]);
+        }
+    }
+
+    // Qr and Kr (the bf16 inputs in the scan's load order) and the per-token scales to the
+    // v-head's record (item = one 16-byte piece)
+    {
+      u32x4* qdst = reinterpret_cast<u32x4*>(rec + kOffQr);
+      u32x4* kdst = reinterpret_cast<u32x4*>(rec + kOffKr);
+#pragma unroll
+      for (int it = 0; it < kC * kDim / 8 / kPrepThreads; ++it) {
+        const int item = it * kPrepThreads + tid;
+        const int l = item & 63;
+        const int i = 16 * (item >> 8) + (l & 15);
+        const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
+        qdst[item] = *reinterpret_cast<const u32x4*>(&sQh[i][c0]);
+        const int k = 16 * (item >> 7) + (l & 15);
+        const int j = 16 * (l >> 4) + 8 * ((item >> 6) & 1);
+        kdst[item] = u32x4{sKh[j][k] | (static_cast<uint32_t>(sKh[j + 1][k]) << 16),
+                           sKh[j + 2][k] | (static_cast<uint32_t>(sKh[j + 3][k]) << 16),
+                           sKh[j + 4][k] | (static_cast<uint32_t>(sKh[j + 5][k]) << 16),
+                           sKh[j + 6][k] | (static_cast<uint32_t>(sKh[j + 7][k]) << 16)};
+      }
+      if (tid < kC)
+        rec[kOffMisc + kMiscSq + tid] = sRq[tid] * sEg[tid];
+      else if (tid < 2 * kC)
+        rec[kOffMisc + kMiscCk + tid - kC] = sRk[tid - kC] * sEk[tid - kC];
+    }
+
+    // scale the tiles: A (negated) and P to LDS, P zero above the diagonal
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      if (t >= tiles) break;
+      const uint32_t code = (codes >> (5 * t)) & 31u;
+      const int mt = (code >> 2) & 3;
+      const int m = 16 * (code & 3) + li;
+      const float gm = sG[m];
+      const float rkm = sRk[m];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t tok = t0 + min(16 * rb + 4 * lg + r, len - 1);
-        const uint16_t* row = p.qkv + tok * p.qkv_row + v_col + n0 + li;
-#pragma unroll
-        for (int nt = 0; nt < kNt; ++nt) vr[rb][nt][r] = row[16 * nt];
+        const int i = 16 * mt + 4 * lg + r;
+        const float gam = __expf(sG[i] - gm);
+        // the products are of the raw inputs: q^_i . k^_m = (rq_i scale rk_m) (q_i . k_m)
+        if (code & 16u)
+          sP[i * kARow + m] = (m <= i && i < len) ? gam * ((sRq[i] * rkm) * prod[t][r]) : 0.0f;
+        else
+          sA[i * kARow + m] = m < i ? -(sBeta[i] * gam * ((sRk[i] * rkm) * prod[t][r])) : 0.0f;
       }
-  }
-
-  // A and P tiles of the raw inputs, q_i . k_m and k_i . k_m: bf16 operands with exact
-  // products and fp32 accumulation (v_mfma_f32_16x16x32_bf16, lane (li, lg) giving
-  // X[row li][32 s + 8 lg + e]), 4 steps of 32 per tile; the third tile for waves 0-3 only
-  // (a uniform branch)
-  const uint32_t codes = prep_tiles(wave);
-  const int tiles = wave < 4 ? 3 : 2;
-  f32x4 prod[3];
-#pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    if (t >= tiles) break;
-    const uint32_t code = (codes >> (5 * t)) & 31u;
-    const int mt = (code >> 2) & 3;
-    const int nt = code & 3;
-    const uint16_t* arow = ((code & 16u) ? &sQh[0][0] : &sKh[0][0]) + (16 * mt + li) * kHRow + 8 * lg;
-    const uint16_t* brow = &sKh[0][0] + (16 * nt + li) * kHRow + 8 * lg;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + 32 * s4);
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(brow + 32 * s4);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
     }
-    prod[t] = acc;
-  }
+    for (int e = tid; e < kC * kC; e += kPrepThreads) {
+      const int i = e >> 6;
+      const int m = e & 63;
+      if ((m >> 4) > (i >> 4)) sP[i * kARow + m] = 0.0f;
+    }
+    __syncthreads();
 
-  // the right-hand sides in the fragment layout: x[rb][nt][r] = B[16 rb + 4 lg + r][n0 + 16 nt + li]
-  // (one uniform branch around two straight-line loops)
-  f32x4 x[4][kNt];
-  if (solves_u) {
+    // P to the workspace in its load order
+    {
+      f32x4* pdst = reinterpret_cast<f32x4*>(rec + kOffP);
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float beta = sBeta[16 * rb + 4 * lg + r];  // zero past the end
-#pragma unroll
-        for (int nt = 0; nt < kNt; ++nt) x[rb][nt][r] = beta * bf16_to_f32(vr[rb][nt][r]);
+      for (int it = 0; it < kC * kC / 4 / kPrepThreads; ++it) {
+        const int item = it * kPrepThreads + tid;
+        const int l = item & 63;
+        const int i = 16 * (item >> 8) + (l & 15);
+        const int j = 16 * (l >> 4) + 4 * ((item >> 6) & 3);
+        pdst[item] = *reinterpret_cast<const f32x4*>(sP + i * kARow + j);
       }
-  } else {
+    }
+    // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
+    // (block w by wave w < 4)
+    if (wave < 4 && lane < 16) {
+      const float* ab = sA + (16 * wave) * kARow + 16 * wave;
+      // row by row: col[i] = delta(i, li) + sum over m < i of (-A)[i][m] col[m], the terms in
+      // order of m (row i of -A read as it is needed)
+      float col[16];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+      for (int i = 0; i < 16; ++i) {
+        float acc = i == li ? 1.0f : 0.0f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * rb + 4 * lg + r;
-        const float wscale = sBeta[i] * sEg[i] * sRk[i];
-#pragma unroll
-        for (int nt = 0; nt < kNt; ++nt)
-          x[rb][nt][r] = wscale * bf16_to_f32(sKh[i][n0 + 16 * nt + li]);
+        for (int m = 0; m < i; ++m) acc = fmaf(ab[i * kARow + m], col[m], acc);
+        col[i] = acc;
       }
-  }
-
-  // Qr and Kr (the bf16 inputs in the scan's load order) and the per-token scales to the
-  // workspace while q and k are still in LDS (item = one 16-byte piece)
-  {
-    u32x4* qdst = reinterpret_cast<u32x4*>(rec + kOffQr);
-    u32x4* kdst = reinterpret_cast<u32x4*>(rec + kOffKr);
+      float* tb = sT + wave * 16 * kTRow;
 #pragma unroll
-    for (int it = 0; it < kC * kDim / 8 / kPrepThreads; ++it) {
-      const int item = it * kPrepThreads + tid;
-      const int l = item & 63;
-      const int i = 16 * (item >> 8) + (l & 15);
-      const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
-      qdst[item] = *reinterpret_cast<const u32x4*>(&sQh[i][c0]);
-      const int k = 16 * (item >> 7) + (l & 15);
-      const int j = 16 * (l >> 4) + 8 * ((item >> 6) & 1);
-      kdst[item] = u32x4{sKh[j][k] | (static_cast<uint32_t>(sKh[j + 1][k]) << 16),
-                         sKh[j + 2][k] | (static_cast<uint32_t>(sKh[j + 3][k]) << 16),
-                         sKh[j + 4][k] | (static_cast<uint32_t>(sKh[j + 5][k]) << 16),
-                         sKh[j + 6][k] | (static_cast<uint32_t>(sKh[j + 7][k]) << 16)};
+      for (int i = 0; i < 16; ++i) tb[i * kTRow + li] = col[i];
     }
-    if (tid < kC)
-      rec[kOffMisc + kMiscSq + tid] = sRq[tid] * sEg[tid];
-    else if (tid < 2 * kC)
-      rec[kOffMisc + kMiscCk + tid - kC] = sRk[tid - kC] * sEk[tid - kC];
-  }
-  __syncthreads();  // q and k no longer read
+    __syncthreads();
 
-  // scale the tiles: A (negated) and P to LDS, P zero above the diagonal
+    // blocked forward substitution: X_rb = T_rb (B_rb - sum over j < rb of A_rb,j X_j)
 #pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    if (t >= tiles) break;
-    const uint32_t code = (codes >> (5 * t)) & 31u;
-    const int mt = (code >> 2) & 3;
-    const int m = 16 * (code & 3) + li;
-    const float gm = sG[m];
-    const float rkm = sRk[m];
+    for (int rb = 0; rb < 4; ++rb) {
+      f32x4 y[kNt];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * mt + 4 * lg + r;
-      const float gam = __expf(sG[i] - gm);
-      // the products are of the raw inputs: q^_i . k^_m = (rq_i scale rk_m) (q_i . k_m)
-      if (code & 16u)
-        sP[i * kARow + m] = (m <= i && i < len) ? gam * ((sRq[i] * rkm) * prod[t][r]) : 0.0f;
-      else
-        sA[i * kARow + m] = m < i ? -(sBeta[i] * gam * ((sRk[i] * rkm) * prod[t][r])) : 0.0f;
-    }
-  }
-  for (int e = tid; e < kC * kC; e += kPrepThreads) {
-    const int i = e >> 6;
-    const int m = e & 63;
-    if ((m >> 4) > (i >> 4)) sP[i * kARow + m] = 0.0f;
-  }
-  __syncthreads();
-
-  // P to the workspace in its load order
-  {
-    f32x4* pdst = reinterpret_cast<f32x4*>(rec + kOffP);
+      for (int nt = 0; nt < kNt; ++nt) y[nt] = x[rb][nt];
 #pragma unroll
-    for (int it = 0; it < kC * kC / 4 / kPrepThreads; ++it) {
-      const int item = it * kPrepThreads + tid;
-      const int l = item & 63;
-      const int i = 16 * (item >> 8) + (l & 15);
-      const int j = 16 * (l >> 4) + 4 * ((item >> 6) & 3);
-      pdst[item] = *reinterpret_cast<const f32x4*>(sP + i * kARow + j);
-    }
-  }
-  // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
-  // (block w by wave w < 4)
-  if (wave < 4 && lane < 16) {
-    const float* ab = sA + (16 * wave) * kARow + 16 * wave;
-    // row by row: col[i] = delta(i, li) + sum over m < i of (-A)[i][m] col[m], the terms in
-    // order of m (row i of -A read as it is needed)
-    float col[16];
+      for (int j = 0; j < rb; ++j) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(sA + (16 * rb + li) * kARow + 16 * j + 4 * lg);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = i == li ? 1.0f : 0.0f;
-#pragma unroll
-      for (int m = 0; m < i; ++m) acc = fmaf(ab[i * kARow + m], col[m], acc);
-      col[i] = acc;
-    }
-    float* tb = sT + wave * 16 * kTRow;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) tb[i * kTRow + li] = col[i];
-  }
-  __syncthreads();
-
-  // blocked forward substitution: X_rb = T_rb (B_rb - sum over j < rb of A_rb,j X_j)
-#pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
-    f32x4 y[kNt];
-#pragma unroll
-    for (int nt = 0; nt < kNt; ++nt) y[nt] = x[rb][nt];
-#pragma unroll
-    for (int j = 0; j < rb; ++j) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(sA + (16 * rb + li) * kARow + 16 * j + 4 * lg);
+        for (int nt = 0; nt < kNt; ++nt) {
+          y[nt] = mfma(a.x, x[j][nt].x, y[nt]);
+          y[nt] = mfma(a.y, x[j][nt].y, y[nt]);
+          y[nt] = mfma(a.z, x[j][nt].z, y[nt]);
+          y[nt] = mfma(a.w, x[j][nt].w, y[nt]);
+        }
+      }
+      const f32x4 tr = *reinterpret_cast<const f32x4*>(sT + (rb * 16 + li) * kTRow + 4 * lg);
 #pragma unroll
       for (int nt = 0; nt < kNt; ++nt) {
-        y[nt] = mfma(a.x, x[j][nt].x, y[nt]);
-        y[nt] = mfma(a.y, x[j][nt].y, y[nt]);
-        y[nt] = mfma(a.z, x[j][nt].z, y[nt]);
-        y[nt] = mfma(a.w, x[j][nt].w, y[nt]);
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        acc = mfma(tr.x, y[nt].x, acc);
+        acc = mfma(tr.y, y[nt].y, acc);
+        acc = mfma(tr.z, y[nt].z, acc);
+        acc = mfma(tr.w, y[nt].w, acc);
+        x[rb][nt] = acc;
       }
     }
-    const f32x4 tr = *reinterpret_cast<const f32x4*>(sT + (rb * 16 + li) * kTRow + 4 * lg);
-#pragma unroll
-    for (int nt = 0; nt < kNt; ++nt) {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      acc = mfma(tr.x, y[nt].x, acc);
-      acc = mfma(tr.y, y[nt].y, acc);
-      acc = mfma(tr.z, y[nt].z, acc);
-      acc = mfma(tr.w, y[nt].w, acc);
-      x[rb][nt] = acc;
-    }
-  }
 
-  // U straight from the fragments (its row block rb is the scan wave, its column tile the
-  // scan's block of v rows); W through LDS, once every wave is past its reads of -A (W takes
-  // the region of -A and P)
-  if (solves_u) {
+    // U straight from the fragments (its row block rb is the scan wave, its column tile the
+    // scan's block of v rows); W through LDS, once every wave is past its reads of -A (W takes
+    // the region of -A and P)
+    if (solves_u) {
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int nt = 0; nt < kNt; ++nt)
-        *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * 4 + rb) * 256 + lane * 4) =
-            x[rb][nt];
-  }
-  __syncthreads();
-  if (!solves_u) {
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-      for (int nt = 0; nt < kNt; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          sW[(16 * rb + 4 * lg + r) * kRow + n0 + 16 * nt + li] = x[rb][nt][r];
-  }
-  __syncthreads();
-  {
-    f32x4* wdst = reinterpret_cast<f32x4*>(rec + kOffW);
-#pragma unroll
-    for (int it = 0; it < kC * kDim / 4 / kPrepThreads; ++it) {
-      const int item = it * kPrepThreads + tid;
-      const int l = item & 63;
-      const int i = 16 * (item >> 9) + (l & 15);
-      const int k4 = 32 * (l >> 4) + 4 * ((item >> 6) & 7);
-      wdst[item] = *reinterpret_cast<const f32x4*>(sW + i * kRow + k4);
+        for (int nt = 0; nt < kNt; ++nt)
+          *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * 4 + rb) * 256 + lane * 4) =
+              x[rb][nt];
     }
+    __syncthreads();
+    if (!solves_u) {
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int nt = 0; nt < kNt; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            sW[(16 * rb + 4 * lg + r) * kRow + n0 + 16 * nt + li] = x[rb][nt][r];
+    }
+    __syncthreads();
+    {
+      f32x4* wdst = reinterpret_cast<f32x4*>(rec + kOffW);
+#pragma unroll
+      for (int it = 0; it < kC * kDim / 4 / kPrepThreads; ++it) {
+        const int item = it * kPrepThreads + tid;
+        const int l = item & 63;
+        const int i = 16 * (item >> 9) + (l & 15);
+        const int k4 = 32 * (l >> 4) + 4 * ((item >> 6) & 7);
+        wdst[item] = *reinterpret_cast<const f32x4*>(sW + i * kRow + k4);
+      }
+    }
+    // the next v-head rewrites the gates, -A, P and W
+    __syncthreads();
   }
 }
 
@@ -931,8 +947,8 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   const int64_t chunks = max_chunks(num_tokens, num_sequences);
   if (chunks > 0x7fffffff || p.num_v_heads > 65535)
     return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large for the chunked form");
-  // (chunk, k-head) units padded to whole groups of 8, times the group's v-heads
-  const int64_t prep_groups = (chunks * p.num_k_heads + 7) / 8 * 8 * p.group;
+  // one workgroup per (chunk, k-head)
+  const int64_t prep_groups = chunks * p.num_k_heads;
   if (prep_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
   const dim3 per_chunk(static_cast<uint32_t>(prep_groups));
   hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, stream, p.cu, num_sequences,
