@@ -69,11 +69,20 @@ ORDER = ("qkv", "a", "b", "a_log", "dt_bias", "slots", "cu", "accepted", "pool",
 TRAFFIC_FILE = ROOT / "profiles" / "gdn_decode_b32_traffic.json"
 # The reference's published H100 operator medians (docs/performance.md:12-25 of the
 # reference; 16/48 heads): (batch, tokens per request) -> (indexed us, graph us).
-REF_H100_US = {
-    (1, 1): (17.47, 12.38), (1, 2): (18.91, 14.11), (1, 3): (21.22, 16.14), (1, 4): (19.90, 19.17),
-    (4, 1): (18.27, 14.72), (4, 2): (19.73, 19.50), (4, 3): (24.70, 24.48), (4, 4): (30.46, 30.10),
-    (8, 1): (20.48, 20.21), (8, 2): (31.98, 31.84), (8, 3): (42.24, 42.29), (8, 4): (53.73, 53.57),
+REF_H100_US = {  # (reference, fusion, indexed, graph) medians in us
+    (1, 1): (983.09, 321.23, 17.47, 12.38), (1, 2): (1476.64, 313.04, 18.91, 14.11),
+    (1, 3): (1781.74, 326.14, 21.22, 16.14), (1, 4): (2089.46, 313.46, 19.90, 19.17),
+    (4, 1): (995.09, 307.68, 18.27, 14.72), (4, 2): (1525.97, 314.86, 19.73, 19.50),
+    (4, 3): (1831.23, 313.06, 24.70, 24.48), (4, 4): (2111.70, 300.53, 30.46, 30.10),
+    (8, 1): (1014.74, 375.63, 20.48, 20.21), (8, 2): (1797.76, 305.09, 31.98, 31.84),
+    (8, 3): (1872.11, 312.96, 42.24, 42.29), (8, 4): (2117.74, 367.98, 53.73, 53.57),
 }
+# The reference benchmark's four configurations (configs/{reference,fusion,indexed,graph}.toml
+# of the reference): compute, state access, graph replay.
+OPERATOR_MODES = (("reference", "torch_reference", "packed", False),
+                  ("fusion", "cuda_fused", "packed", False),
+                  ("indexed", "cuda_fused", "indexed", False),
+                  ("graph", "cuda_fused", "indexed", True))
 
 
 def parse_args():
@@ -320,9 +329,11 @@ def operator_table(device, iterations=30):
     the reference): 16 qk / 48 v heads, B in {1, 4, 8} x T in {1..4}, its seeded inputs
     (qkv and gate bf16 0.2 N(0,1), pool 0.1 N(0,1) over slots 1..B*T, bf16 dt_bias and norm
     weight), five warm-up calls on a side stream, then `iterations` samples that each restore
-    the pool outside the timed interval and time one call with HIP events: `indexed` an eager
-    GDNBackend call (indexed state access, host dispatch included), `graph` the replay of
-    that call captured in a HIP graph.  Medians in us, beside the reference's H100 medians
+    the pool outside the timed interval and time one call with HIP events, for its four
+    GDNBackend configurations: `reference` (the unfused Torch computation, packed state
+    access), `fusion` (the fused kernel, packed state access), `indexed` (the fused kernel on
+    the pool directly) -- all eager, host dispatch included -- and `graph` (the indexed call
+    replayed from a HIP graph).  Medians in us, beside the reference's H100 medians
     (docs/performance.md:12-25 of the reference)."""
     import statistics
 
@@ -355,20 +366,24 @@ def operator_table(device, iterations=30):
                     weight=torch.randn(128, device=device, dtype=torch.bfloat16),
                     out=torch.empty(n, 48, 128, device=device, dtype=torch.bfloat16),
                 )
-                backend = GDNBackend(BackendConfig(compute="cuda_fused", state_io="indexed"))
-                side = torch.cuda.Stream()
-                side.wait_stream(torch.cuda.current_stream())
-                with torch.cuda.stream(side):
-                    for _ in range(5):
-                        pool.copy_(state)
-                        backend(**case)
-                torch.cuda.current_stream().wait_stream(side)
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph):
-                    backend(**case)
                 cell = {}
-                for name, execute in (("indexed", lambda: backend(**case)),
-                                      ("graph", graph.replay)):
+                for name, compute, state_io, replay in OPERATOR_MODES:
+                    backend = GDNBackend(BackendConfig(compute=compute, state_io=state_io))
+                    side = torch.cuda.Stream()
+                    side.wait_stream(torch.cuda.current_stream())
+                    with torch.cuda.stream(side):
+                        for _ in range(5):
+                            pool.copy_(state)
+                            backend(**case)
+                    torch.cuda.current_stream().wait_stream(side)
+                    graph = None
+                    if replay:
+                        graph = torch.cuda.CUDAGraph()
+                        with torch.cuda.graph(graph):
+                            backend(**case)
+                        execute = graph.replay
+                    else:
+                        execute = (lambda b: lambda: b(**case))(backend)
                     timers = []
                     for _ in range(iterations):
                         start, end = events()
@@ -380,12 +395,12 @@ def operator_table(device, iterations=30):
                     torch.cuda.synchronize()
                     cell[f"{name}_us"] = round(statistics.median(
                         a.elapsed_time(b) * 1000 for a, b in timers), 2)
-                ref_indexed, ref_graph = REF_H100_US[(batch, width)]
-                cell["h100_indexed_us"], cell["h100_graph_us"] = ref_indexed, ref_graph
-                cell["speedup_indexed"] = round(ref_indexed / cell["indexed_us"], 2)
-                cell["speedup_graph"] = round(ref_graph / cell["graph_us"], 2)
+                    del graph, backend
+                for (name, *_), h100 in zip(OPERATOR_MODES, REF_H100_US[(batch, width)]):
+                    cell[f"h100_{name}_us"] = h100
+                    cell[f"speedup_{name}"] = round(h100 / cell[f"{name}_us"], 2)
                 rows[f"B{batch}_T{width}"] = cell
-                del graph, case, pool, state, qkvz, ba
+                del case, pool, state, qkvz, ba
     finally:
         ops.set_state_cache_policy(saved)
     # The same method on a one-kernel graph of a trivial torch op: what a HIP graph replay
@@ -409,11 +424,14 @@ def operator_table(device, iterations=30):
     torch.cuda.synchronize()
     rows["graph_replay_floor_us"] = round(statistics.median(
         a.elapsed_time(b) * 1000 for a, b in timers), 2)
-    rows["workload"] = ("the reference's operator benchmark: 16 qk / 48 v heads, indexed state "
-                        "access, eager (host dispatch included) and HIP-graph replay, median of "
-                        f"{iterations} samples, pool restored outside the timed interval; "
-                        "h100_* = the reference's published H100 medians; graph_replay_floor_us "
-                        "= the replay of a one-kernel graph of torch's x.add_(1), same method")
+    rows["workload"] = ("the reference's operator benchmark: 16 qk / 48 v heads, its four "
+                        "GDNBackend configurations (reference: Torch computation + packed state; "
+                        "fusion: fused kernel + packed state; indexed: fused kernel on the pool; "
+                        "all eager, host dispatch included; graph: the indexed call replayed from "
+                        f"a HIP graph), median of {iterations} samples, pool restored outside "
+                        "the timed interval; h100_* = the reference's published H100 medians; "
+                        "graph_replay_floor_us = the replay of a one-kernel graph of torch's "
+                        "x.add_(1), same method")
     return rows
 
 
