@@ -1,11 +1,12 @@
-// Dispatcher kernels of torch.ops.lightdelta.decode and decode_conv (CUDA key, under which
-// HIP tensors dispatch on PyTorch-ROCm): the argument checks of the reference's launcher
+// Dispatcher kernels of the lightdelta ops (CUDA key, under which HIP tensors dispatch on
+// PyTorch-ROCm): decode and decode_conv with the argument checks of the reference's launcher
 // (csrc/gdn_decode.cu:366-403), generalised to any H, HV with HV % H == 0, with its
-// messages, then the C ABI of liblightdelta_hip.so on the current HIP stream of the
-// tensors' device.  The schemas are defined by lightdelta_amd/ops.py, which loads this
-// library; the other ops keep their Python kernels.  Host-only C++ (no device code): one
-// eager call costs a few microseconds of host time, as the reference's C++ launcher does,
-// where a Python kernel costs about twelve.
+// messages; the state-pool ops with the checks of the reference's state_io
+// (csrc/state_io.cu:29-49) and of the additive ones; then the C ABI of liblightdelta_hip.so
+// on the current HIP stream of the tensors' device.  The schemas are defined by
+// lightdelta_amd/ops.py, which loads this library (prefill keeps a Python kernel).
+// Host-only C++ (no device code): one eager call costs a few microseconds of host time, as
+// the reference's C++ launcher does, where a Python kernel costs about twelve.
 #include <ATen/core/Tensor.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -185,11 +186,155 @@ void decode_conv(const at::Tensor& mixed_qkv, at::Tensor conv_state, const at::T
   TORCH_CHECK(rc == LD_OK, ld_last_error());
 }
 
+// ---- state-pool ops ----------------------------------------------------------------------
+
+// Every dimension after the first densely packed (row-major).
+bool dense_inner(const at::Tensor& t) {
+  int64_t expected = 1;
+  for (int64_t d = t.dim() - 1; d >= 1; --d) {
+    if (t.size(d) != 1 && t.stride(d) != expected) return false;
+    expected *= t.size(d);
+  }
+  return true;
+}
+
+int64_t row_bytes(const at::Tensor& t) {
+  int64_t count = 1;
+  for (int64_t d = 1; d < t.dim(); ++d) count *= t.size(d);
+  return count * static_cast<int64_t>(t.element_size());
+}
+
+bool same_row_shape(const at::Tensor& a, const at::Tensor& b) {
+  if (a.dim() != b.dim()) return false;
+  for (int64_t d = 1; d < a.dim(); ++d)
+    if (a.size(d) != b.size(d)) return false;
+  return true;
+}
+
+// The reference's `check` (csrc/state_io.cu:29-41); fp32_4d = false drops the fp32 / 4-D
+// requirement for the dtype-generic ops.
+void check_state_layout(const at::Tensor& pool, const at::Tensor& slots, const at::Tensor& packed,
+                        bool fp32_4d) {
+  if (fp32_4d) {
+    TORCH_CHECK(pool.is_cuda() && pool.scalar_type() == at::kFloat && pool.dim() == 4 &&
+                    pool.stride(3) == 1 && pool.stride(2) == pool.size(3) &&
+                    pool.stride(1) == pool.size(2) * pool.size(3),
+                "pool must be CUDA FP32 with dense inner dimensions");
+  } else {
+    TORCH_CHECK(pool.is_cuda() && pool.dim() >= 1 && dense_inner(pool),
+                "pool must be a CUDA tensor with dense inner dimensions");
+  }
+  TORCH_CHECK(slots.device() == pool.device() && slots.scalar_type() == at::kInt &&
+                  slots.dim() == 1,
+              "slots must be a CUDA int32 vector");
+  TORCH_CHECK(packed.device() == pool.device() && packed.scalar_type() == pool.scalar_type() &&
+                  packed.dim() == pool.dim() && packed.size(0) == slots.numel() &&
+                  same_row_shape(packed, pool) && dense_inner(packed),
+              "invalid packed layout");
+}
+
+void check_valid(const at::Tensor& valid, const at::Tensor& slots, const at::Tensor& pool) {
+  TORCH_CHECK(valid.device() == pool.device() && valid.scalar_type() == at::kBool &&
+                  valid.sizes() == slots.sizes() && valid.is_contiguous(),
+              "valid must be a CUDA bool vector");
+}
+
+hipStream_t stream_of(const at::Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.get_device()).stream();
+}
+
+void gather(const at::Tensor& pool, const at::Tensor& slots, const at::Tensor& valid,
+            at::Tensor out) {
+  if (slots.numel() == 0) return;
+  const int64_t size = static_cast<int64_t>(pool.element_size());
+  const c10::DeviceGuard guard(pool.device());
+  const int rc = ld_state_gather(pool.data_ptr(), pool.stride(0) * size,
+                                 static_cast<const int32_t*>(slots.data_ptr()), slots.stride(0),
+                                 static_cast<const uint8_t*>(valid.data_ptr()), out.data_ptr(),
+                                 out.stride(0) * size, row_bytes(pool), slots.numel(),
+                                 stream_of(pool));
+  TORCH_CHECK(rc == LD_OK, ld_last_error());
+}
+
+void scatter(const at::Tensor& packed, const at::Tensor& slots, at::Tensor pool) {
+  if (slots.numel() == 0) return;
+  const int64_t size = static_cast<int64_t>(pool.element_size());
+  const c10::DeviceGuard guard(pool.device());
+  const int rc = ld_state_scatter(packed.data_ptr(), packed.stride(0) * size,
+                                  static_cast<const int32_t*>(slots.data_ptr()), slots.stride(0),
+                                  pool.data_ptr(), pool.stride(0) * size, row_bytes(pool),
+                                  slots.numel(), stream_of(pool));
+  TORCH_CHECK(rc == LD_OK, ld_last_error());
+}
+
+void gather_state(const at::Tensor& pool, const at::Tensor& slots, const at::Tensor& valid,
+                  at::Tensor out) {
+  check_state_layout(pool, slots, out, true);
+  check_valid(valid, slots, pool);
+  gather(pool, slots, valid, out);
+}
+
+void scatter_state(const at::Tensor& packed, const at::Tensor& slots, at::Tensor pool) {
+  check_state_layout(pool, slots, packed, true);
+  scatter(packed, slots, pool);
+}
+
+void gather_slots(const at::Tensor& pool, const at::Tensor& slots, const at::Tensor& valid,
+                  at::Tensor out) {
+  check_state_layout(pool, slots, out, false);
+  check_valid(valid, slots, pool);
+  gather(pool, slots, valid, out);
+}
+
+void scatter_slots(const at::Tensor& packed, const at::Tensor& slots, at::Tensor pool) {
+  check_state_layout(pool, slots, packed, false);
+  scatter(packed, slots, pool);
+}
+
+void copy_state(at::Tensor pool, const at::Tensor& src, const at::Tensor& dst) {
+  TORCH_CHECK(pool.is_cuda() && pool.dim() >= 1 && dense_inner(pool),
+              "pool must be a CUDA tensor with dense inner dimensions");
+  for (const at::Tensor* t : {&src, &dst})
+    TORCH_CHECK(t->device() == pool.device() && t->scalar_type() == at::kInt && t->dim() == 1 &&
+                    t->is_contiguous(),
+                "src and dst must be contiguous CUDA int32 vectors");
+  TORCH_CHECK(src.numel() == dst.numel(), "src and dst must have the same length");
+  if (src.numel() == 0) return;
+  const c10::DeviceGuard guard(pool.device());
+  const int rc = ld_state_copy(pool.data_ptr(),
+                               pool.stride(0) * static_cast<int64_t>(pool.element_size()),
+                               static_cast<const int32_t*>(src.data_ptr()),
+                               static_cast<const int32_t*>(dst.data_ptr()), src.numel(),
+                               row_bytes(pool), stream_of(pool));
+  TORCH_CHECK(rc == LD_OK, ld_last_error());
+}
+
+void zero_slots(at::Tensor pool, const at::Tensor& slots) {
+  TORCH_CHECK(pool.is_cuda() && pool.dim() >= 1 && dense_inner(pool),
+              "pool must be a CUDA tensor with dense inner dimensions");
+  TORCH_CHECK(slots.device() == pool.device() && slots.scalar_type() == at::kInt &&
+                  slots.dim() == 1 && slots.is_contiguous(),
+              "slots must be a contiguous CUDA int32 vector");
+  if (slots.numel() == 0) return;
+  const c10::DeviceGuard guard(pool.device());
+  const int rc = ld_state_zero(pool.data_ptr(),
+                               pool.stride(0) * static_cast<int64_t>(pool.element_size()),
+                               static_cast<const int32_t*>(slots.data_ptr()), slots.numel(),
+                               row_bytes(pool), stream_of(pool));
+  TORCH_CHECK(rc == LD_OK, ld_last_error());
+}
+
 }  // namespace
 
 TORCH_LIBRARY_IMPL(lightdelta, CUDA, m) {
   m.impl("decode", &decode);
   m.impl("decode_conv", &decode_conv);
+  m.impl("gather_state", &gather_state);
+  m.impl("scatter_state", &scatter_state);
+  m.impl("gather_slots", &gather_slots);
+  m.impl("scatter_slots", &scatter_slots);
+  m.impl("copy_state", &copy_state);
+  m.impl("zero_slots", &zero_slots);
 }
 
 // The state cache policy these kernels pass (LD_CACHE_KEEP / LD_CACHE_STREAM), set from

@@ -31,8 +31,12 @@ Additive ops (no reference counterpart):
   gather_slots / scatter_slots          dtype-generic gather_state / scatter_state, for the
                                         bf16 conv-state pool and any dense-inner pool
 
-Every impl launches on the caller's current stream, allocates nothing and reads no device
-memory on the host, so it can be captured in a HIP graph.
+Every kernel launches on the caller's current stream and reads no device memory on the host,
+so it can be captured in a HIP graph.  None allocates, except prefill's chunked form, which
+keeps one workspace per device and stream for later calls (release_prefill_workspaces frees
+them).  The kernels of every op but prefill are C++ (csrc/torch_ops.cpp,
+liblightdelta_torch.so); the check_* functions below restate their argument checks so they
+can run without a GPU.
 """
 
 from __future__ import annotations
@@ -368,7 +372,7 @@ def check_decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, a, b, a_log
 
 
 # ---------------------------------------------------------------------------------------
-# state-pool copies
+# state-pool copies: the checks of the C++ kernels (csrc/torch_ops.cpp), restated
 # ---------------------------------------------------------------------------------------
 
 
@@ -380,13 +384,6 @@ def _dense_inner(t: torch.Tensor) -> bool:
             return False
         expected *= size
     return True
-
-
-def _row_bytes(t: torch.Tensor) -> int:
-    count = 1
-    for size in t.shape[1:]:
-        count *= size
-    return count * t.element_size()
 
 
 def check_state_layout(pool, slots, packed, *, fp32_4d: bool):
@@ -432,71 +429,6 @@ def _check_valid(valid, slots, pool):
     )
 
 
-def _gather(pool, slots, valid, out):
-    if slots.numel() == 0:
-        return
-    size = pool.element_size()
-    lib = _lib.load()
-    with _DeviceGuard(pool.device):
-        _lib.check(
-            lib.ld_state_gather(
-                pool.data_ptr(),
-                pool.stride(0) * size,
-                slots.data_ptr(),
-                slots.stride(0),
-                valid.data_ptr(),
-                out.data_ptr(),
-                out.stride(0) * size,
-                _row_bytes(pool),
-                slots.numel(),
-                _stream(pool.device),
-            )
-        )
-
-
-def _scatter(packed, slots, pool):
-    if slots.numel() == 0:
-        return
-    size = pool.element_size()
-    lib = _lib.load()
-    with _DeviceGuard(pool.device):
-        _lib.check(
-            lib.ld_state_scatter(
-                packed.data_ptr(),
-                packed.stride(0) * size,
-                slots.data_ptr(),
-                slots.stride(0),
-                pool.data_ptr(),
-                pool.stride(0) * size,
-                _row_bytes(pool),
-                slots.numel(),
-                _stream(pool.device),
-            )
-        )
-
-
-def _gather_state_impl(pool, slots, valid, out):
-    check_state_layout(pool, slots, out, fp32_4d=True)
-    _check_valid(valid, slots, pool)
-    _gather(pool, slots, valid, out)
-
-
-def _scatter_state_impl(packed, slots, pool):
-    check_state_layout(pool, slots, packed, fp32_4d=True)
-    _scatter(packed, slots, pool)
-
-
-def _gather_slots_impl(pool, slots, valid, out):
-    check_state_layout(pool, slots, out, fp32_4d=False)
-    _check_valid(valid, slots, pool)
-    _gather(pool, slots, valid, out)
-
-
-def _scatter_slots_impl(packed, slots, pool):
-    check_state_layout(pool, slots, packed, fp32_4d=False)
-    _scatter(packed, slots, pool)
-
-
 def check_copy(pool, src, dst):
     _require(
         _is_gpu(pool) and pool.dim() >= 1 and _dense_inner(pool),
@@ -508,25 +440,6 @@ def check_copy(pool, src, dst):
             "src and dst must be contiguous CUDA int32 vectors",
         )
     _require(src.numel() == dst.numel(), "src and dst must have the same length")
-
-
-def _copy_state_impl(pool, src, dst):
-    check_copy(pool, src, dst)
-    if src.numel() == 0:
-        return
-    lib = _lib.load()
-    with _DeviceGuard(pool.device):
-        _lib.check(
-            lib.ld_state_copy(
-                pool.data_ptr(),
-                pool.stride(0) * pool.element_size(),
-                src.data_ptr(),
-                dst.data_ptr(),
-                src.numel(),
-                _row_bytes(pool),
-                _stream(pool.device),
-            )
-        )
 
 
 def check_zero(pool, slots):
@@ -541,39 +454,17 @@ def check_zero(pool, slots):
     )
 
 
-def _zero_slots_impl(pool, slots):
-    check_zero(pool, slots)
-    if slots.numel() == 0:
-        return
-    lib = _lib.load()
-    with _DeviceGuard(pool.device):
-        _lib.check(
-            lib.ld_state_zero(
-                pool.data_ptr(),
-                pool.stride(0) * pool.element_size(),
-                slots.data_ptr(),
-                slots.numel(),
-                _row_bytes(pool),
-                _stream(pool.device),
-            )
-        )
-
-
 # ---------------------------------------------------------------------------------------
 # registration
 # ---------------------------------------------------------------------------------------
 
-# decode and decode_conv have C++ kernels (csrc/torch_ops.cpp, liblightdelta_torch.so): their
-# host path is on every decode step.  The other ops' kernels are these Python functions.
-_CXX_KERNELS = ("decode", "decode_conv")
+# The per-step ops have C++ kernels (csrc/torch_ops.cpp, liblightdelta_torch.so): their host
+# path is on every decode step.  prefill's kernel is the Python function below (it keeps the
+# chunked form's workspace cache and the algorithm choice).
+_CXX_KERNELS = ("decode", "decode_conv", "gather_state", "scatter_state", "gather_slots",
+                "scatter_slots", "copy_state", "zero_slots")
 _IMPLS = {
-    "gather_state": _gather_state_impl,
-    "scatter_state": _scatter_state_impl,
-    "copy_state": _copy_state_impl,
-    "zero_slots": _zero_slots_impl,
     "prefill": _prefill_impl,
-    "gather_slots": _gather_slots_impl,
-    "scatter_slots": _scatter_slots_impl,
 }
 
 

@@ -128,6 +128,45 @@ def test_decode_kernel_validation_messages(gpu, mutate, message):
         torch.ops.lightdelta.decode(*args.values())
 
 
+@pytest.mark.gpu
+def test_state_op_kernel_validation_messages(gpu):
+    """The state-pool cases of test_state_io_validation_messages through the ops on the GPU:
+    the C++ kernels (csrc/torch_ops.cpp) raise the same messages, before any launch."""
+    ops_ = torch.ops.lightdelta
+    pool = torch.zeros(8, 4, 128, 128, device=gpu)
+    slots = torch.tensor([1, -1, 3], dtype=torch.int32, device=gpu)
+    valid = torch.ones(3, dtype=torch.bool, device=gpu)
+    packed = torch.zeros(3, 4, 128, 128, device=gpu)
+    ops_.gather_state(pool, slots, valid, packed)
+    ops_.scatter_state(packed, slots, pool)
+    with pytest.raises(RuntimeError, match="pool must be CUDA FP32"):
+        ops_.gather_state(pool.bfloat16(), slots, valid, packed.bfloat16())
+    with pytest.raises(RuntimeError, match="pool must be CUDA FP32"):
+        ops_.scatter_state(packed, slots, torch.zeros(8, 4, 128, 256, device=gpu)[..., :128])
+    with pytest.raises(RuntimeError, match="slots must be a CUDA int32 vector"):
+        ops_.gather_state(pool, slots.long(), valid, packed)
+    with pytest.raises(RuntimeError, match="invalid packed layout"):
+        ops_.scatter_state(packed[:2], slots, pool)
+    with pytest.raises(RuntimeError, match="valid must be a CUDA bool vector"):
+        ops_.gather_state(pool, slots, valid.int(), packed)
+    conv = torch.zeros(8, 4, 8192, dtype=torch.bfloat16, device=gpu)
+    conv_packed = torch.zeros(3, 4, 8192, dtype=torch.bfloat16, device=gpu)
+    ops_.gather_slots(conv, slots, valid, conv_packed)
+    ops_.scatter_slots(conv_packed, slots, conv)
+    with pytest.raises(RuntimeError, match="invalid packed layout"):
+        ops_.gather_slots(conv, slots, valid, torch.zeros(3, 4, 8192, device=gpu))
+    with pytest.raises(RuntimeError, match="same length"):
+        ops_.copy_state(pool, slots, slots[:2].contiguous())
+    with pytest.raises(RuntimeError, match="src and dst must be contiguous CUDA int32 vectors"):
+        ops_.copy_state(pool, slots.long(), slots)
+    ops_.zero_slots(conv, slots)
+    with pytest.raises(RuntimeError, match="slots must be a contiguous CUDA int32 vector"):
+        ops_.zero_slots(pool, slots.long())
+    with pytest.raises(RuntimeError, match="dense inner dimensions"):
+        ops_.zero_slots(torch.zeros(8, 4, 128, 256, device=gpu)[..., :128], slots)
+    torch.cuda.synchronize()
+
+
 def test_cpu_tensors_are_rejected():
     args = decode_args("cpu")
     with pytest.raises(RuntimeError, match="qkv must be CUDA BF16"):
