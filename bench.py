@@ -253,8 +253,9 @@ def conv_fused(case, op_args, steps, device):
     """The step with the causal conv1d (width 4, SiLU, bf16 conv pool of 8192 channels, no
     bias) fused in front, one decode_conv launch per step on the pre-conv activations:
     `hot` (B=32, the same 32 slots, keep policy), `cold` (B=32, 16 disjoint slot sets
-    rotated through 2048-slot SSM and conv pools, stream policy) and `verify` (B=64, T=4
-    speculative verify with a 6-column conv state and random accepted counts, hot)."""
+    rotated through 2048-slot SSM and conv pools, stream policy), `verify_b64_t4` (B=64,
+    T=4 speculative verify with a 6-column conv state and random accepted counts, hot) and
+    `verify_b64_t4_cold` (the same through 8 disjoint slot sets, stream policy)."""
     import torch
 
     from lightdelta_amd import ops
@@ -319,6 +320,30 @@ def conv_fused(case, op_args, steps, device):
             "us_per_step": round(us, 3), "tokens_per_s": round(batch * width * 1e6 / us, 1),
             "TBps": round(v_bytes / us / 1e6, 3), "cache_policy": "keep",
             "accepted": "random in 1..4 per request, conv state of 6 columns"}
+        del v_conv
+
+        # the same verify cache-cold: 8 disjoint slot sets rotated through 2049-slot pools
+        ops.set_state_cache_policy("stream")
+        big = torch.empty(2049, HV, DIM, DIM, device=device).normal_(0.0, 0.02)
+        big_conv = torch.zeros(2049, conv_dim, 3 + width - 1, dtype=torch.bfloat16, device=device)
+        perm = torch.randperm(2048, device=device)[: 8 * batch * width] + 1
+        vsets = [perm[i * batch * width:(i + 1) * batch * width].to(torch.int32).view(batch, width)
+                 for i in range(8)]
+        cold_args = list(v_args)
+        cold_args[pool_at] = big
+
+        def verify_cold_pass():
+            for s in vsets:
+                cold_args[slots_at] = s
+                torch.ops.lightdelta.decode_conv(v["qkv"], big_conv, conv_weight, None,
+                                                 *cold_args, 1e-6)
+
+        us = _graph_us(verify_cold_pass, max(1, steps // 8)) / 8
+        result["verify_b64_t4_cold"] = {
+            "us_per_step": round(us, 3), "tokens_per_s": round(batch * width * 1e6 / us, 1),
+            "TBps": round(v_bytes / us / 1e6, 3), "frac": round(v_bytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "cache_policy": "stream"}
+        del big, big_conv
     finally:
         ops.set_state_cache_policy(saved)
     return result

@@ -216,10 +216,18 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 // cold in-place read-modify-write of 64 KiB per workgroup in this layout runs at 6.26 TB/s
 // as 1024 threads x 4 pieces against 5.63 as 256 x 16 (B=128 tiles at random slots,
 // non-temporal loads, system-scope stores).
+// Waves per SIMD the register allocation aims at: 4 (four 4-wave workgroups per CU, or one
+// 16-wave workgroup for the conv-fused verify, whose conv arguments need the SGPRs that a
+// second one would take: at 8 it spilled 44 of them) or 8 (two 16-wave workgroups).
+constexpr int waves_per_simd(int waves, int conv_cols) {
+  return waves == kWaves || conv_cols > 0 ? 4 : 8;
+}
+
 template <bool DtBf16, bool WBf16, int LoadPol, int StorePol, int Width, int ConvCols,
           int Waves = kWaves, bool Packed = false>
 __global__ __launch_bounds__(64 * Waves)
-__attribute__((amdgpu_waves_per_eu(Waves == kWaves ? 4 : 8, Waves == kWaves ? 4 : 8)))
+__attribute__((amdgpu_waves_per_eu(waves_per_simd(Waves, ConvCols),
+                                   waves_per_simd(Waves, ConvCols))))
 void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
                        const int32_t* md_accepted, int md_num_v_heads, const DecodeParams args) {
   // The request metadata pointers and the head count are kernel arguments of their own, ahead
@@ -240,12 +248,13 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // inputs at once -- by wave 0 once, like tokens 1..W-1, behind one barrier.
   constexpr bool kShared0 = Width > 1 && Waves == 16;
   constexpr int kChunks = kPc / 4;             // chunks of 2 rows per lane (8 per wave)
-  static_assert(Waves == kWaves || (Waves == 16 && !Conv), "16 waves only without the conv");
+  static_assert(Waves == kWaves || Waves == 16, "4 or 16 waves");
   // The conv runs before the tile loads for several tokens or more than 4 state columns;
   // one token with 3..4 columns keeps it in registers while the tile streams in.
   constexpr bool kConvFirst = Conv && (Width > 1 || kCols > 4);
   constexpr bool kConvLate = Conv && !kConvFirst;
   static_assert(!kConvLate || kCols == 4, "the in-flight conv holds 4 state columns");
+  static_assert(!kConvLate || Waves == kWaves, "the in-flight conv runs with 4 waves");
   static_assert(!Packed || (kConvLate && Waves == 4), "the packed conv state: one token, 4 waves");
   // Every kernel argument, then all request metadata, is loaded before the first branch:
   // two dependent scalar round trips (kernel-argument segment; cu/accepted/indices) instead
@@ -382,23 +391,30 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   if constexpr (kConvFirst) {
     // Several tokens (speculative verify), or a long conv state: the conv runs to
     // completion before the tile loads, so its inputs do not compete with the tile for
-    // registers.  The v channels are
-    // this workgroup's alone and are shifted in place (threads 128..255 repeat the stores
-    // of 0..127 with identical bytes); the q/k channels are kept for the end-of-kernel write.
+    // registers.  Threads 0..255 convolve (with 16 waves, waves 4..15 only wait at the
+    // barrier).  The v channels are this workgroup's alone and are shifted in place
+    // (threads 128..255 repeat the stores of 0..127 with identical bytes); the q/k channels
+    // are kept for the end-of-kernel write.
+    const bool convolves = tid < 2 * kDim;   // wave-uniform
     uint16_t qk_new[kCols], v_new[kCols];
-    const bool has_bias = p.conv_bias != nullptr;
-    conv_channel_tokens<Width, kCols>(p, bos, num_tokens, conv_offset, cs_qk_at, conv_qk, has_bias,
-                                      &s_conv[0][tid], qk_new);
-    conv_channel_tokens<Width, kCols>(p, bos, num_tokens, conv_offset, cs_v_at, conv_v, has_bias,
-                                      &s_conv[0][2 * kDim + (tid & (kDim - 1))], v_new);
+    if (convolves) {
+      const bool has_bias = p.conv_bias != nullptr;
+      conv_channel_tokens<Width, kCols>(p, bos, num_tokens, conv_offset, cs_qk_at, conv_qk,
+                                        has_bias, &s_conv[0][tid], qk_new);
+      conv_channel_tokens<Width, kCols>(p, bos, num_tokens, conv_offset, cs_v_at, conv_v,
+                                        has_bias, &s_conv[0][2 * kDim + (tid & (kDim - 1))],
+                                        v_new);
 #pragma unroll
-    for (int k = 0; k < kCols; ++k) s_conv_new[tid][k] = qk_new[k];
+      for (int k = 0; k < kCols; ++k) s_conv_new[tid][k] = qk_new[k];
+    }
     // Every wave has consumed its conv-state reads once past the barrier, so the v channels
     // (read by two threads each) can be overwritten.
     lds_barrier();
+    if (convolves) {
 #pragma unroll
-    for (int k = 0; k < kCols; ++k)
-      p.conv_state[cs_v_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new[k];
+      for (int k = 0; k < kCols; ++k)
+        p.conv_state[cs_v_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new[k];
+    }
     if (p.group > 1 && tid == 0)
       arrived = count_in(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
                          p.group);
@@ -709,8 +725,7 @@ void launch_kernel(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t bl
 template <typename One, typename Verify, typename ConvOne, typename ConvVerify>
 void launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
                    uint32_t blocks, hipStream_t stream) {
-  static_assert(ConvOne::kWaveCount == kWaves && ConvVerify::kWaveCount == kWaves,
-                "the conv-fused kernels run 4 waves");
+  static_assert(ConvOne::kWaveCount == kWaves, "the single-token conv-fused kernel runs 4 waves");
   if (conv) {
     switch (p.width) {
       case 1:  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
@@ -807,14 +822,18 @@ int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, b
   //   verify, stream:    16 waves, non-temporal loads, system-scope stores, one workgroup
   //                      per CU (B=64, T=4 cold: 114.4 us = 5.87 TB/s; two per CU 116.0;
   //                      the keep kernel 120.8).
-  //   conv-fused, one token: 4 waves, plain loads and stores (keep; 22.4 us hot) or
-  //                      non-temporal ones (stream; 28.5 us cold, against 30.0 with
-  //                      system-scope stores); conv-fused verify: 4 waves, plain loads,
-  //                      non-temporal stores.
+  //   conv-fused, one token: 4 waves, plain loads and stores (keep; 21.4 us hot) or
+  //                      non-temporal ones (stream; 28.0 us cold, against 30.0 with
+  //                      system-scope stores).
+  //   conv-fused verify, keep: 4 waves, plain loads, non-temporal stores (B=64, T=4, 6
+  //                      conv columns: 108.3 us hot; 16 waves 112.9).
+  //   conv-fused verify, stream: 16 waves, non-temporal loads and stores, one workgroup
+  //                      per CU (127.9 us cold against 143.3 with the keep kernel, 135.6
+  //                      with system-scope stores, 148.5 with 4 waves).
   const uint32_t n = static_cast<uint32_t>(blocks);
   if (a.cache_policy == LD_CACHE_STREAM)
     launch_decode<Shape<kPolNT, kPolSys, 16>, Shape<kPolNT, kPolSys, 16, true>,
-                  Shape<kPolNT, kPolNT, kWaves>, Shape<kPolPlain, kPolNT, kWaves>>(
+                  Shape<kPolNT, kPolNT, kWaves>, Shape<kPolNT, kPolNT, 16, true>>(
         p, conv, dt_bf16, w_bf16, n, s);
   else
     launch_decode<Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, 16, true>,
