@@ -11,7 +11,7 @@
 //
 // Work decomposition (one workgroup = one (request, v-head) 128x128 fp32 state tile):
 //   * 256 threads = 4 wave64s (16 wave64s for the single-token step under the stream
-//     policy and for the verify steps without the conv).  Inside a wave, the 16 lanes of a
+//     policy and for the verify steps).  Inside a wave, the 16 lanes of a
 //     DPP row span one 512-byte K row: lane kq holds k = 4kq..4kq+3 and 64+4kq..64+4kq+3 (two 16-byte pieces); the 4 DPP rows of the
 //     wave take 4 consecutive V rows.  Wave w's rows are 4w..4w+3 plus multiples of 4 * waves:
 //     a piece pair of all waves covers one contiguous block of the tile (16 rows = 8 KiB with
@@ -151,6 +151,56 @@ __device__ __forceinline__ uint16_t conv_output(uint16_t x, const uint16_t (&sta
 // t < Width (tokens past n use copies of the last input and are discarded by the caller);
 // new_state[k] holds column min(k, len - 1).  Reads nothing out of bounds: every column is
 // clamped to len - 1 and every token to n - 1 when loaded.
+// The inputs of one channel's conv over a verify step: its state columns, the tokens'
+// inputs, weights and bias (the weight array stands in for a missing bias).
+struct ConvIn {
+  Packed8 st, x;
+  uint32_t w[2];
+  uint16_t bias;
+};
+
+// Fills `in` in place: a ConvIn returned by value was left as a private aggregate, which the
+// backend then placed in LDS (96 bytes a thread for the two channels).
+template <int Width, int Cols>
+__device__ __forceinline__ void conv_load(const DecodeParams& p, int64_t bos, int n,
+                                          int64_t state_at, int channel, ConvIn& in) {
+  static_assert(Cols <= 8 && Width <= 4, "packed conv registers hold 8 columns, 4 tokens");
+#pragma unroll
+  for (int j = 0; j < Cols; ++j)
+    in.st.set(j, p.conv_state[state_at + min(j, p.conv_len - 1) * p.conv_len_stride]);
+#pragma unroll
+  for (int t = 0; t < Width; ++t)
+    in.x.set(t, p.conv_x[(bos + min(t, n - 1)) * p.conv_x_row + channel]);
+  const uint32_t* wsrc = reinterpret_cast<const uint32_t*>(p.conv_weight + channel * kConvWidth);
+  in.w[0] = wsrc[0];
+  in.w[1] = wsrc[1];
+  in.bias = (p.conv_bias != nullptr ? p.conv_bias : p.conv_weight)[channel];
+}
+
+// `in` by value, its weights copied into a local array for conv_dot: a reference into the
+// caller's ConvIn kept that aggregate in memory.
+template <int Width, int Cols>
+__device__ __forceinline__ void conv_compute(const ConvIn in, int len, int n, int offset,
+                                             bool has_bias, uint16_t* out,
+                                             uint16_t (&new_state)[Cols]) {
+  const uint32_t w[2] = {in.w[0], in.w[1]};
+  uint16_t seq[3 + Width];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) seq[m] = in.st.get(offset + m);
+#pragma unroll
+  for (int t = 0; t < Width; ++t) seq[3 + t] = in.x.get(t);
+#pragma unroll
+  for (int t = 0; t < Width; ++t)
+    out[t * 3 * kDim] = conv_dot(seq[t], seq[t + 1], seq[t + 2], seq[t + 3], w, in.bias,
+                                 has_bias);
+  const int kept = len - n;  // state columns that survive (<= 0: none)
+#pragma unroll
+  for (int k = 0; k < Cols; ++k) {
+    const int col = min(k, len - 1);
+    new_state[k] = col < kept ? in.st.get(offset + 1 + col) : in.x.get(col - kept);
+  }
+}
+
 template <int Width, int Cols>
 __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64_t bos, int n,
                                                     int offset, int64_t state_at, int channel,
@@ -212,7 +262,7 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 // column (B=32, 3 columns: 22.04 -> 21.41 us, bit-identical results).
 //
 // Waves: 4 (32 V rows and 16 tile pieces per wave), or 16 (8 rows, 4 pieces) for the
-// single-token step under the stream policy and for every verify step without the conv.  A
+// single-token step under the stream policy and for every verify step.  A
 // cold in-place read-modify-write of 64 KiB per workgroup in this layout runs at 6.26 TB/s
 // as 1024 threads x 4 pieces against 5.63 as 256 x 16 (B=128 tiles at random slots,
 // non-temporal loads, system-scope stores).
@@ -251,8 +301,11 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   static_assert(Waves == kWaves || Waves == 16, "4 or 16 waves");
   // The conv runs before the tile loads for several tokens or more than 4 state columns;
   // one token with 3..4 columns keeps it in registers while the tile streams in.
-  constexpr bool kConvFirst = Conv && (Width > 1 || kCols > 4);
-  constexpr bool kConvLate = Conv && !kConvFirst;
+  // The conv of a verify step with 16 waves: its inputs load before the tile, the arithmetic
+  // runs while the tile streams in (16 waves leave the registers for both).
+  constexpr bool kConvSplit = Conv && Width > 1 && Waves == 16;
+  constexpr bool kConvFirst = Conv && (Width > 1 || kCols > 4) && !kConvSplit;
+  constexpr bool kConvLate = Conv && !kConvFirst && !kConvSplit;
   static_assert(!kConvLate || kCols == 4, "the in-flight conv holds 4 state columns");
   static_assert(!kConvLate || Waves == kWaves, "the in-flight conv runs with 4 waves");
   static_assert(!Packed || (kConvLate && Waves == 4), "the packed conv state: one token, 4 waves");
@@ -286,7 +339,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // The step's arguments too -- except where the conv runs to completion before the tile
   // loads (several tokens, or a long conv state): those have no loads to get ahead of, and
   // holding every argument through the conv would exceed the 102 SGPRs.
-  if constexpr (!kConvFirst) {
+  if constexpr (!kConvFirst && !kConvSplit) {
     if constexpr (!Conv) {  // the conv variant reads its activations from conv_x
       pin_sgpr(p.qkv);
       pin_sgpr(p.qkv_row);
@@ -371,8 +424,11 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // Conv variant: this thread convolves q/k channel `conv_qk` and (tid < 128) v channel
   // `conv_v`; it loads their input, conv-state columns (clamped to the last column past
   // conv_len, so every load is in bounds), weights and bias.
-  const int conv_qk = tid < kDim ? q_col + tid : k_col + (tid - kDim);
-  const int conv_v = v_col + (tid & (kDim - 1));
+  // (with 16 waves, threads 256.. take the channels of threads tid & 255: their loads are
+  // the same as those threads', so every wave issues the same loads)
+  const int ctid = tid & (2 * kDim - 1);
+  const int conv_qk = ctid < kDim ? q_col + ctid : k_col + (ctid - kDim);
+  const int conv_v = v_col + (ctid & (kDim - 1));
   const int64_t conv_slot_at = static_cast<int64_t>(slot[0]) * p.conv_slot;
   int64_t cs_qk_at = conv_slot_at + conv_qk * p.conv_dim_stride;
   int64_t cs_v_at = conv_slot_at + conv_v * p.conv_dim_stride;
@@ -380,6 +436,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   uint16_t cs_qk_raw[kConvLate ? 4 : 1], cs_v_raw[kConvLate ? 4 : 1];
   uint32_t cw_qk[2], cw_v[2];
   uint32_t arrived = 0;  // ticket count before this workgroup's increment (thread 0)
+  ConvIn ci_qk, ci_v;    // kConvSplit: the conv inputs, loaded ahead of the tile
   // Packed: the wave's first q/k and v channel (waves 0, 1: q channels 0..63, 64..127;
   // waves 2, 3: the k channels; the v channels of waves 2, 3 repeat those of 0, 1), and the
   // lane's 16-byte piece of a 128 * len-byte run (lanes past its 8 * len pieces repeat the
@@ -395,7 +452,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     // barrier).  The v channels are this workgroup's alone and are shifted in place
     // (threads 128..255 repeat the stores of 0..127 with identical bytes); the q/k channels
     // are kept for the end-of-kernel write.
-    const bool convolves = tid < 2 * kDim;   // wave-uniform
+    const bool convolves = Waves == kWaves || tid < 2 * kDim;   // wave-uniform
     uint16_t qk_new[kCols], v_new[kCols];
     if (convolves) {
       const bool has_bias = p.conv_bias != nullptr;
@@ -420,6 +477,9 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
                          p.group);
     in0.a = p.a[static_cast<int64_t>(bos) * p.a_row + head];
     in0.b = p.b[static_cast<int64_t>(bos) * p.b_row + head];
+  } else if constexpr (kConvSplit) {
+    conv_load<Width, kCols>(p, bos, num_tokens, cs_qk_at, conv_qk, ci_qk);
+    conv_load<Width, kCols>(p, bos, num_tokens, cs_v_at, conv_v, ci_v);
   } else if constexpr (kConvLate) {
     const uint16_t* xrow = p.conv_x + static_cast<int64_t>(bos) * p.conv_x_row;
     cx_qk = xrow[conv_qk];
@@ -461,11 +521,26 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   const int64_t token_w = bos + min(wave, num_tokens - 1);
   TokenIn inw;
   uint16_t vw_hi = 0;
-  if constexpr (Conv && Width > 1) {  // post-conv token from LDS (ready: barrier above)
+  // post-conv token from LDS, for the split conv (in the staging below, after its barrier)
+  auto conv_token_w = [&]() {
+    const uint16_t* conv_w = s_conv[min(wave, num_tokens - 1)];
+    const TokenIn t = conv_token(conv_w, kq);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      inw.q[e] = t.q[e];
+      inw.k[e] = t.k[e];
+    }
+    inw.v = conv_w[2 * kDim + 2 * lane];
+    vw_hi = conv_w[2 * kDim + 2 * lane + 1];
+  };
+  if constexpr (Conv && Width > 1 && !kConvSplit) {  // post-conv token from LDS (barrier above)
     const uint16_t* conv_w = s_conv[min(wave, num_tokens - 1)];
     inw = conv_token(conv_w, kq);
     inw.v = conv_w[2 * kDim + 2 * lane];
     vw_hi = conv_w[2 * kDim + 2 * lane + 1];
+    inw.a = p.a[token_w * p.a_row + head];
+    inw.b = p.b[token_w * p.b_row + head];
+  } else if constexpr (kConvSplit) {
     inw.a = p.a[token_w * p.a_row + head];
     inw.b = p.b[token_w * p.b_row + head];
   } else if (Width > 1) {
@@ -500,6 +575,30 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   }
 
   // ---- staging, while the tile streams in ----
+  if constexpr (kConvSplit) {
+    const bool convolves = tid < 2 * kDim;   // wave-uniform
+    uint16_t qk_new[kCols], v_new[kCols];
+    if (convolves) {
+      const bool has_bias = p.conv_bias != nullptr;
+      conv_compute<Width, kCols>(ci_qk, p.conv_len, num_tokens, conv_offset, has_bias,
+                                 &s_conv[0][tid], qk_new);
+      conv_compute<Width, kCols>(ci_v, p.conv_len, num_tokens, conv_offset, has_bias,
+                                 &s_conv[0][2 * kDim + (tid & (kDim - 1))], v_new);
+#pragma unroll
+      for (int k = 0; k < kCols; ++k) s_conv_new[tid][k] = qk_new[k];
+    }
+    // conv outputs visible to every wave; every conv-state read of the workgroup consumed
+    lds_barrier();
+    if (convolves) {
+#pragma unroll
+      for (int k = 0; k < kCols; ++k)
+        p.conv_state[cs_v_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new[k];
+    }
+    if (p.group > 1 && tid == 0)
+      arrived = count_in(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
+                         p.group);
+    conv_token_w();
+  }
   if constexpr (kConvLate) {
     const int len = p.conv_len;
     const bool has_bias = p.conv_bias != nullptr;
@@ -706,47 +805,64 @@ struct Shape {
   static constexpr bool kSolo = Solo;
 };
 constexpr size_t kSoloLds = 96 * 1024;
+constexpr size_t kLdsPerWorkgroup = 160 * 1024;
 
-template <typename S, int Width, int ConvCols, bool Packed = false>
-void launch_kernel(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
-                   hipStream_t stream) {
+// Whether `kernel`'s static LDS plus `dynamic` bytes fit a workgroup (checked once per kernel
+// on the host: an oversized request is not a launch error but a queue abort).
+template <typename Kernel>
+bool lds_fits(Kernel kernel, size_t dynamic) {
+  hipFuncAttributes attr{};
+  return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) == hipSuccess &&
+         attr.sharedSizeBytes + dynamic <= kLdsPerWorkgroup;
+}
+
+template <typename S, int Width, int ConvCols, bool Packed, bool DtBf16, bool WBf16>
+int launch_one(const DecodeParams& p, uint32_t blocks, hipStream_t stream) {
   constexpr int LP = S::kLoad, SP = S::kStore, W = S::kWaveCount;
-  auto kernel =
-      dt_bf16 ? (w_bf16 ? gdn_decode_kernel<true, true, LP, SP, Width, ConvCols, W, Packed>
-                        : gdn_decode_kernel<true, false, LP, SP, Width, ConvCols, W, Packed>)
-              : (w_bf16 ? gdn_decode_kernel<false, true, LP, SP, Width, ConvCols, W, Packed>
-                        : gdn_decode_kernel<false, false, LP, SP, Width, ConvCols, W, Packed>);
+  const auto kernel = gdn_decode_kernel<DtBf16, WBf16, LP, SP, Width, ConvCols, W, Packed>;
+  if constexpr (S::kSolo) {
+    static const bool fits = lds_fits(kernel, kSoloLds);
+    if (!fits)
+      return fail(LD_ERR_LAUNCH, "decode kernel: static LDS plus the one-workgroup-per-CU "
+                                 "request exceed a workgroup's 160 KiB");
+  }
   hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * W), S::kSolo ? kSoloLds : 0, stream,
                      p.indices, p.cu, p.accepted, p.num_v_heads, p);
+  return LD_OK;
+}
+
+template <typename S, int Width, int ConvCols, bool Packed = false>
+int launch_kernel(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blocks,
+                  hipStream_t stream) {
+  return dt_bf16 ? (w_bf16 ? launch_one<S, Width, ConvCols, Packed, true, true>(p, blocks, stream)
+                           : launch_one<S, Width, ConvCols, Packed, true, false>(p, blocks, stream))
+                 : (w_bf16 ? launch_one<S, Width, ConvCols, Packed, false, true>(p, blocks, stream)
+                           : launch_one<S, Width, ConvCols, Packed, false, false>(p, blocks, stream));
 }
 
 // One cache policy: the shapes of the single-token step (One), of verify steps (Verify), and
 // of the conv-fused single-token (ConvOne) and verify (ConvVerify) steps, which run 4 waves.
 template <typename One, typename Verify, typename ConvOne, typename ConvVerify>
-void launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
-                   uint32_t blocks, hipStream_t stream) {
+int launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
+                  uint32_t blocks, hipStream_t stream) {
   static_assert(ConvOne::kWaveCount == kWaves, "the single-token conv-fused kernel runs 4 waves");
   if (conv) {
     switch (p.width) {
       case 1:  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
         if (p.conv_len <= 4 && p.conv_packed)
-          launch_kernel<ConvOne, 1, 4, true>(p, dt_bf16, w_bf16, blocks, stream);
-        else if (p.conv_len <= 4)
-          launch_kernel<ConvOne, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
-        else
-          launch_kernel<ConvOne, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
-        break;
-      case 2: launch_kernel<ConvVerify, 2, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
-      case 3: launch_kernel<ConvVerify, 3, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
-      default: launch_kernel<ConvVerify, 4, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream); break;
+          return launch_kernel<ConvOne, 1, 4, true>(p, dt_bf16, w_bf16, blocks, stream);
+        if (p.conv_len <= 4) return launch_kernel<ConvOne, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
+        return launch_kernel<ConvOne, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
+      case 2: return launch_kernel<ConvVerify, 2, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
+      case 3: return launch_kernel<ConvVerify, 3, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
+      default: return launch_kernel<ConvVerify, 4, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
     }
-    return;
   }
   switch (p.width) {
-    case 1: launch_kernel<One, 1, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 2: launch_kernel<Verify, 2, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
-    case 3: launch_kernel<Verify, 3, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
-    default: launch_kernel<Verify, 4, 0>(p, dt_bf16, w_bf16, blocks, stream); break;
+    case 1: return launch_kernel<One, 1, 0>(p, dt_bf16, w_bf16, blocks, stream);
+    case 2: return launch_kernel<Verify, 2, 0>(p, dt_bf16, w_bf16, blocks, stream);
+    case 3: return launch_kernel<Verify, 3, 0>(p, dt_bf16, w_bf16, blocks, stream);
+    default: return launch_kernel<Verify, 4, 0>(p, dt_bf16, w_bf16, blocks, stream);
   }
 }
 
@@ -825,20 +941,22 @@ int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, b
   //   conv-fused, one token: 4 waves, plain loads and stores (keep; 21.4 us hot) or
   //                      non-temporal ones (stream; 28.0 us cold, against 30.0 with
   //                      system-scope stores).
-  //   conv-fused verify, keep: 4 waves, plain loads, non-temporal stores (B=64, T=4, 6
-  //                      conv columns: 108.3 us hot; 16 waves 112.9).
-  //   conv-fused verify, stream: 16 waves, non-temporal loads and stores, one workgroup
-  //                      per CU (127.9 us cold against 143.3 with the keep kernel, 135.6
-  //                      with system-scope stores, 148.5 with 4 waves).
+  //   conv-fused verify, either: 16 waves, the conv's inputs loaded ahead of the tile,
+  //                      plain loads, non-temporal stores, one workgroup per CU (B=64, T=4,
+  //                      6 conv columns: 105.5 us hot, 127.4 cold, against 108.8 and 143.2
+  //                      with 4 waves and the conv run before the tile loads; non-temporal
+  //                      loads 128.9 and 129.0).
   const uint32_t n = static_cast<uint32_t>(blocks);
+  int rc;
   if (a.cache_policy == LD_CACHE_STREAM)
-    launch_decode<Shape<kPolNT, kPolSys, 16>, Shape<kPolNT, kPolSys, 16, true>,
-                  Shape<kPolNT, kPolNT, kWaves>, Shape<kPolNT, kPolNT, 16, true>>(
+    rc = launch_decode<Shape<kPolNT, kPolSys, 16>, Shape<kPolNT, kPolSys, 16, true>,
+                       Shape<kPolNT, kPolNT, kWaves>, Shape<kPolPlain, kPolNT, 16, true>>(
         p, conv, dt_bf16, w_bf16, n, s);
   else
-    launch_decode<Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, 16, true>,
-                  Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, kWaves>>(
+    rc = launch_decode<Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, 16, true>,
+                       Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, 16, true>>(
         p, conv, dt_bf16, w_bf16, n, s);
+  if (rc != LD_OK) return rc;
   return check_launch(conv ? "ld_gdn_decode_conv" : "ld_gdn_decode");
 }
 
