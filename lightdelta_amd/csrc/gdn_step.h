@@ -175,7 +175,9 @@ __device__ __forceinline__ f32x4 load_tile_piece(const char* tile, uint32_t offs
 // row0 + PairRows, whose v values are v0 and v1):
 //   S <- decay*S ; delta = (v - S k^) * beta ; S += delta k^ ; raw = bf16(S q^)
 // The updated pieces go to `dst` and the two rows' raw outputs to LDS (one lane per row).
-template <int C, int PairRows = 4, int N = kPieces, typename Dst>
+// RoundOut = false leaves S q^ unrounded there, for a reader that rounds it to bf16 itself
+// (the same bits, and no rounding in the token's chain).
+template <int C, int PairRows = 4, int N = kPieces, bool RoundOut = true, typename Dst>
 __device__ __forceinline__ void chunk_step(f32x4 (&s)[N], const Vectors& x, float v0,
                                            float v1, float* o, float decay, float beta,
                                            int kq, int row0, const Dst& dst,
@@ -201,8 +203,8 @@ __device__ __forceinline__ void chunk_step(f32x4 (&s)[N], const Vectors& x, floa
   float out1 = dot8(s[j0 + 2], s[j0 + 3], x.q0, x.q1);
   row_sum2(out0, out1);
   if (kq == 0) {
-    o[row0] = round_bf16(out0);
-    o[row0 + PairRows] = round_bf16(out1);
+    o[row0] = RoundOut ? round_bf16(out0) : out0;
+    o[row0 + PairRows] = RoundOut ? round_bf16(out1) : out1;
   }
 }
 

@@ -13,8 +13,9 @@
 //   Chunks < 4: every wave writes its rows' raw outputs (rounded to bf16, the reference's
 //   rounding point before the norm) to `out`; prefill_norm_kernel applies the gated RMSNorm
 //   in place afterwards, with the epilogue's arithmetic.
-// The next token's inputs are prefetched.  Three to four waves per SIMD: the token loop
-// keeps them in flight on top of the tile, which does not fit 128 VGPRs without spills.
+// The next token's inputs are prefetched.  Four waves per SIMD: the tile, the token in
+// flight and the staged one fit 128 VGPRs, with the rounding of raw outputs to bf16 left to
+// their readers and the token fetch addressed from a uniform row start.
 //
 // Also here: the gated-RMSNorm pass over raw outputs (prefill_norm_kernel, used by the
 // row-split kernels and the chunked form) and the prefill entry points of the C ABI, which
@@ -29,7 +30,7 @@ namespace {
 constexpr int kPrefillGroup = 4;
 
 template <bool DtBf16, bool WBf16, int Chunks>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 4)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void gdn_prefill_kernel(const DecodeParams args) {
   static_assert(Chunks == 1 || Chunks == 2 || Chunks == 4, "8, 16 or 32 rows per wave");
   constexpr int kBlocks = 4 / Chunks;         // workgroups per (sequence, head)
@@ -63,7 +64,9 @@ void gdn_prefill_kernel(const DecodeParams args) {
   __shared__ float s_o[Chunks == 4 ? 2 : 1][Chunks == 4 ? kPrefillGroup : kWaves]
                       [Chunks == 4 ? kDim : kWaveRows];
 
-  const float dt_bias = load_param(p.dt_bias, head, DtBf16);
+  // uniform: kept in an SGPR (a bf16 load would leave it in a VGPR)
+  const float dt_bias = __int_as_float(
+      __builtin_amdgcn_readfirstlane(__float_as_int(load_param(p.dt_bias, head, DtBf16))));
   const float a_log = p.a_log[head];
   float w[2];
 #pragma unroll
@@ -83,59 +86,87 @@ void gdn_prefill_kernel(const DecodeParams args) {
     for (int j = 0; j < kTilePieces; ++j) s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
+  // One token: stage it, fetch the inputs of token t + 1 (of the last token again past the
+  // end: an unconditional fetch needs no merge of old and new values), apply it to the tile
+  // and leave its raw outputs (unrounded) in the group's slot i.
+  const int last = eos - 1;
+  // load_token's values, addressed from the uniform row start with 32-bit lane offsets
+  const uint32_t q_bytes = static_cast<uint32_t>(q_col + kq * 4) * 2u;
+  const uint32_t k_bytes = static_cast<uint32_t>(k_col + kq * 4) * 2u;
+  const uint32_t v_bytes = static_cast<uint32_t>(v_lane) * 2u;
+  auto fetch = [&](int64_t token) __attribute__((always_inline)) {
+    const char* row = reinterpret_cast<const char*>(p.qkv + token * p.qkv_row);
+    auto u16 = [row](uint32_t offset) __attribute__((always_inline)) {
+      return static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(row + offset));
+    };
+    TokenIn in;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t off = e * 128u;
+      in.q[2 * e] = u16(q_bytes + off) | (u16(q_bytes + off + 2) << 16);
+      in.q[2 * e + 1] = u16(q_bytes + off + 4) | (u16(q_bytes + off + 6) << 16);
+      in.k[2 * e] = u16(k_bytes + off) | (u16(k_bytes + off + 2) << 16);
+      in.k[2 * e + 1] = u16(k_bytes + off + 4) | (u16(k_bytes + off + 6) << 16);
+    }
+    in.v = static_cast<uint16_t>(u16(v_bytes));
+    in.a = p.a[token * p.a_row + head];
+    in.b = p.b[token * p.b_row + head];
+    return in;
+  };
   TokenIn next;  // inputs of the next token
-  if (bos < eos) next = load_token(p, bos, q_col, k_col, v_lane, head, kq);
+  if (bos < eos) next = fetch(bos);
   int buf = 0;
-  for (int g0 = bos; g0 < eos; g0 += kPrefillGroup, buf ^= 1) {
-    // gate of the token whose epilogue this wave runs after the group (one workgroup per head)
+  auto token_step = [&](int t, int i) __attribute__((always_inline)) {
+    const TokenIn in = next;
+    next = fetch(min(t + 1, last));
+    const Staged x = stage_token(in, a_log, dt_bias, p.scale);
+    if (lane < kWaveRows) s_v[wave][lane] = bf16_to_f32(in.v);
+    // s_v (and s_o below) are read back by other lanes of this wave: a wave's LDS
+    // operations run in program order, so only the compiler must not reorder them.
+    asm volatile("" ::: "memory");
+    Vectors vec;
+    vec.q0 = x.q0;
+    vec.q1 = x.q1;
+    vec.k0 = x.k0;
+    vec.k1 = x.k1;
+    // output rows: absolute in the per-group buffer, wave-relative in the per-wave one
+    float* o = Chunks == 4 ? s_o[buf][i] : s_o[0][wave];
+    const int orow = Chunks == 4 ? row_base : rsub;
+#define LD_PREFILL_CHUNK(C)                                                                    \
+  if constexpr ((C) < Chunks)                                                                  \
+    chunk_step<C, 4, kTilePieces, false>(s, vec, s_v[wave][8 * (C) + rsub],                     \
+                                         s_v[wave][8 * (C) + 4 + rsub], o, x.decay, x.beta,    \
+                                         kq, orow + 8 * (C), NoStore{}, lane_bytes);
+    LD_PREFILL_CHUNK(0)
+    LD_PREFILL_CHUNK(1)
+    LD_PREFILL_CHUNK(2)
+    LD_PREFILL_CHUNK(3)
+#undef LD_PREFILL_CHUNK
+    asm volatile("" ::: "memory");
+    if constexpr (Chunks < 4) {  // raw outputs of the wave's rows, rounded to bf16
+      if (lane < kWaveRows)
+        p.out[(static_cast<int64_t>(t) * p.num_v_heads + head) * kDim + wave_row0 + lane] =
+            f32_to_bf16(s_o[0][wave][lane]);
+    }
+  };
+  // A group of tokens: gate loads for the epilogue, the tokens, then (one workgroup per
+  // head) the gated RMSNorm epilogue of the group's token `wave` after one barrier.
+  auto group = [&](int g0, auto&& tokens) __attribute__((always_inline)) {
     uint16_t gh[2] = {0, 0};
     if constexpr (Chunks == 4) {
-      const int64_t etoken = min(g0 + wave, eos - 1);
+      const int64_t etoken = min(g0 + wave, last);
 #pragma unroll
       for (int e = 0; e < 2; ++e) gh[e] = p.gate[etoken * p.gate_row + head * kDim + 2 * lane + e];
     }
-    for (int i = 0; i < kPrefillGroup && g0 + i < eos; ++i) {
-      const int t = g0 + i;
-      const TokenIn in = next;
-      if (t + 1 < eos) next = load_token(p, t + 1, q_col, k_col, v_lane, head, kq);
-      const Staged x = stage_token(in, a_log, dt_bias, p.scale);
-      if (lane < kWaveRows) s_v[wave][lane] = bf16_to_f32(in.v);
-      // s_v (and s_o below) are read back by other lanes of this wave: a wave's LDS
-      // operations run in program order, so only the compiler must not reorder them.
-      asm volatile("" ::: "memory");
-      Vectors vec;
-      vec.q0 = x.q0;
-      vec.q1 = x.q1;
-      vec.k0 = x.k0;
-      vec.k1 = x.k1;
-      // output rows: absolute in the per-group buffer, wave-relative in the per-wave one
-      float* o = Chunks == 4 ? s_o[buf][i] : s_o[0][wave];
-      const int orow = Chunks == 4 ? row_base : rsub;
-#define LD_PREFILL_CHUNK(C)                                                                    \
-  if constexpr ((C) < Chunks)                                                                  \
-    chunk_step<C, 4, kTilePieces>(s, vec, s_v[wave][8 * (C) + rsub],                            \
-                               s_v[wave][8 * (C) + 4 + rsub], o, x.decay, x.beta, kq,          \
-                               orow + 8 * (C), NoStore{}, lane_bytes);
-      LD_PREFILL_CHUNK(0)
-      LD_PREFILL_CHUNK(1)
-      LD_PREFILL_CHUNK(2)
-      LD_PREFILL_CHUNK(3)
-#undef LD_PREFILL_CHUNK
-      asm volatile("" ::: "memory");
-      if constexpr (Chunks < 4) {  // raw outputs of the wave's rows (bf16-exact values)
-        if (lane < kWaveRows)
-          p.out[(static_cast<int64_t>(t) * p.num_v_heads + head) * kDim + wave_row0 + lane] =
-              f32_to_bf16(s_o[0][wave][lane]);
-      }
-    }
+    tokens();
     if constexpr (Chunks == 4) {
       lds_barrier();  // the group's raw outputs are complete
-      if (g0 + wave < eos) {  // gated RMSNorm epilogue of the group's token `wave`
+      if (g0 + wave < eos) {
         float raw[2];
         float ss = 0.0f;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          raw[e] = s_o[buf][wave][2 * lane + e];
+          raw[e] = round_bf16(s_o[buf][wave][2 * lane + e]);
           ss = fmaf(raw[e], raw[e], ss);
         }
         ss = wave_sum(ss);
@@ -147,7 +178,20 @@ void gdn_prefill_kernel(const DecodeParams args) {
               f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(bf16_to_f32(gh[e])));
       }
     }
-  }
+    buf ^= 1;
+  };
+  // Whole groups first, then the partial last group (as alternatives inside one loop the two
+  // paths would need different register assignments of the tile).
+  int g0 = bos;
+  for (; g0 + kPrefillGroup <= eos; g0 += kPrefillGroup)
+    group(g0, [&]() __attribute__((always_inline)) {
+#pragma unroll 1  // unrolled, the tokens' fetches move up and spill registers
+      for (int i = 0; i < kPrefillGroup; ++i) token_step(g0 + i, i);
+    });
+  if (g0 < eos)
+    group(g0, [&]() __attribute__((always_inline)) {
+      for (int i = 0; g0 + i < eos; ++i) token_step(g0 + i, i);
+    });
 
   if (slot > 0) {  // the state after the last token (the initial one for an empty sequence)
     char* dst_tile = reinterpret_cast<char*>(p.state + static_cast<int64_t>(slot) * p.state_slot +
@@ -260,11 +304,11 @@ void gdn_prefill_rows_kernel(const DecodeParams args) {
     vec.k0 = now.k0;
     vec.k1 = now.k1;
     float* o = s_o[wave];
-    chunk_step<0, 4, kTilePieces>(s, vec, vv[0], vv[1], o, now.decay, now.beta, kq, rsub,
-                               NoStore{}, lane_bytes);
+    chunk_step<0, 4, kTilePieces, false>(s, vec, vv[0], vv[1], o, now.decay, now.beta, kq, rsub,
+                                         NoStore{}, lane_bytes);
     if constexpr (Chunks == 2)
-      chunk_step<1, 4, kTilePieces>(s, vec, vv[2], vv[3], o, now.decay, now.beta, kq, rsub + 8,
-                                 NoStore{}, lane_bytes);
+      chunk_step<1, 4, kTilePieces, false>(s, vec, vv[2], vv[3], o, now.decay, now.beta, kq,
+                                           rsub + 8, NoStore{}, lane_bytes);
     // s_o is read back by other lanes of this wave: a wave's LDS operations run in program
     // order, so only the compiler must not reorder them.
     asm volatile("" ::: "memory");
