@@ -51,7 +51,9 @@ constexpr int kC = 64;                          // tokens per chunk
 //   misc [0] exp(G_n-1); [64 + i] sq_i = rq_i scale exp(G_i); [128 + j] ck_j = rk_j exp(G_n-1 - G_j)
 // with rq, rk the inverse L2 norms; rows past the chunk's end hold zeros.  So the scan's
 // operands are Qg = diag(sq) Qr (applied to the product's rows) and Kd = diag(ck) Kr
-// (applied to V_new's rows in the update).
+// (applied to V_new's rows in the update).  Qr and Kr depend on the k-head alone: only the
+// record of a group's first v-head holds them (the others leave that space unwritten), and
+// the scans of all the group's v-heads read them there.
 constexpr int64_t kOffW = 0;
 constexpr int64_t kOffU = kOffW + kC * kDim;
 constexpr int64_t kOffP = kOffU + kDim * kC;
@@ -164,7 +166,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // I + A's diagonal blocks, the substitution for W and U, and the v-head's record.  (One
 // workgroup per (chunk, v-head) recomputed the q/k part for every v-head of a group: with
 // 16 qk / 32 v heads, about a third of each workgroup's lifetime.)
-template <bool DtBf16>
+// Wide: qkv rows at 16-byte alignment, so q, k and v come in 16-byte pieces (8 bf16 of one
+// row) instead of one or two bf16 per load: a quarter of the q / k loads and an eighth of
+// the v loads, v then transposed through LDS.  Same values, same arithmetic.
+template <bool DtBf16, bool Wide>
 __global__ __launch_bounds__(kPrepThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
                        const int32_t* chunk_start, int records) {
@@ -182,32 +187,154 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 
   constexpr int kHRow = kDim + 8;  // padded LDS row of the bf16 q / k (272 bytes)
   constexpr int kRow = kDim + 4;   // padded LDS row of W (floats)
-  constexpr int kARow = kC + 4;    // padded LDS row of -A and P
+  constexpr int kARow = kC + 4;    // padded LDS row of -A
   constexpr int kTRow = 20;        // padded LDS row of a diagonal block's inverse
-  // q and k (the bf16 inputs, [64][136] each) for the whole workgroup; per v-head, -A and P
-  // ([64][68] fp32 each), then W ([64][132] fp32) in their place on its way to the
-  // workspace; the four inverses [4][16][20] have their own 5 KiB.
+  constexpr int kVCol = kC / 2 + 2;  // padded column of the v staging (token pairs, dwords)
+  // q and k (the bf16 inputs, [64][136] each) for the whole workgroup; per v-head, -A
+  // ([64][68] fp32) and above it (Wide) the U waves' v, column-major ([128][68] bf16, while
+  // they form U's right-hand side), then W ([64][132] fp32) in their place on its way to
+  // the workspace; the four inverses [4][16][20] have their own 5 KiB.
   constexpr int kHalfBytes = kC * kHRow * 2;
   constexpr int kApBytes = 2 * kC * kARow * 4;
-  static_assert(kC * kRow * 4 <= kApBytes, "LDS plan");
+  static_assert(kC * kRow * 4 <= kApBytes && kDim * kVCol * 4 <= kApBytes / 2, "LDS plan");
   __shared__ __attribute__((aligned(16))) uint8_t sQk[2 * kHalfBytes];
   __shared__ __attribute__((aligned(16))) uint8_t sAp[kApBytes];
   __shared__ __attribute__((aligned(16))) float sT[4 * 16 * kTRow];
-  __shared__ float sG[kC];
-  __shared__ float sBeta[kC];
-  __shared__ float sEg[kC];     // exp(G_i)
-  __shared__ float sEk[kC];     // exp(G_n-1 - G_i)
+  // a v-head's gates, double-buffered (v-head m in buffer m & 1): G_i, beta_i, exp(G_i),
+  // exp(G_n-1 - G_i)
+  __shared__ float sGates[2][4][kC];
   __shared__ float sRq[kC];     // rq_i scale (zero past the end)
   __shared__ float sRk[kC];     // rk_i (zero past the end)
   uint16_t (*const sQh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sQk);
   uint16_t (*const sKh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sQk + kHalfBytes);
   float* const sA = reinterpret_cast<float*>(sAp);
-  float* const sP = reinterpret_cast<float*>(sAp + kApBytes / 2);
   float* const sW = reinterpret_cast<float*>(sAp);
+  uint32_t* const sV = reinterpret_cast<uint32_t*>(sAp + kApBytes / 2);
+
+  // Waves 0-3 solve for W's columns 32w .. 32w + 31, waves 4-7 for U's (2 column tiles
+  // each).
+  constexpr int kNt = 2;   // column tiles per wave
+  const bool solves_u = wave >= 4;
+  const int n0 = (wave & 3) * 16 * kNt;
+
+  // A v-head's global inputs, fetched one v-head ahead (the first with q and k): U's
+  // right-hand side v (U waves) and the gate inputs (wave 0, lane = token).  v comes in the
+  // fragment layout, vr[rb][nt][r] = v of token 16 rb + 4 lg + r, column n0 + 16 nt + li,
+  // or (Wide) as vw[pr][h] = columns n0 + 8 (lane & 3) .. + 7 of token 2 a + h, token pair
+  // a = lane / 4 + 16 pr.
+  uint16_t vr[4][kNt][4];
+  u32x4 vw[2][2];
+  uint16_t gate_a = 0, gate_b = 0;
+  float gate_a_log = 0.0f, gate_dt_bias = 0.0f;
+  auto fetch_v = [&](int head, int li, int lg) __attribute__((always_inline)) {
+    const int v_col = (2 * p.num_k_heads + head) * kDim;
+    if constexpr (Wide) {
+      const int lane = 16 * lg + li;
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int64_t tok = t0 + min(2 * ((lane >> 2) + 16 * pr) + h, len - 1);
+          vw[pr][h] = *reinterpret_cast<const u32x4*>(p.qkv + tok * p.qkv_row + v_col + n0 +
+                                                      8 * (lane & 3));
+        }
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t tok = t0 + min(16 * rb + 4 * lg + r, len - 1);
+          const uint16_t* row = p.qkv + tok * p.qkv_row + v_col + n0 + li;
+#pragma unroll
+          for (int nt = 0; nt < kNt; ++nt) vr[rb][nt][r] = row[16 * nt];
+        }
+    }
+  };
+  auto fetch_gates = [&](int head, int lane) __attribute__((always_inline)) {
+    const int64_t tok = t0 + min(lane, len - 1);
+    gate_a = p.a[tok * p.a_row + head];
+    gate_b = p.b[tok * p.b_row + head];
+    gate_a_log = p.a_log[head];
+    gate_dt_bias = load_param(p.dt_bias, head, DtBf16);
+  };
+  // The gates and the in-chunk cumulative log decay of v-head `member` from the fetched
+  // inputs (one wave, lane = token), then the fetch of the inputs two v-heads on.  Wave 4
+  // computes those of v-head 0 before the q / k barrier and those of v-head m + 1 while
+  // waves 0-3 invert v-head m's diagonal blocks; each is read after at least one barrier.
+  auto gates = [&](int member, int lane) __attribute__((always_inline)) {
+    const int head = key_head * p.group + member;
+    const bool live = lane < len;
+    const float x = bf16_to_f32(gate_a) + gate_dt_bias;
+    const float gl = live ? -__expf(gate_a_log) * softplus(x) : 0.0f;
+    const float beta = live ? sigmoid(bf16_to_f32(gate_b)) : 0.0f;
+    if (member + 1 < p.group) fetch_gates(head + 1, lane);
+    float G = gl;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float up = __shfl_up(G, d);
+      if (lane >= d) G += up;
+    }
+    const float glast = __shfl(G, len - 1);
+    float (*const gb)[kC] = sGates[member & 1];
+    gb[0][lane] = G;
+    gb[1][lane] = beta;
+    gb[2][lane] = __expf(G);
+    gb[3][lane] = __expf(glast - G);
+    if (lane == 0) ws[(static_cast<int64_t>(g) * p.num_v_heads + head) * kRecord + kOffMisc] = __expf(glast);
+  };
+  if (solves_u) fetch_v(key_head * p.group, threadIdx.x & 15, (threadIdx.x >> 4) & 3);
+  if (wave == 4) fetch_gates(key_head * p.group, threadIdx.x & 63);
 
   // q and k of the chunk's tokens and their inverse norms (zero rows past its end); wave w
   // does tokens 8w .. 8w+7, all 8 tokens' loads in flight before the first norm
-  {
+  if constexpr (Wide) {
+    // lane (row quarter, l16) holds elements 8 l16 .. 8 l16 + 7 of tokens 8w + 4h + quarter:
+    // the sum of squares runs in wave_sum's order (a lane's four pairs as four of its lanes
+    // would sum them, then the 16 lanes of the DPP row as its remaining levels)
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15;
+    const int quarter = lane >> 4;
+    u32x4 qv[2], kv[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t tok = t0 + min(wave * kPrepTokens + 4 * h + quarter, len - 1);
+      const uint16_t* row = p.qkv + tok * p.qkv_row;
+      qv[h] = *reinterpret_cast<const u32x4*>(row + q_col + 8 * l16);
+      kv[h] = *reinterpret_cast<const u32x4*>(row + k_col + 8 * l16);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = wave * kPrepTokens + 4 * h + quarter;
+      float pq[4], pk[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float q0 = __builtin_bit_cast(float, qv[h][m] << 16);
+        const float q1 = __builtin_bit_cast(float, qv[h][m] & 0xffff0000u);
+        const float k0 = __builtin_bit_cast(float, kv[h][m] << 16);
+        const float k1 = __builtin_bit_cast(float, kv[h][m] & 0xffff0000u);
+        pq[m] = fmaf(q1, q1, q0 * q0);
+        pk[m] = fmaf(k1, k1, k0 * k0);
+      }
+      float qq = (pq[0] + pq[1]) + (pq[2] + pq[3]);
+      float kk = (pk[0] + pk[1]) + (pk[2] + pk[3]);
+      qq += dpp<kDppQuadXor1>(qq);
+      kk += dpp<kDppQuadXor1>(kk);
+      qq += dpp<kDppQuadXor2>(qq);
+      kk += dpp<kDppQuadXor2>(kk);
+      qq += dpp<kDppRowHalfMirror>(qq);
+      kk += dpp<kDppRowHalfMirror>(kk);
+      qq += dpp<kDppRowMirror>(qq);
+      kk += dpp<kDppRowMirror>(kk);
+      const bool live = i < len;
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(&sQh[i][8 * l16]) = live ? qv[h] : zero;
+      *reinterpret_cast<u32x4*>(&sKh[i][8 * l16]) = live ? kv[h] : zero;
+      if (l16 == 0) {
+        sRq[i] = live ? fast_rsqrt(qq + 1e-6f) * p.scale : 0.0f;
+        sRk[i] = live ? fast_rsqrt(kk + 1e-6f) : 0.0f;
+      }
+    }
+  } else {
     const int lane = threadIdx.x & 63;
     uint32_t qr[kPrepTokens], kr[kPrepTokens];
 #pragma unroll
@@ -235,13 +362,32 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
     }
   }
+  if (wave == 4) gates(0, threadIdx.x & 63);
   __syncthreads();
 
-  // Waves 0-3 solve for W's columns 32w .. 32w + 31, waves 4-7 for U's (2 column tiles
-  // each).
-  constexpr int kNt = 2;   // column tiles per wave
-  const bool solves_u = wave >= 4;
-  const int n0 = (wave & 3) * 16 * kNt;
+  // Qr and Kr (the bf16 inputs in the scan's load order, item = one 16-byte piece) depend on
+  // the k-head alone: they go once, to the record of the group's first v-head, where the
+  // scans of all its v-heads read them
+  {
+    const int tid = threadIdx.x;
+    float* rec0 = ws + (static_cast<int64_t>(g) * p.num_v_heads + key_head * p.group) * kRecord;
+    u32x4* qdst = reinterpret_cast<u32x4*>(rec0 + kOffQr);
+    u32x4* kdst = reinterpret_cast<u32x4*>(rec0 + kOffKr);
+#pragma unroll
+    for (int it = 0; it < kC * kDim / 8 / kPrepThreads; ++it) {
+      const int item = it * kPrepThreads + tid;
+      const int l = item & 63;
+      const int i = 16 * (item >> 8) + (l & 15);
+      const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
+      qdst[item] = *reinterpret_cast<const u32x4*>(&sQh[i][c0]);
+      const int k = 16 * (item >> 7) + (l & 15);
+      const int j = 16 * (l >> 4) + 8 * ((item >> 6) & 1);
+      kdst[item] = u32x4{sKh[j][k] | (static_cast<uint32_t>(sKh[j + 1][k]) << 16),
+                         sKh[j + 2][k] | (static_cast<uint32_t>(sKh[j + 3][k]) << 16),
+                         sKh[j + 4][k] | (static_cast<uint32_t>(sKh[j + 5][k]) << 16),
+                         sKh[j + 6][k] | (static_cast<uint32_t>(sKh[j + 7][k]) << 16)};
+    }
+  }
 
   for (int member = 0; member < p.group; ++member) {
     // The lane coordinates are derived anew in every iteration, through a zero the compiler
@@ -255,44 +401,12 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     const int li = lane & 15;
     const int lg = lane >> 4;
     const int head = key_head * p.group + member;
-    const int v_col = (2 * p.num_k_heads + head) * kDim;
+    const bool next = member + 1 < p.group;
     float* rec = ws + (static_cast<int64_t>(g) * p.num_v_heads + head) * kRecord;
-
-    // U's right-hand side (beta_i v_i) comes from global memory: its loads go out first
-    uint16_t vr[4][kNt][4];   // [row block][column tile][r]
-    if (solves_u) {
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t tok = t0 + min(16 * rb + 4 * lg + r, len - 1);
-          const uint16_t* row = p.qkv + tok * p.qkv_row + v_col + n0 + li;
-#pragma unroll
-          for (int nt = 0; nt < kNt; ++nt) vr[rb][nt][r] = row[16 * nt];
-        }
-    }
-    // gates and the in-chunk cumulative log decay (wave 0, lane = token)
-    if (wave == 0) {
-      const bool live = lane < len;
-      const int64_t tok = t0 + min(lane, len - 1);
-      const float dt_bias = load_param(p.dt_bias, head, DtBf16);
-      const float x = bf16_to_f32(p.a[tok * p.a_row + head]) + dt_bias;
-      const float gl = live ? -__expf(p.a_log[head]) * softplus(x) : 0.0f;
-      const float beta = live ? sigmoid(bf16_to_f32(p.b[tok * p.b_row + head])) : 0.0f;
-      float G = gl;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float up = __shfl_up(G, d);
-        if (lane >= d) G += up;
-      }
-      const float glast = __shfl(G, len - 1);
-      sG[lane] = G;
-      sBeta[lane] = beta;
-      sEg[lane] = __expf(G);
-      sEk[lane] = __expf(glast - G);
-      if (lane == 0) rec[kOffMisc] = __expf(glast);
-    }
-    __syncthreads();
+    const float* const sG = sGates[member & 1][0];
+    const float* const sBeta = sGates[member & 1][1];
+    const float* const sEg = sGates[member & 1][2];
+    const float* const sEk = sGates[member & 1][3];
 
     // A and P tiles of the raw inputs, q_i . k_m and k_i . k_m: bf16 operands with exact
     // products and fp32 accumulation (v_mfma_f32_16x16x32_bf16, lane (li, lg) giving
@@ -308,8 +422,12 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       const uint32_t code = (codes >> (5 * t)) & 31u;
       const int mt = (code >> 2) & 3;
       const int nt = code & 3;
-      const uint16_t* arow = ((code & 16u) ? &sQh[0][0] : &sKh[0][0]) + (16 * mt + li) * kHRow + 8 * lg;
-      const uint16_t* brow = &sKh[0][0] + (16 * nt + li) * kHRow + 8 * lg;
+      // A tiles as K K^T (row tile mt, column tile nt); P tiles transposed, as K Q^T (row
+      // tile nt of K against row tile mt of Q), so that a lane's four results are four
+      // consecutive columns of one row of P: one 16-byte piece of its record layout
+      const bool is_p = (code & 16u) != 0;
+      const uint16_t* arow = &sKh[0][0] + (16 * (is_p ? nt : mt) + li) * kHRow + 8 * lg;
+      const uint16_t* brow = (is_p ? &sQh[0][0] : &sKh[0][0]) + (16 * (is_p ? mt : nt) + li) * kHRow + 8 * lg;
       f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
@@ -324,14 +442,44 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     // (one uniform branch around two straight-line loops)
     f32x4 x[4][kNt];
     if (solves_u) {
+      if constexpr (Wide) {
+        // the wave's 32 columns of v to LDS column by column, a dword per token pair, and
+        // back in the fragment layout (4 tokens of one column per 8-byte read); the wave's
+        // own region, so program order is the only ordering needed
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
+        for (int pr = 0; pr < 2; ++pr) {
+          const int a = (lane >> 2) + 16 * pr;
+          const int c0 = n0 + 8 * (lane & 3);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float beta = sBeta[16 * rb + 4 * lg + r];  // zero past the end
-#pragma unroll
-          for (int nt = 0; nt < kNt; ++nt) x[rb][nt][r] = beta * bf16_to_f32(vr[rb][nt][r]);
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t lo = vw[pr][0][d];
+            const uint32_t hi = vw[pr][1][d];
+            sV[(c0 + 2 * d) * kVCol + a] = (lo & 0xffffu) | (hi << 16);
+            sV[(c0 + 2 * d + 1) * kVCol + a] = (lo >> 16) | (hi & 0xffff0000u);
+          }
         }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+          for (int nt = 0; nt < kNt; ++nt) {
+            const uint2 t4 = *reinterpret_cast<const uint2*>(
+                &sV[(n0 + 16 * nt + li) * kVCol + 8 * rb + 2 * lg]);
+            const uint16_t tv[4] = {static_cast<uint16_t>(t4.x), static_cast<uint16_t>(t4.x >> 16),
+                                    static_cast<uint16_t>(t4.y), static_cast<uint16_t>(t4.y >> 16)};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              x[rb][nt][r] = sBeta[16 * rb + 4 * lg + r] * bf16_to_f32(tv[r]);  // beta: zero past the end
+          }
+      } else {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float beta = sBeta[16 * rb + 4 * lg + r];  // zero past the end
+#pragma unroll
+            for (int nt = 0; nt < kNt; ++nt) x[rb][nt][r] = beta * bf16_to_f32(vr[rb][nt][r]);
+          }
+      }
     } else {
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb)
@@ -345,70 +493,56 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         }
     }
 
-    // Qr and Kr (the bf16 inputs in the scan's load order) and the per-token scales to the
-    // v-head's record (item = one 16-byte piece)
-    {
-      u32x4* qdst = reinterpret_cast<u32x4*>(rec + kOffQr);
-      u32x4* kdst = reinterpret_cast<u32x4*>(rec + kOffKr);
-#pragma unroll
-      for (int it = 0; it < kC * kDim / 8 / kPrepThreads; ++it) {
-        const int item = it * kPrepThreads + tid;
-        const int l = item & 63;
-        const int i = 16 * (item >> 8) + (l & 15);
-        const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
-        qdst[item] = *reinterpret_cast<const u32x4*>(&sQh[i][c0]);
-        const int k = 16 * (item >> 7) + (l & 15);
-        const int j = 16 * (l >> 4) + 8 * ((item >> 6) & 1);
-        kdst[item] = u32x4{sKh[j][k] | (static_cast<uint32_t>(sKh[j + 1][k]) << 16),
-                           sKh[j + 2][k] | (static_cast<uint32_t>(sKh[j + 3][k]) << 16),
-                           sKh[j + 4][k] | (static_cast<uint32_t>(sKh[j + 5][k]) << 16),
-                           sKh[j + 6][k] | (static_cast<uint32_t>(sKh[j + 7][k]) << 16)};
-      }
-      if (tid < kC)
-        rec[kOffMisc + kMiscSq + tid] = sRq[tid] * sEg[tid];
-      else if (tid < 2 * kC)
-        rec[kOffMisc + kMiscCk + tid - kC] = sRk[tid - kC] * sEk[tid - kC];
-    }
+    // the per-token scales to the v-head's record
+    if (tid < kC)
+      rec[kOffMisc + kMiscSq + tid] = sRq[tid] * sEg[tid];
+    else if (tid < 2 * kC)
+      rec[kOffMisc + kMiscCk + tid - kC] = sRk[tid - kC] * sEk[tid - kC];
 
-    // scale the tiles: A (negated) and P to LDS, P zero above the diagonal
+    // scale the tiles: A (negated) to LDS; P straight to the record, where its piece
+    // [row tile mt][q = lg][lane (li, column tile nt)] holds P[16 mt + li][16 nt + 4 lg + r]
+    // (the products are of the raw inputs: q^_i . k^_m = (rq_i scale rk_m) (q_i . k_m))
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
       if (t >= tiles) break;
       const uint32_t code = (codes >> (5 * t)) & 31u;
       const int mt = (code >> 2) & 3;
-      const int m = 16 * (code & 3) + li;
-      const float gm = sG[m];
-      const float rkm = sRk[m];
+      const int nt = code & 3;
+      if (code & 16u) {
+        const int i = 16 * mt + li;
+        const float gi = sG[i];
+        const float rqi = sRq[i];
+        f32x4 piece;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * mt + 4 * lg + r;
-        const float gam = __expf(sG[i] - gm);
-        // the products are of the raw inputs: q^_i . k^_m = (rq_i scale rk_m) (q_i . k_m)
-        if (code & 16u)
-          sP[i * kARow + m] = (m <= i && i < len) ? gam * ((sRq[i] * rkm) * prod[t][r]) : 0.0f;
-        else
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * nt + 4 * lg + r;
+          const float gam = __expf(gi - sG[m]);
+          piece[r] = (m <= i && i < len) ? gam * ((rqi * sRk[m]) * prod[t][r]) : 0.0f;
+        }
+        *reinterpret_cast<f32x4*>(rec + kOffP + ((mt * 4 + lg) * 64 + nt * 16 + li) * 4) = piece;
+      } else {
+        const int m = 16 * nt + li;
+        const float gm = sG[m];
+        const float rkm = sRk[m];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * mt + 4 * lg + r;
+          const float gam = __expf(sG[i] - gm);
           sA[i * kARow + m] = m < i ? -(sBeta[i] * gam * ((sRk[i] * rkm) * prod[t][r])) : 0.0f;
+        }
       }
     }
-    for (int e = tid; e < kC * kC; e += kPrepThreads) {
-      const int i = e >> 6;
-      const int m = e & 63;
-      if ((m >> 4) > (i >> 4)) sP[i * kARow + m] = 0.0f;
+    // P's six tiles above the diagonal, (row tile, column tile) = (0, 1..3), (1, 2..3),
+    // (2, 3): zeros, one 16-byte piece per thread
+    if (tid < 6 * 64) {
+      const int z = tid >> 6;
+      const int mt = z < 3 ? 0 : (z < 5 ? 1 : 2);
+      const int nt = z < 3 ? z + 1 : (z < 5 ? z - 1 : 3);
+      *reinterpret_cast<f32x4*>(rec + kOffP + ((mt * 4 + lg) * 64 + nt * 16 + li) * 4) =
+          f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     __syncthreads();
-
-    // P to the workspace in its load order
-    {
-      f32x4* pdst = reinterpret_cast<f32x4*>(rec + kOffP);
-#pragma unroll
-      for (int it = 0; it < kC * kC / 4 / kPrepThreads; ++it) {
-        const int item = it * kPrepThreads + tid;
-        const int l = item & 63;
-        const int i = 16 * (item >> 8) + (l & 15);
-        const int j = 16 * (l >> 4) + 4 * ((item >> 6) & 3);
-        pdst[item] = *reinterpret_cast<const f32x4*>(sP + i * kARow + j);
-      }
-    }
+    if (wave == 4 && next) gates(member + 1, lane);
     // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
     // (block w by wave w < 4)
     if (wave < 4 && lane < 16) {
@@ -491,6 +625,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         wdst[item] = *reinterpret_cast<const f32x4*>(sW + i * kRow + k4);
       }
     }
+    if (solves_u && next) fetch_v(head + 1, li, lg);
     // the next v-head rewrites the gates, -A, P and W
     __syncthreads();
   }
@@ -526,9 +661,8 @@ struct OutputOperands {
 // gfx9 raw-buffer format) and a 16-byte load at lane offset + uniform offset: the address
 // stays a scalar resource plus one offset register, whatever the compiler's register
 // pressure.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t record_resource(const float* r) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(r), 0,
-                                           static_cast<int>(kRecord * 4), 0x00020000);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t record_resource(const float* r, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(r), 0, bytes, 0x00020000);
 }
 
 // bf16 by the hardware's round-to-nearest-even conversion (v_cvt_pk_bf16_f32): the same
@@ -562,19 +696,19 @@ __device__ __forceinline__ float load4(__amdgpu_buffer_rsrc_t rsrc, int byte_off
 // workgroup's first 16-row tile of U; lg16 = 16 lg (the lane's 4 tokens of ck and sq).
 template <int RT>
 __device__ __forceinline__ void load_state_piece(StateOperands<RT>& o,
-                                                 __amdgpu_buffer_rsrc_t rs, int w,
+                                                 __amdgpu_buffer_rsrc_t rs, int own, int w,
                                                  uint32_t lane16, uint32_t lg16, int tile0,
                                                  int piece) {
   if (piece < 4) {
-    const int wbase = static_cast<int>(kOffW * 4) + w * 8 * 1024;
+    const int wbase = own + static_cast<int>(kOffW * 4) + w * 8 * 1024;
     o.w[piece] = load16(rs, lane16, wbase + piece * 1024);
     o.w[piece + 4] = load16(rs, lane16, wbase + (piece + 4) * 1024);
     if (piece == 0) {
 #pragma unroll
       for (int h = 0; h < RT; ++h)
-        o.u[h] = load16(rs, lane16, static_cast<int>(kOffU * 4) + ((tile0 + h) * 4 + w) * 1024);
-      o.ck = load16(rs, lg16, static_cast<int>((kOffMisc + kMiscCk) * 4) + w * 64);
-      o.gamma = load4(rs, static_cast<int>(kOffMisc * 4));
+        o.u[h] = load16(rs, lane16, own + static_cast<int>(kOffU * 4) + ((tile0 + h) * 4 + w) * 1024);
+      o.ck = load16(rs, lg16, own + static_cast<int>((kOffMisc + kMiscCk) * 4) + w * 64);
+      o.gamma = load4(rs, own + static_cast<int>(kOffMisc * 4));
     }
   } else {
     const int q = piece - 4;
@@ -584,13 +718,14 @@ __device__ __forceinline__ void load_state_piece(StateOperands<RT>& o,
 }
 
 __device__ __forceinline__ void load_output_piece(OutputOperands& o, __amdgpu_buffer_rsrc_t rs,
-                                                  int w, uint32_t lane16, uint32_t lg16,
-                                                  int piece) {
+                                                  int own, int w, uint32_t lane16,
+                                                  uint32_t lg16, int piece) {
   if (piece < 4) {
     o.qr[piece] = load16u(rs, lane16, static_cast<int>(kOffQr * 4) + (w * 4 + piece) * 1024);
-    if (piece == 0) o.sq = load16(rs, lg16, static_cast<int>((kOffMisc + kMiscSq) * 4) + w * 64);
+    if (piece == 0)
+      o.sq = load16(rs, lg16, own + static_cast<int>((kOffMisc + kMiscSq) * 4) + w * 64);
   } else {
-    const int pbase = static_cast<int>(kOffP * 4) + w * 4 * 1024;
+    const int pbase = own + static_cast<int>(kOffP * 4) + w * 4 * 1024;
     o.p[piece - 4] = load16(rs, lane16, pbase + (piece - 4) * 1024);
     o.p[piece - 2] = load16(rs, lane16, pbase + (piece - 2) * 1024);
   }
@@ -672,8 +807,15 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];  // V_new^T [row][token]
   __shared__ __attribute__((aligned(16))) float sVk[kRows][kVRow];  // ditto, token j times ck_j
 
+  // The operands of chunk c: through a resource over the records of the head's group (the
+  // first v-head's record holds the group's Qr and Kr), the head's own at byte `own`.
+  const int member = head % p.group;
+  const int own = member * static_cast<int>(kRecord * 4);
+  const int group_bytes = p.group * static_cast<int>(kRecord * 4);
   auto record = [&](int c) {
-    return ws + (static_cast<int64_t>(gbase + c) * p.num_v_heads + head) * kRecord;
+    return record_resource(
+        ws + (static_cast<int64_t>(gbase + c) * p.num_v_heads + head - member) * kRecord,
+        group_bytes);
   };
   // B fragments of S^T for k = 32 lg + step (step = 4 q + e), rows 16 h + li
   auto s_fragment = [&](int h, int q) {
@@ -708,9 +850,8 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     auto step = [&](const StateOperands<RT>& op, StateOperands<RT>& fill, int c) {
       // fill: unconditionally (the last chunk's record again past the end: a branch around
       // the loads would make the waits that follow conservative)
-      const __amdgpu_buffer_rsrc_t next =
-          record_resource(record(min(c + (kHalf ? 1 : 2), chunks - 1)));
-      const __amdgpu_buffer_rsrc_t cur = kHalf ? record_resource(record(c)) : next;
+      const __amdgpu_buffer_rsrc_t next = record(min(c + (kHalf ? 1 : 2), chunks - 1));
+      const __amdgpu_buffer_rsrc_t cur = kHalf ? record(c) : next;
       __syncthreads();  // sS holds the state at the chunk's start
       // two accumulation chains per row tile (k < 64, k >= 64 of each lane group) so that
       // consecutive matrix instructions do not wait on each other's results
@@ -722,7 +863,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_state_piece(fill, cur, w, lane16, lg16, row_block * RT, kHalf ? 4 + q : q);
+        load_state_piece(fill, cur, own, w, lane16, lg16, row_block * RT, kHalf ? 4 + q : q);
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b0 = s_fragment(h, q);
@@ -751,7 +892,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
         for (int h = 0; h < RT; ++h) st[t][h] *= op.gamma;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        load_state_piece(fill, next, w, lane16, lg16, row_block * RT, kHalf ? q : 4 + q);
+        load_state_piece(fill, next, own, w, lane16, lg16, row_block * RT, kHalf ? q : 4 + q);
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b = vk_fragment(h, q);
@@ -775,10 +916,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     // The first sets, piece by piece in the loop's order, so that the wait counts at the
     // loop head are the same from either side.
     auto prefill_set = [&](StateOperands<RT>& set, int c) {
-      const __amdgpu_buffer_rsrc_t r = record_resource(record(c));
+      const __amdgpu_buffer_rsrc_t r = record(c);
 #pragma unroll
       for (int piece = 0; piece < 8; ++piece) {
-        load_state_piece(set, r, w, lane16, lg16, row_block * RT, piece);
+        load_state_piece(set, r, own, w, lane16, lg16, row_block * RT, piece);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -792,10 +933,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       ring_scan(step, ring0, ring1, ring2, chunks);
     } else {
       if (chunks > 0) {
-        const __amdgpu_buffer_rsrc_t r = record_resource(record(0));
+        const __amdgpu_buffer_rsrc_t r = record(0);
 #pragma unroll
         for (int piece = 0; piece < 4; ++piece) {
-          load_state_piece(ring0, r, w, lane16, lg16, row_block * RT, piece);
+          load_state_piece(ring0, r, own, w, lane16, lg16, row_block * RT, piece);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -813,9 +954,8 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     const int out_row = p.num_v_heads * kDim;   // elements per token row of out
     uint16_t* out_block = p.out + static_cast<int64_t>(head) * kDim + row0;
     auto step = [&](const OutputOperands& op, OutputOperands& fill, int c) {
-      const __amdgpu_buffer_rsrc_t next =
-          record_resource(record(min(c + (kHalf ? 1 : 2), chunks - 1)));
-      const __amdgpu_buffer_rsrc_t cur = kHalf ? record_resource(record(c)) : next;
+      const __amdgpu_buffer_rsrc_t next = record(min(c + (kHalf ? 1 : 2), chunks - 1));
+      const __amdgpu_buffer_rsrc_t cur = kHalf ? record(c) : next;
       __syncthreads();  // sS holds the state at the chunk's start
       f32x4 o0[RT], o1[RT];
 #pragma unroll
@@ -826,9 +966,9 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         if (!kHalf)
-          load_output_piece(fill, next, w, lane16, lg16, q);
+          load_output_piece(fill, next, own, w, lane16, lg16, q);
         else if (q < 2)
-          load_output_piece(fill, cur, w, lane16, lg16, 4 + q);   // P of this chunk
+          load_output_piece(fill, cur, own, w, lane16, lg16, 4 + q);   // P of this chunk
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
           const f32x4 b0 = s_fragment(h, q);
@@ -856,10 +996,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         if (!kHalf) {
-          load_output_piece(fill, next, w, lane16, lg16, 4 + q);
+          load_output_piece(fill, next, own, w, lane16, lg16, 4 + q);
         } else {   // Qr of the next chunk
-          load_output_piece(fill, next, w, lane16, lg16, 2 * q);
-          load_output_piece(fill, next, w, lane16, lg16, 2 * q + 1);
+          load_output_piece(fill, next, own, w, lane16, lg16, 2 * q);
+          load_output_piece(fill, next, own, w, lane16, lg16, 2 * q + 1);
         }
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
@@ -893,10 +1033,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
     };
     auto prefill_set = [&](OutputOperands& set, int c) {
-      const __amdgpu_buffer_rsrc_t r = record_resource(record(c));
+      const __amdgpu_buffer_rsrc_t r = record(c);
 #pragma unroll
       for (int piece = 0; piece < 6; ++piece) {
-        load_output_piece(set, r, w, lane16, lg16, piece);
+        load_output_piece(set, r, own, w, lane16, lg16, piece);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -910,10 +1050,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       ring_scan(step, ring0, ring1, ring2, chunks);
     } else {
       if (chunks > 0) {
-        const __amdgpu_buffer_rsrc_t r = record_resource(record(0));
+        const __amdgpu_buffer_rsrc_t r = record(0);
 #pragma unroll
         for (int piece = 0; piece < 4; ++piece) {
-          load_output_piece(ring0, r, w, lane16, lg16, piece);
+          load_output_piece(ring0, r, own, w, lane16, lg16, piece);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -953,12 +1093,23 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   const dim3 per_chunk(static_cast<uint32_t>(prep_groups));
   hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, stream, p.cu, num_sequences,
                      chunk_start);
-  if (dt_bf16)
-    hipLaunchKernelGGL(chunk_prep_kernel<true>, per_chunk, dim3(kPrepThreads), 0, stream, p,
-                       num_sequences, ws, chunk_start, static_cast<int>(chunks));
-  else
-    hipLaunchKernelGGL(chunk_prep_kernel<false>, per_chunk, dim3(kPrepThreads), 0, stream, p,
-                       num_sequences, ws, chunk_start, static_cast<int>(chunks));
+  // 16-byte pieces of q, k and v when every row starts at a 16-byte boundary
+  const bool wide = (reinterpret_cast<uintptr_t>(p.qkv) & 15) == 0 && (p.qkv_row & 7) == 0;
+#define LD_PREP_LAUNCH(D, W)                                                                   \
+  hipLaunchKernelGGL((chunk_prep_kernel<D, W>), per_chunk, dim3(kPrepThreads), 0, stream, p,  \
+                     num_sequences, ws, chunk_start, static_cast<int>(chunks))
+  if (dt_bf16) {
+    if (wide)
+      LD_PREP_LAUNCH(true, true);
+    else
+      LD_PREP_LAUNCH(true, false);
+  } else {
+    if (wide)
+      LD_PREP_LAUNCH(false, true);
+    else
+      LD_PREP_LAUNCH(false, false);
+  }
+#undef LD_PREP_LAUNCH
   const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
   // two row tiles per workgroup once they still give 2 workgroups per CU
   const bool two_tiles = pairs * (kDim / 32) >= 512;

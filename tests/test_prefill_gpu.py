@@ -249,6 +249,40 @@ def test_chunked_many_sequences_match_the_token_serial_form(gpu):
     chunked_against_token_serial(case)
 
 
+@pytest.mark.parametrize("layout", ["odd_row_stride", "shifted_base"])
+def test_chunked_unaligned_rows_match_aligned_rows(gpu, layout):
+    """qkv rows that do not start at 16-byte boundaries (an odd row stride, or a base one
+    element past one) take the chunked prep's one- and two-element loads instead of its
+    16-byte pieces: the same values and arithmetic, so the same bits."""
+    announce(test="prefill_chunked_unaligned", layout=layout)
+    case = prefill_case(gpu, [130, 64, 7, 200, 0, 65], seed=21)
+    case["has_initial"][1] = False
+    pool0 = case["pool"].clone()
+    saved = ops.prefill_algorithm()
+    ops.set_prefill_algorithm("chunked")
+    try:
+        run(case)
+        torch.cuda.synchronize()
+        ref_out, ref_pool = case["out"].clone(), case["pool"].clone()
+        n, cols = case["qkv"].shape
+        if layout == "odd_row_stride":
+            qkv = torch.empty(n, cols + 3, dtype=torch.bfloat16, device=gpu)[:, :cols]
+        else:
+            flat = torch.empty(n * (cols + 8) + 1, dtype=torch.bfloat16, device=gpu)
+            qkv = flat[1:].view(n, cols + 8)[:, :cols]
+        assert qkv.data_ptr() % 16 != 0 or qkv.stride(0) % 8 != 0
+        qkv.copy_(case["qkv"])
+        case["qkv"] = qkv
+        case["pool"].copy_(pool0)
+        case["out"].zero_()
+        run(case)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_prefill_algorithm(saved)
+    assert torch.equal(case["out"], ref_out)
+    assert torch.equal(case["pool"], ref_pool)
+
+
 def test_rows_outside_every_sequence_are_left_alone(gpu, algorithm):
     """qkv rows that no sequence covers (all sequences empty here, or the tail after the
     last one): their outputs stay as they were; states are written back unchanged."""
