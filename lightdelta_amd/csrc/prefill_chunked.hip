@@ -113,24 +113,37 @@ __global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int32_t* cu
   }
 }
 
-// Global chunk g -> (sequence, first row, tokens) by binary search in chunk_start; false
-// past the last chunk.
+// Global chunk g -> (sequence, first row, tokens): the last n with chunk_start[n] <= g
+// (empty sequences come before it), by a 64-way search with one wave-wide load per level
+// (one level up to 64 sequences, two up to 4096; a binary search took one dependent load per
+// halving); false past the last chunk.  Called by every lane of a wave; the results are
+// uniform.
 __device__ bool find_chunk(const int32_t* cu, const int32_t* chunk_start, int num_sequences,
                            int g, int& seq, int& t0, int& len) {
   if (g >= chunk_start[num_sequences]) return false;
-  int lo = 0;
-  int hi = num_sequences - 1;
-  while (lo < hi) {  // the last n with chunk_start[n] <= g (empty sequences come before it)
-    const int mid = (lo + hi + 1) >> 1;
-    if (chunk_start[mid] <= g)
-      lo = mid;
-    else
-      hi = mid - 1;
+  const int lane = threadIdx.x & 63;
+  int lo = 0;              // chunk_start[lo] <= g throughout
+  int count = num_sequences;
+  for (;;) {
+    const int step = (count + 63) >> 6;   // entries per lane at this level
+    const bool in = lane * step < count;
+    const int idx = lo + (in ? lane * step : 0);
+    const int start = chunk_start[idx];
+    int row0 = 0, row1 = 0;
+    if (step == 1) {   // the last level: the rows of every candidate in the same round trip
+      row0 = cu[idx];
+      row1 = cu[idx + 1];
+    }
+    const int k = 63 - __clzll(static_cast<long long>(__ballot(in && start <= g)));
+    if (step == 1) {
+      seq = lo + k;
+      t0 = __builtin_amdgcn_readlane(row0, k) + (g - __builtin_amdgcn_readlane(start, k)) * kC;
+      len = min(kC, __builtin_amdgcn_readlane(row1, k) - t0);
+      return true;
+    }
+    lo += k * step;
+    count = min(step, count - k * step);
   }
-  seq = lo;
-  t0 = cu[lo] + (g - chunk_start[lo]) * kC;
-  len = min(kC, cu[lo + 1] - t0);
-  return true;
 }
 
 // The 20 tiles of A (K K^T) and P (Q K^T) on or below the diagonal over the prep's 8 waves:
@@ -282,7 +295,6 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     gb[3][lane] = __expf(glast - G);
     if (lane == 0) ws[(static_cast<int64_t>(g) * p.num_v_heads + head) * kRecord + kOffMisc] = __expf(glast);
   };
-  if (solves_u) fetch_v(key_head * p.group, threadIdx.x & 15, (threadIdx.x >> 4) & 3);
   if (wave == 4) fetch_gates(key_head * p.group, threadIdx.x & 63);
 
   // q and k of the chunk's tokens and their inverse norms (zero rows past its end); wave w
@@ -302,6 +314,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       qv[h] = *reinterpret_cast<const u32x4*>(row + q_col + 8 * l16);
       kv[h] = *reinterpret_cast<const u32x4*>(row + k_col + 8 * l16);
     }
+    // v of the first v-head behind q and k (loads return in order; the norms come first)
+    if (solves_u) fetch_v(key_head * p.group, threadIdx.x & 15, (threadIdx.x >> 4) & 3);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int i = wave * kPrepTokens + 4 * h + quarter;
@@ -344,6 +358,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       qr[ii] = row[q_col + 2 * lane] | (static_cast<uint32_t>(row[q_col + 2 * lane + 1]) << 16);
       kr[ii] = row[k_col + 2 * lane] | (static_cast<uint32_t>(row[k_col + 2 * lane + 1]) << 16);
     }
+    if (solves_u) fetch_v(key_head * p.group, threadIdx.x & 15, (threadIdx.x >> 4) & 3);
 #pragma unroll
     for (int ii = 0; ii < kPrepTokens; ++ii) {
       const int i = wave * kPrepTokens + ii;
@@ -543,6 +558,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     }
     __syncthreads();
     if (wave == 4 && next) gates(member + 1, lane);
+    // the U waves are idle here; the next v-head forms its right-hand side from these
+    if (solves_u && next) fetch_v(head + 1, li, lg);
     // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
     // (block w by wave w < 4)
     if (wave < 4 && lane < 16) {
@@ -625,7 +642,6 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         wdst[item] = *reinterpret_cast<const f32x4*>(sW + i * kRow + k4);
       }
     }
-    if (solves_u && next) fetch_v(head + 1, li, lg);
     // the next v-head rewrites the gates, -A, P and W
     __syncthreads();
   }
