@@ -65,7 +65,7 @@ def token_serial():
     ops.set_prefill_algorithm(saved)
 
 
-@pytest.mark.parametrize("heads", [(16, 32), (4, 8), (16, 48)])
+@pytest.mark.parametrize("heads", [(16, 32), (4, 8), (16, 48), (8, 8)])
 def test_prefill_matches_oracle(gpu, heads, algorithm):
     announce(test="prefill_oracle", heads=heads, algorithm=algorithm)
     case = prefill_case(gpu, [5, 0, 1, 33, 70], heads=heads, seed=heads[1])
