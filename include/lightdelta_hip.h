@@ -235,7 +235,7 @@ int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t num_sequences
 
 /*
  * 1 if LD_PREFILL_AUTO takes the chunked form for this shape (given a workspace), else 0:
- * prompts of 48 tokens or more on average (num_v_heads does not enter the rule on MI355X).
+ * prompts of 52 tokens or more on average (num_v_heads does not enter the rule on MI355X).
  * Callers use it to decide whether to provide the workspace.  No
  * counterpart in the reference (its prefill always runs chunk_gated_delta_rule).
  */

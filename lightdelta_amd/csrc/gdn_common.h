@@ -115,14 +115,14 @@ __device__ __forceinline__ float softplus(float x) {
 // num_sequences sequences and num_v_heads heads, and the launch of its three phases; the
 // raw outputs go to p.out for prefill_norm_kernel.
 // The shapes for which the chunked prefill beats the token-serial one on MI355X, measured
-// over 1 x 64 .. 1024 x 16 tokens at 32 v heads: every shape with prompts of 48 tokens or
-// more (1.05x at 1024 x 48, 1.3x at 512 x 64 .. 9.7x at 1 x 4096), none with 40 or fewer (a
-// full 64-token record per chunk and head makes short prompts costly: 0.89x at 1024 x 40,
-// 0.74x at 1024 x 32, 0.43x at 1024 x 16).  The head count does not move the crossover.
+// over 1 x 64 .. 1024 x 16 tokens at 32 v heads: every shape with prompts of 56 tokens or
+// more (1.07x at 512 x 56, 1.2x at 512 x 64 .. 10x at 1 x 4096), none with 48 or fewer but
+// 16 x 48 (a full 64-token record per chunk and head makes short prompts costly: 0.94x at
+// 1024 x 48, 0.68x at 1024 x 32, 0.40x at 1024 x 16).  The rule takes the midpoint.
 inline bool prefill_auto_chunked(int64_t num_tokens, int64_t num_sequences, int64_t num_v_heads) {
   (void)num_v_heads;
   if (num_sequences <= 0 || num_tokens <= 0) return false;
-  return num_tokens / num_sequences >= 48;
+  return num_tokens / num_sequences >= 52;
 }
 
 int64_t prefill_chunked_workspace_bytes(int64_t num_tokens, int64_t num_sequences,

@@ -1,21 +1,19 @@
 // Token-serial prefill for gfx950: the sequence's tokens run in order with a block of state
 // rows in registers for the whole prompt (read once, from the slot or as zeros; written
-// once, to the slot).  The
-// per-token arithmetic is the decode kernel's (stage_token, chunk_step), so a prefill of n
-// tokens gives bit for bit the states and outputs of n single-token decode steps.  Rows of
-// the state evolve independently (row v needs only v[v], k, q and the gates), so a head's
-// 128 rows may be split over 4 / Chunks workgroups of 4 waves, each wave holding 8 * Chunks
-// rows: fewer rows per wave shorten the per-token chain and spread a few long prompts over
-// more of the GPU, at the price of staging q and k in every workgroup.
-//   Chunks == 4 (one workgroup per head): the raw outputs of a group of 4 tokens collect in
-//   LDS (double-buffered); after one barrier per group, wave w runs the gated-RMSNorm
-//   epilogue of the group's token w.
-//   Chunks < 4: every wave writes its rows' raw outputs (rounded to bf16, the reference's
-//   rounding point before the norm) to `out`; prefill_norm_kernel applies the gated RMSNorm
-//   in place afterwards, with the epilogue's arithmetic.
-// The next token's inputs are prefetched.  Four waves per SIMD: the tile, the token in
-// flight and the staged one fit 128 VGPRs, with the rounding of raw outputs to bf16 left to
-// their readers and the token fetch addressed from a uniform row start.
+// once, to the slot).  The per-token arithmetic is the decode kernel's (stage_token,
+// chunk_step), so a prefill of n tokens gives bit for bit the states and outputs of n
+// single-token decode steps.  Rows of the state evolve independently (row v needs only
+// v[v], k, q and the gates), so a head's 128 rows may be split over several workgroups.
+//   gdn_prefill_kernel: one workgroup per (sequence, head), 32 rows per wave; each token is
+//   staged once per workgroup (by one wave, a group of 4 tokens ahead, through LDS), and
+//   the raw outputs of a group of 4 tokens collect in LDS; after one barrier per group,
+//   wave w runs the gated-RMSNorm epilogue of the group's token w.  Four waves per SIMD:
+//   the tile and a token's vectors fit 128 VGPRs.
+//   gdn_prefill_rows_kernel (few sequences): a head's rows over 2 or 4 workgroups, 8 or 16
+//   rows per wave, for a shorter per-token chain and more of the GPU; every wave writes its
+//   rows' raw outputs (rounded to bf16, the reference's rounding point before the norm) to
+//   `out`, and prefill_norm_kernel applies the gated RMSNorm in place afterwards, with the
+//   epilogue's arithmetic.
 //
 // Also here: the gated-RMSNorm pass over raw outputs (prefill_norm_kernel, used by the
 // row-split kernels and the chunked form) and the prefill entry points of the C ABI, which
@@ -29,19 +27,20 @@ namespace {
 
 constexpr int kPrefillGroup = 4;
 
-template <bool DtBf16, bool WBf16, int Chunks>
+// One workgroup per (sequence, v-head), wave w holding rows 32w .. 32w + 31.  Tokens go in
+// groups of 4: before the group's barrier, wave w stages token w of the next group (q^ and
+// k^ in the lane layout, decay, beta: stage_token) into double-buffered LDS, and every wave
+// reads a token's staging from there, so each token is staged once per workgroup and off
+// the per-token chain.  A wave's v values come one token ahead.
+template <bool DtBf16, bool WBf16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void gdn_prefill_kernel(const DecodeParams args) {
-  static_assert(Chunks == 1 || Chunks == 2 || Chunks == 4, "8, 16 or 32 rows per wave");
-  constexpr int kBlocks = 4 / Chunks;         // workgroups per (sequence, head)
-  constexpr int kWaveRows = 8 * Chunks;       // state rows per wave
-  constexpr int kTilePieces = 4 * Chunks;     // 16-byte pieces per lane
+  constexpr int kWaveRows = 32;    // state rows per wave
+  constexpr int kTilePieces = 16;  // 16-byte pieces per lane
   const DecodeParams& p = args;
   const int tile = blockIdx.x;
-  const int sequence = tile / (p.num_v_heads * kBlocks);
-  const int rest = tile - sequence * p.num_v_heads * kBlocks;
-  const int head = rest / kBlocks;
-  const int block = rest - head * kBlocks;
+  const int sequence = tile / p.num_v_heads;
+  const int head = tile - sequence * p.num_v_heads;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -53,24 +52,26 @@ void gdn_prefill_kernel(const DecodeParams args) {
   const int key_head = head / p.group;
   const int kq = lane & 15;
   const int rsub = lane >> 4;
-  const int wave_row0 = block * kWaves * kWaveRows + wave * kWaveRows;  // first row of the wave
+  const int wave_row0 = wave * kWaveRows;  // first row of the wave
   const int row_base = wave_row0 + rsub;
   const int q_col = key_head * kDim;
   const int k_col = (p.num_k_heads + key_head) * kDim;
   const int v_col = (2 * p.num_k_heads + head) * kDim;
-  const int v_lane = v_col + wave_row0 + (lane & (kWaveRows - 1));
 
   __shared__ float s_v[kWaves][kWaveRows];
-  __shared__ float s_o[Chunks == 4 ? 2 : 1][Chunks == 4 ? kPrefillGroup : kWaves]
-                      [Chunks == 4 ? kDim : kWaveRows];
+  __shared__ float s_o[2][kPrefillGroup][kDim];
+  __shared__ f32x4 s_qk[2][kPrefillGroup][2][kDim / 4];  // [buffer][token][q^ | k^][piece]
+  __shared__ float s_db[2][kPrefillGroup][2];             // [buffer][token][decay | beta]
+  __shared__ float s_w[kDim];                              // the norm weight
 
   // uniform: kept in an SGPR (a bf16 load would leave it in a VGPR)
   const float dt_bias = __int_as_float(
       __builtin_amdgcn_readfirstlane(__float_as_int(load_param(p.dt_bias, head, DtBf16))));
   const float a_log = p.a_log[head];
-  float w[2];
+  if (wave == 0) {  // read by every wave's epilogue, after the first barrier
 #pragma unroll
-  for (int e = 0; e < 2; ++e) w[e] = Chunks == 4 ? load_param(p.norm_weight, 2 * lane + e, WBf16) : 0.0f;
+    for (int e = 0; e < 2; ++e) s_w[2 * lane + e] = load_param(p.norm_weight, 2 * lane + e, WBf16);
+  }
 
   const int64_t head_offset = static_cast<int64_t>(head) * kDim * kDim;
   const uint32_t lane_bytes = static_cast<uint32_t>(row_base * kDim + kq * 4) * 4u;
@@ -86,97 +87,111 @@ void gdn_prefill_kernel(const DecodeParams args) {
     for (int j = 0; j < kTilePieces; ++j) s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  // One token: stage it, fetch the inputs of token t + 1 (of the last token again past the
-  // end: an unconditional fetch needs no merge of old and new values), apply it to the tile
-  // and leave its raw outputs (unrounded) in the group's slot i.
+  // Inputs, addressed from the uniform row start with 32-bit lane offsets; tokens past the
+  // end read the last one (an unconditional fetch needs no merge of old and new values).
   const int last = eos - 1;
-  // load_token's values, addressed from the uniform row start with 32-bit lane offsets
   const uint32_t q_bytes = static_cast<uint32_t>(q_col + kq * 4) * 2u;
   const uint32_t k_bytes = static_cast<uint32_t>(k_col + kq * 4) * 2u;
-  const uint32_t v_bytes = static_cast<uint32_t>(v_lane) * 2u;
+  const uint32_t v_bytes = static_cast<uint32_t>(v_col + wave_row0 + (lane & (kWaveRows - 1))) * 2u;
+  auto row_of = [&](int64_t token) __attribute__((always_inline)) {
+    return reinterpret_cast<const char*>(p.qkv + token * p.qkv_row);
+  };
+  auto u16 = [](const char* row, uint32_t offset) __attribute__((always_inline)) {
+    return static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(row + offset));
+  };
+  // load_token's values of a token to stage (its v is not needed there)
   auto fetch = [&](int64_t token) __attribute__((always_inline)) {
-    const char* row = reinterpret_cast<const char*>(p.qkv + token * p.qkv_row);
-    auto u16 = [row](uint32_t offset) __attribute__((always_inline)) {
-      return static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(row + offset));
-    };
+    const char* row = row_of(token);
     TokenIn in;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const uint32_t off = e * 128u;
-      in.q[2 * e] = u16(q_bytes + off) | (u16(q_bytes + off + 2) << 16);
-      in.q[2 * e + 1] = u16(q_bytes + off + 4) | (u16(q_bytes + off + 6) << 16);
-      in.k[2 * e] = u16(k_bytes + off) | (u16(k_bytes + off + 2) << 16);
-      in.k[2 * e + 1] = u16(k_bytes + off + 4) | (u16(k_bytes + off + 6) << 16);
+      in.q[2 * e] = u16(row, q_bytes + off) | (u16(row, q_bytes + off + 2) << 16);
+      in.q[2 * e + 1] = u16(row, q_bytes + off + 4) | (u16(row, q_bytes + off + 6) << 16);
+      in.k[2 * e] = u16(row, k_bytes + off) | (u16(row, k_bytes + off + 2) << 16);
+      in.k[2 * e + 1] = u16(row, k_bytes + off + 4) | (u16(row, k_bytes + off + 6) << 16);
     }
-    in.v = static_cast<uint16_t>(u16(v_bytes));
+    in.v = 0;
     in.a = p.a[token * p.a_row + head];
     in.b = p.b[token * p.b_row + head];
     return in;
   };
-  TokenIn next;  // inputs of the next token
-  if (bos < eos) next = fetch(bos);
-  int buf = 0;
-  auto token_step = [&](int t, int i) __attribute__((always_inline)) {
-    const TokenIn in = next;
-    next = fetch(min(t + 1, last));
+  // stage_token's results into buffer b, token i (lanes of DPP row 0 write the pieces)
+  auto stage = [&](const TokenIn& in, int b, int i) __attribute__((always_inline)) {
     const Staged x = stage_token(in, a_log, dt_bias, p.scale);
-    if (lane < kWaveRows) s_v[wave][lane] = bf16_to_f32(in.v);
-    // s_v (and s_o below) are read back by other lanes of this wave: a wave's LDS
-    // operations run in program order, so only the compiler must not reorder them.
+    if (rsub == 0) {
+      s_qk[b][i][0][kq] = x.q0;
+      s_qk[b][i][0][16 + kq] = x.q1;
+      s_qk[b][i][1][kq] = x.k0;
+      s_qk[b][i][1][16 + kq] = x.k1;
+    }
+    if (lane == 0) {
+      s_db[b][i][0] = x.decay;
+      s_db[b][i][1] = x.beta;
+    }
+  };
+
+  // the first group's staging (wave w: token bos + w) and the first token's v
+  int buf = 0;
+  uint16_t v_next = 0;
+  if (bos < eos) {
+    stage(fetch(min(bos + wave, last)), 0, wave);
+    v_next = static_cast<uint16_t>(u16(row_of(bos), v_bytes));
+  }
+  lds_barrier();
+
+  // One token: its v values to the wave's LDS row (read back by other lanes of the wave:
+  // a wave's LDS operations run in program order, so only the compiler must not reorder
+  // them), the next token's v fetched, the staged vectors read, the tile updated; its raw
+  // outputs (unrounded) go to the group's slot i.
+  auto token_step = [&](int t, int i) __attribute__((always_inline)) {
+    if (lane < kWaveRows) s_v[wave][lane] = bf16_to_f32(v_next);
+    v_next = static_cast<uint16_t>(u16(row_of(min(t + 1, last)), v_bytes));
     asm volatile("" ::: "memory");
-    Vectors vec;
-    vec.q0 = x.q0;
-    vec.q1 = x.q1;
-    vec.k0 = x.k0;
-    vec.k1 = x.k1;
-    // output rows: absolute in the per-group buffer, wave-relative in the per-wave one
-    float* o = Chunks == 4 ? s_o[buf][i] : s_o[0][wave];
-    const int orow = Chunks == 4 ? row_base : rsub;
+    const Vectors vec = load_vectors(s_qk[buf][i], kq);
+    const float decay = s_db[buf][i][0];
+    const float beta = s_db[buf][i][1];
 #define LD_PREFILL_CHUNK(C)                                                                    \
-  if constexpr ((C) < Chunks)                                                                  \
-    chunk_step<C, 4, kTilePieces, false>(s, vec, s_v[wave][8 * (C) + rsub],                     \
-                                         s_v[wave][8 * (C) + 4 + rsub], o, x.decay, x.beta,    \
-                                         kq, orow + 8 * (C), NoStore{}, lane_bytes);
+  chunk_step<C, 4, kTilePieces, false>(s, vec, s_v[wave][8 * (C) + rsub],                     \
+                                       s_v[wave][8 * (C) + 4 + rsub], s_o[buf][i], decay,    \
+                                       beta, kq, row_base + 8 * (C), NoStore{}, lane_bytes);
     LD_PREFILL_CHUNK(0)
     LD_PREFILL_CHUNK(1)
     LD_PREFILL_CHUNK(2)
     LD_PREFILL_CHUNK(3)
 #undef LD_PREFILL_CHUNK
     asm volatile("" ::: "memory");
-    if constexpr (Chunks < 4) {  // raw outputs of the wave's rows, rounded to bf16
-      if (lane < kWaveRows)
-        p.out[(static_cast<int64_t>(t) * p.num_v_heads + head) * kDim + wave_row0 + lane] =
-            f32_to_bf16(s_o[0][wave][lane]);
-    }
   };
-  // A group of tokens: gate loads for the epilogue, the tokens, then (one workgroup per
-  // head) the gated RMSNorm epilogue of the group's token `wave` after one barrier.
+  // A group of tokens: the next group's token `wave` fetched first, the tokens, this
+  // group's gate of token `wave` fetched, the staging of that next token (into the other
+  // buffer, last read before the previous barrier), one barrier, then the gated RMSNorm
+  // epilogue of the group's token `wave`.
   auto group = [&](int g0, auto&& tokens) __attribute__((always_inline)) {
-    uint16_t gh[2] = {0, 0};
-    if constexpr (Chunks == 4) {
+    const TokenIn next_in = fetch(min(g0 + kPrefillGroup + wave, last));
+    tokens();
+    uint16_t gh[2];
+    {
       const int64_t etoken = min(g0 + wave, last);
 #pragma unroll
       for (int e = 0; e < 2; ++e) gh[e] = p.gate[etoken * p.gate_row + head * kDim + 2 * lane + e];
     }
-    tokens();
-    if constexpr (Chunks == 4) {
-      lds_barrier();  // the group's raw outputs are complete
-      if (g0 + wave < eos) {
-        float raw[2];
-        float ss = 0.0f;
+    stage(next_in, buf ^ 1, wave);
+    lds_barrier();  // the group's raw outputs and the next group's staging are complete
+    if (g0 + wave < eos) {
+      float raw[2];
+      float ss = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          raw[e] = round_bf16(s_o[buf][wave][2 * lane + e]);
-          ss = fmaf(raw[e], raw[e], ss);
-        }
-        ss = wave_sum(ss);
-        const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
-        uint16_t* orow_ptr = p.out + (static_cast<int64_t>(g0 + wave) * p.num_v_heads + head) * kDim;
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-          orow_ptr[2 * lane + e] =
-              f32_to_bf16(((raw[e] * rstd) * w[e]) * silu(bf16_to_f32(gh[e])));
+      for (int e = 0; e < 2; ++e) {
+        raw[e] = round_bf16(s_o[buf][wave][2 * lane + e]);
+        ss = fmaf(raw[e], raw[e], ss);
       }
+      ss = wave_sum(ss);
+      const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
+      uint16_t* orow_ptr = p.out + (static_cast<int64_t>(g0 + wave) * p.num_v_heads + head) * kDim;
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        orow_ptr[2 * lane + e] =
+            f32_to_bf16(((raw[e] * rstd) * s_w[2 * lane + e]) * silu(bf16_to_f32(gh[e])));
     }
     buf ^= 1;
   };
@@ -459,11 +474,11 @@ int prefill(const ld_gdn_prefill_args& a, void* workspace, int64_t workspace_byt
   // would leave the GPU short of work (1024 tiles fill 256 CUs at 4 per CU).
   const int chunks = chunked ? 0 : (tiles >= 256 ? 4 : (tiles >= 128 ? 2 : 1));
   const uint32_t grid = chunks > 0 ? static_cast<uint32_t>(tiles * (4 / chunks)) : 0u;
-#define LD_PREFILL_LAUNCH(C)                                                                 \
-  hipLaunchKernelGGL(dt_bf16 ? (w_bf16 ? gdn_prefill_kernel<true, true, C>                   \
-                                       : gdn_prefill_kernel<true, false, C>)                 \
-                             : (w_bf16 ? gdn_prefill_kernel<false, true, C>                  \
-                                       : gdn_prefill_kernel<false, false, C>),               \
+#define LD_PREFILL_LAUNCH()                                                                  \
+  hipLaunchKernelGGL(dt_bf16 ? (w_bf16 ? gdn_prefill_kernel<true, true>                      \
+                                       : gdn_prefill_kernel<true, false>)                    \
+                             : (w_bf16 ? gdn_prefill_kernel<false, true>                     \
+                                       : gdn_prefill_kernel<false, false>),                  \
                      dim3(grid), dim3(kThreads), 0, s, p)
 #define LD_PREFILL_ROWS_LAUNCH(C)                                                            \
   hipLaunchKernelGGL(dt_bf16 ? (w_bf16 ? gdn_prefill_rows_kernel<true, true, C>              \
@@ -472,7 +487,7 @@ int prefill(const ld_gdn_prefill_args& a, void* workspace, int64_t workspace_byt
                                        : gdn_prefill_rows_kernel<false, false, C>),          \
                      dim3(grid), dim3(kThreads), 0, s, p)
   if (chunks == 4) {
-    LD_PREFILL_LAUNCH(4);
+    LD_PREFILL_LAUNCH();
   } else {
     if (chunks == 2)
       LD_PREFILL_ROWS_LAUNCH(2);

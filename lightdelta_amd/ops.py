@@ -261,7 +261,7 @@ def check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, sta
 
 
 # Prefill algorithm: "auto" runs 64-token chunks in the WY form for the shapes where they are
-# faster (ld_gdn_prefill_auto_chunked: prompts of 48 tokens or more on average), else the
+# faster (ld_gdn_prefill_auto_chunked: prompts of 52 tokens or more on average), else the
 # token-serial recurrence; "token_serial" and "chunked" force one.  Results agree within
 # rounding; the token-serial form reproduces the decode kernel bit for bit.
 _PREFILL_ALGORITHMS = {"auto": _lib.PREFILL_AUTO, "token_serial": _lib.PREFILL_TOKEN_SERIAL,

@@ -149,9 +149,9 @@ def test_prefill_workspace_query_and_chunked_without_workspace():
     (16 * 128, 16, 32, 1),   # 128-token prompts, 512 (sequence, head) tiles
     (512 * 64, 512, 32, 1),  # 64-token prompts, 16384 tiles
     (4 * 64, 4, 32, 1),
-    (1024 * 48, 1024, 32, 1),  # the shortest prompts that go chunked
-    (512 * 48 - 1, 512, 32, 0),  # a mean just under 48 tokens
-    (1024 * 40, 1024, 32, 0),
+    (1024 * 52, 1024, 32, 1),  # the shortest prompts that go chunked
+    (512 * 52 - 1, 512, 32, 0),  # a mean just under 52 tokens
+    (1024 * 48, 1024, 32, 0),
     (1024 * 32, 1024, 32, 0),  # short prompts
     (2 * 16, 2, 32, 0),
     (0, 1, 32, 0),
