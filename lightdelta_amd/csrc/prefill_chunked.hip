@@ -14,11 +14,12 @@
 //   O     = (q^_i exp(G_i)) S^T + P V_new,  P_ij = Gam_ij (q^_i . k^_j) for j <= i
 //   S'    = exp(G_{n-1}) S + V_new^T (k^_j exp(G_{n-1} - G_j))
 // which equals the token-by-token recurrence of the decode kernel (checked against it in
-// float64: 7e-8 relative on the state).  Two launches:
-//   chunk_prep_kernel  one workgroup per (chunk, v-head), all chunks in parallel: norms,
-//                      gates, A and P, the blocked forward substitution for W and U, and
-//                      q and k with their per-token scales; everything to a workspace
-//                      record.
+// float64: 7e-8 relative on the state).  After chunk_index_kernel (where each sequence's
+// chunks start), two launches:
+//   chunk_prep_kernel  one workgroup per (chunk, k-head), all chunks in parallel, running
+//                      the group's v-heads in turn: norms, gates, A and P, the blocked
+//                      forward substitution for W and U, and q and k with their per-token
+//                      scales; everything to workspace records.
 //   chunk_scan_kernel  one workgroup per (sequence, v-head, block of 16 or 32 state rows),
 //                      the only sequential part: chunk by chunk, V_new, the raw outputs of
 //                      its columns (rounded to bf16 into `out`, the reference's rounding
@@ -611,7 +612,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 
     // U straight from the fragments (its row block rb is the scan wave, its column tile the
     // scan's block of v rows); W through LDS, once every wave is past its reads of -A (W takes
-    // the region of -A and P)
+    // the region of -A and the v staging)
     if (solves_u) {
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb)
