@@ -575,9 +575,11 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   }
 
   // ---- staging, while the tile streams in ----
+  uint16_t v_new_split[kConvSplit ? kCols : 1];
   if constexpr (kConvSplit) {
     const bool convolves = tid < 2 * kDim;   // wave-uniform
-    uint16_t qk_new[kCols], v_new[kCols];
+    uint16_t qk_new[kCols];
+    uint16_t (&v_new)[kCols] = v_new_split;
     if (convolves) {
       const bool has_bias = p.conv_bias != nullptr;
       conv_compute<Width, kCols>(ci_qk, p.conv_len, num_tokens, conv_offset, has_bias,
@@ -588,15 +590,8 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
       for (int k = 0; k < kCols; ++k) s_conv_new[tid][k] = qk_new[k];
     }
     // conv outputs visible to every wave; every conv-state read of the workgroup consumed
+    // (the shifted v state and the ticket follow the tokens' staging, off its path)
     lds_barrier();
-    if (convolves) {
-#pragma unroll
-      for (int k = 0; k < kCols; ++k)
-        p.conv_state[cs_v_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new[k];
-    }
-    if (p.group > 1 && tid == 0)
-      arrived = count_in(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
-                         p.group);
     conv_token_w();
   }
   if constexpr (kConvLate) {
@@ -737,6 +732,16 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     }                                                                                       \
   }
   if constexpr (kShared0) lds_barrier();  // every token staged
+  if constexpr (kConvSplit) {
+    if (tid < 2 * kDim) {
+#pragma unroll
+      for (int k = 0; k < kCols; ++k)
+        p.conv_state[cs_v_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new_split[k];
+    }
+    if (p.group > 1 && tid == 0)
+      arrived = count_in(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
+                         p.group);
+  }
   LD_CHUNK(0)
   if constexpr (kChunks > 1) LD_CHUNK(1)
   if constexpr (kChunks > 2) {
