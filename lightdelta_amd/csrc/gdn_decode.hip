@@ -268,16 +268,17 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 // non-temporal loads, system-scope stores).
 // Waves per SIMD the register allocation aims at: 4 (four 4-wave workgroups per CU, or one
 // 16-wave workgroup for the conv-fused verify, whose conv arguments need the SGPRs that a
-// second one would take: at 8 it spilled 44 of them) or 8 (two 16-wave workgroups).
-constexpr int waves_per_simd(int waves, int conv_cols) {
-  return waves == kWaves || conv_cols > 0 ? 4 : 8;
+// second one would take: at 8 it spilled 44 of them) or 8 (two 16-wave workgroups, the
+// conv-fused single token included).
+constexpr int waves_per_simd(int waves, int conv_cols, int width) {
+  return waves == kWaves || (conv_cols > 0 && width > 1) ? 4 : 8;
 }
 
 template <bool DtBf16, bool WBf16, int LoadPol, int StorePol, int Width, int ConvCols,
           int Waves = kWaves, bool Packed = false>
 __global__ __launch_bounds__(64 * Waves)
-__attribute__((amdgpu_waves_per_eu(waves_per_simd(Waves, ConvCols),
-                                   waves_per_simd(Waves, ConvCols))))
+__attribute__((amdgpu_waves_per_eu(waves_per_simd(Waves, ConvCols, Width),
+                                   waves_per_simd(Waves, ConvCols, Width))))
 void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
                        const int32_t* md_accepted, int md_num_v_heads, const DecodeParams args) {
   // The request metadata pointers and the head count are kernel arguments of their own, ahead
@@ -304,8 +305,12 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // The conv of a verify step with 16 waves: its inputs load before the tile, the arithmetic
   // runs while the tile streams in (16 waves leave the registers for both).
   constexpr bool kConvSplit = Conv && Width > 1 && Waves == 16;
+  // One token, 3..4 state columns, 16 waves: one channel per thread (0..255 q/k, 256..383
+  // v), its inputs loaded ahead of the tile and convolved while the tile streams in, in 6
+  // registers, so that two workgroups fit a CU.
+  constexpr bool kConvOne16 = Conv && Width == 1 && kCols <= 4 && Waves == 16;
   constexpr bool kConvFirst = Conv && (Width > 1 || kCols > 4) && !kConvSplit;
-  constexpr bool kConvLate = Conv && !kConvFirst && !kConvSplit;
+  constexpr bool kConvLate = Conv && !kConvFirst && !kConvSplit && !kConvOne16;
   static_assert(!kConvLate || kCols == 4, "the in-flight conv holds 4 state columns");
   static_assert(!kConvLate || Waves == kWaves, "the in-flight conv runs with 4 waves");
   static_assert(!Packed || (kConvLate && Waves == 4), "the packed conv state: one token, 4 waves");
@@ -437,6 +442,10 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   uint32_t cw_qk[2], cw_v[2];
   uint32_t arrived = 0;  // ticket count before this workgroup's increment (thread 0)
   ConvIn ci_qk, ci_v;    // kConvSplit: the conv inputs, loaded ahead of the tile
+  // kConvOne16: the thread's channel (state columns as bf16 pairs, input, weights, bias)
+  uint32_t c1_st[2] = {0u, 0u}, c1_w[2] = {0u, 0u};
+  uint16_t c1_x = 0, c1_bias = 0;
+  int64_t c1_at = 0;
   // Packed: the wave's first q/k and v channel (waves 0, 1: q channels 0..63, 64..127;
   // waves 2, 3: the k channels; the v channels of waves 2, 3 repeat those of 0, 1), and the
   // lane's 16-byte piece of a 128 * len-byte run (lanes past its 8 * len pieces repeat the
@@ -480,6 +489,25 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   } else if constexpr (kConvSplit) {
     conv_load<Width, kCols>(p, bos, num_tokens, cs_qk_at, conv_qk, ci_qk);
     conv_load<Width, kCols>(p, bos, num_tokens, cs_v_at, conv_v, ci_v);
+  } else if constexpr (kConvOne16) {
+    if (tid < 3 * kDim) {  // wave-uniform; every column clamped to the state's last
+      const int ch = tid < kDim ? q_col + tid
+                                : (tid < 2 * kDim ? k_col + (tid - kDim) : v_col + (tid - 2 * kDim));
+      c1_at = conv_slot_at + ch * p.conv_dim_stride;
+      c1_x = p.conv_x[static_cast<int64_t>(bos) * p.conv_x_row + ch];
+      uint32_t st[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        st[j] = p.conv_state[c1_at + min(j, p.conv_len - 1) * p.conv_len_stride];
+      c1_st[0] = st[0] | (st[1] << 16);
+      c1_st[1] = st[2] | (st[3] << 16);
+      const uint32_t* wsrc = reinterpret_cast<const uint32_t*>(p.conv_weight + ch * kConvWidth);
+      c1_w[0] = wsrc[0];
+      c1_w[1] = wsrc[1];
+      c1_bias = (p.conv_bias != nullptr ? p.conv_bias : p.conv_weight)[ch];
+    }
+    in0.a = p.a[static_cast<int64_t>(bos) * p.a_row + head];
+    in0.b = p.b[static_cast<int64_t>(bos) * p.b_row + head];
   } else if constexpr (kConvLate) {
     const uint16_t* xrow = p.conv_x + static_cast<int64_t>(bos) * p.conv_x_row;
     cx_qk = xrow[conv_qk];
@@ -593,6 +621,32 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     // (the shifted v state and the ticket follow the tokens' staging, off its path)
     lds_barrier();
     conv_token_w();
+  }
+  if constexpr (kConvOne16) {
+    if (tid < 3 * kDim) {
+      const int len = p.conv_len;
+      const uint16_t st[4] = {static_cast<uint16_t>(c1_st[0]), static_cast<uint16_t>(c1_st[0] >> 16),
+                              static_cast<uint16_t>(c1_st[1]), static_cast<uint16_t>(c1_st[1] >> 16)};
+      s_conv[0][tid] = conv_output(c1_x, st, c1_w, c1_bias, p.conv_bias != nullptr);
+      // shifted state: columns 1..len-1, then the new input; q/k kept for the end-of-kernel
+      // write, the thread's own v channel shifted in place (only it reads that channel)
+      uint16_t shifted[kCols];
+#pragma unroll
+      for (int j = 0; j < kCols; ++j) shifted[j] = j + 1 < len ? st[j + 1 < kCols ? j + 1 : j] : c1_x;
+      if (tid < 2 * kDim) {
+#pragma unroll
+        for (int j = 0; j < kCols; ++j) s_conv_new[tid][j] = shifted[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < kCols; ++j)
+          p.conv_state[c1_at + min(j, len - 1) * p.conv_len_stride] = shifted[j];
+      }
+    }
+    // conv outputs visible to every wave; every q/k conv-state read of the workgroup consumed
+    lds_barrier();
+    if (p.group > 1 && tid == 0)
+      arrived = count_in(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
+                         p.group);
   }
   if constexpr (kConvLate) {
     const int len = p.conv_len;
@@ -850,14 +904,17 @@ int launch_kernel(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blo
 template <typename One, typename Verify, typename ConvOne, typename ConvVerify>
 int launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
                   uint32_t blocks, hipStream_t stream) {
-  static_assert(ConvOne::kWaveCount == kWaves, "the single-token conv-fused kernel runs 4 waves");
+  // a state of more than 4 columns runs its conv before the tile loads, with 4 waves
+  using ConvLong = Shape<ConvOne::kLoad, ConvOne::kStore, kWaves>;
   if (conv) {
     switch (p.width) {
       case 1:  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
-        if (p.conv_len <= 4 && p.conv_packed)
-          return launch_kernel<ConvOne, 1, 4, true>(p, dt_bf16, w_bf16, blocks, stream);
+        if constexpr (ConvOne::kWaveCount == kWaves) {  // the packed state: 4 waves
+          if (p.conv_len <= 4 && p.conv_packed)
+            return launch_kernel<ConvOne, 1, 4, true>(p, dt_bf16, w_bf16, blocks, stream);
+        }
         if (p.conv_len <= 4) return launch_kernel<ConvOne, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
-        return launch_kernel<ConvOne, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
+        return launch_kernel<ConvLong, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
       case 2: return launch_kernel<ConvVerify, 2, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
       case 3: return launch_kernel<ConvVerify, 3, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
       default: return launch_kernel<ConvVerify, 4, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
@@ -943,9 +1000,10 @@ int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, b
   //   verify, stream:    16 waves, non-temporal loads, system-scope stores, one workgroup
   //                      per CU (B=64, T=4 cold: 114.4 us = 5.87 TB/s; two per CU 116.0;
   //                      the keep kernel 120.8).
-  //   conv-fused, one token: 4 waves, plain loads and stores (keep; 21.4 us hot) or
-  //                      non-temporal ones (stream; 28.0 us cold, against 30.0 with
-  //                      system-scope stores).
+  //   conv-fused, one token: 4 waves, plain loads and stores (keep; 21.4 us hot); under
+  //                      stream 16 waves, one conv channel per thread, non-temporal loads
+  //                      and stores, two workgroups per CU (27.1 us cold, against 27.7 with
+  //                      4 waves and 27.6 with system-scope stores).
   //   conv-fused verify, either: 16 waves, the conv's inputs loaded ahead of the tile,
   //                      plain loads, non-temporal stores, one workgroup per CU (B=64, T=4,
   //                      6 conv columns: 105.5 us hot, 127.4 cold, against 108.8 and 143.2
@@ -955,7 +1013,7 @@ int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, b
   int rc;
   if (a.cache_policy == LD_CACHE_STREAM)
     rc = launch_decode<Shape<kPolNT, kPolSys, 16>, Shape<kPolNT, kPolSys, 16, true>,
-                       Shape<kPolNT, kPolNT, kWaves>, Shape<kPolPlain, kPolNT, 16, true>>(
+                       Shape<kPolNT, kPolNT, 16>, Shape<kPolPlain, kPolNT, 16, true>>(
         p, conv, dt_bf16, w_bf16, n, s);
   else
     rc = launch_decode<Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, 16, true>,

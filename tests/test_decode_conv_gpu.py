@@ -4,15 +4,17 @@ state is a pure shift of bf16 data and must match bit for bit; SSM states and ou
 the decode tolerances.  Covers the workload's first configuration (B=1, 4/8 heads,
 zero-initialised conv state), the k-head groups 1, 2 and 3 (direct write and the
 last-reader write of the shared q/k conv state), vLLM's dim-first and dim-last conv pools,
-the kernel's packed conv-state path against its per-element path, state lengths 3, 4 and 6, bias, padding and zero-token requests, speculative verify with 2
-to 4 tokens and random accepted counts over consecutive steps, requests the conv rejects,
-and graph replay."""
+the kernel's packed conv-state path against its per-element path, state lengths 3, 4 and 6,
+bias, padding and zero-token requests, speculative verify with 2 to 4 tokens and random
+accepted counts over consecutive steps, requests the conv rejects, and graph replay.  The
+single-token cases run under both state cache policies, which launch different shapes."""
 
 from __future__ import annotations
 
 import pytest
 import torch
 
+from lightdelta_amd import ops
 from lightdelta_amd.workloads import decode_case
 from oracle.decode import expected_decode_conv
 from tests.parity import assert_bf16_outputs, assert_states
@@ -26,6 +28,17 @@ STEP_STATE = dict(rtol=3e-4, atol=3e-6)
 
 def announce(**what):
     print("case:", " ".join(f"{k}={v}" for k, v in what.items()), flush=True)
+
+
+@pytest.fixture(params=["keep", "stream"])
+def policy(request):
+    """Runs the test under each state cache policy: a single-token step launches 4 waves per
+    workgroup (its conv state moved as packed pieces when aligned) under keep and 16 waves
+    (one conv channel per thread) under stream."""
+    saved = ops.state_cache_policy()
+    ops.set_state_cache_policy(request.param)
+    yield request.param
+    ops.set_state_cache_policy(saved)
 
 
 def conv_case(gpu, batch, heads, pool_slots, length=3, dim_last=False, bias=False, seed=0,
@@ -82,15 +95,15 @@ def test_first_workload_config_zero_conv_state(gpu):
 
 
 @pytest.mark.parametrize("heads", [(16, 16), (16, 32), (16, 48)])
-def test_head_groups_and_shared_conv_state(gpu, heads):
-    announce(test="conv_groups", heads=heads)
+def test_head_groups_and_shared_conv_state(gpu, heads, policy):
+    announce(test="conv_groups", heads=heads, policy=policy)
     case = conv_case(gpu, 8, heads, pool_slots=12, seed=heads[1])
     run_and_check(case, 3, torch.Generator().manual_seed(2), label=f"heads {heads}")
 
 
 @pytest.mark.parametrize("dim_last,length,bias", [(False, 4, True), (True, 3, False), (True, 4, True)])
-def test_conv_pool_layouts(gpu, dim_last, length, bias):
-    announce(test="conv_layouts", dim_last=dim_last, length=length, bias=bias)
+def test_conv_pool_layouts(gpu, dim_last, length, bias, policy):
+    announce(test="conv_layouts", dim_last=dim_last, length=length, bias=bias, policy=policy)
     case = conv_case(gpu, 6, (16, 32), pool_slots=10, length=length, dim_last=dim_last,
                      bias=bias, seed=length)
     run_and_check(case, 3, torch.Generator().manual_seed(3), label="layout")
@@ -103,8 +116,8 @@ def test_workload_batch(gpu):
     run_and_check(case, 4, torch.Generator().manual_seed(4), label="b32")
 
 
-def test_padding_and_empty_requests(gpu):
-    announce(test="conv_padding")
+def test_padding_and_empty_requests(gpu, policy):
+    announce(test="conv_padding", policy=policy)
     case = conv_case(gpu, 4, (16, 32), pool_slots=8, seed=6)
     case["slots"][1, 0] = 0  # padding request
     case["cu"].copy_(torch.tensor([0, 1, 2, 2, 3], device=gpu, dtype=torch.int32))  # request 2 empty
@@ -185,12 +198,15 @@ def test_ragged_verify_and_rejected_requests(gpu):
 
 @pytest.mark.parametrize("length,heads,bias", [(3, (16, 32), False), (4, (4, 8), True),
                                                  (3, (16, 48), True)])
-def test_packed_and_per_element_conv_paths_agree(gpu, length, heads, bias):
-    """A dense, 16-byte aligned dim-first conv pool takes the kernel's packed path (each wave
-    moves its channels' columns as 16-byte pieces); the same data one element into a larger
-    buffer (2-byte aligned) takes the per-element path.  Over 3 steps both give the same bits
-    for the conv state, the SSM pool and the outputs, and the packed run matches the oracle."""
-    announce(test="conv_packed_vs_per_element", length=length, heads=heads, bias=bias)
+def test_packed_and_per_element_conv_paths_agree(gpu, length, heads, bias, policy):
+    """Under the keep policy a dense, 16-byte aligned dim-first conv pool takes the kernel's
+    packed path (each wave moves its channels' columns as 16-byte pieces); the same data one
+    element into a larger buffer (2-byte aligned) takes the per-element path.  Under the
+    stream policy both pools take the one-channel-per-thread path, which loads each column as
+    one element and needs no alignment beyond the element's.  Over 3 steps both give the same bits for
+    the conv state, the SSM pool and the outputs, and the aligned run matches the oracle."""
+    announce(test="conv_packed_vs_per_element", length=length, heads=heads, bias=bias,
+             policy=policy)
     case = conv_case(gpu, 8, heads, pool_slots=10, length=length, bias=bias, seed=90 + length)
     dense = case["conv_state"]
     flat = torch.empty(dense.numel() + 1, dtype=dense.dtype, device=dense.device)
@@ -219,9 +235,9 @@ def test_packed_and_per_element_conv_paths_agree(gpu, length, heads, bias):
         pool2.copy_(case["pool"])
 
 
-def test_single_token_long_conv_state(gpu):
+def test_single_token_long_conv_state(gpu, policy):
     """One token per request with a 6-column conv state (the conv runs before the tile)."""
-    announce(test="conv_long_state")
+    announce(test="conv_long_state", policy=policy)
     case = conv_case(gpu, 8, (16, 32), pool_slots=12, length=6, bias=True, seed=50)
     run_and_check(case, 3, torch.Generator().manual_seed(51), label="long state")
 
@@ -252,14 +268,14 @@ def test_verify_graph_replay(gpu):
 
 
 @pytest.mark.parametrize("batch,width,steps", [(32, 1, 32), (8, 3, 16)])
-def test_drift_without_resync(gpu, batch, width, steps):
+def test_drift_without_resync(gpu, batch, width, steps, policy):
     """The GPU carries its own SSM and conv pools for `steps` consecutive steps (no copy of
     the oracle's state back into the GPU pool), the oracle its own trajectory from the same
     inputs: the conv state stays bit-exact, every step's outputs meet the decode tolerance
     and the SSM pool stays within rtol = atol = 2e-3 of the oracle's at the end.  With
     width > 1, every step's accepted count is random in 1..width, so the source state and
     the conv history come from different per-token slots and columns each step."""
-    announce(test="conv_drift", batch=batch, width=width, steps=steps)
+    announce(test="conv_drift", batch=batch, width=width, steps=steps, policy=policy)
     case = conv_case(gpu, batch, (16, 32), pool_slots=batch * width + 2, length=3 + width - 1,
                      bias=width > 1, seed=70 + width, width=width)
     cpu = {k: (None if v is None else v.cpu().clone()) for k, v in case.items()}
