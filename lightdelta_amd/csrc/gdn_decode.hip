@@ -900,7 +900,9 @@ int launch_kernel(const DecodeParams& p, bool dt_bf16, bool w_bf16, uint32_t blo
 }
 
 // One cache policy: the shapes of the single-token step (One), of verify steps (Verify), and
-// of the conv-fused single-token (ConvOne) and verify (ConvVerify) steps, which run 4 waves.
+// of the conv-fused single-token (ConvOne) and verify (ConvVerify) steps.  A conv-fused
+// verify keeps one workgroup per CU: at the register budget of two (64 VGPRs) it spills
+// 108-128 bytes per lane to scratch.
 template <typename One, typename Verify, typename ConvOne, typename ConvVerify>
 int launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
                   uint32_t blocks, hipStream_t stream) {
