@@ -160,7 +160,7 @@ struct ConvIn {
 };
 
 // Fills `in` in place: a ConvIn returned by value was left as a private aggregate, which the
-// backend then placed in LDS (96 bytes a thread for the two channels).
+// backend then placed in LDS (48 bytes a thread per channel).
 template <int Width, int Cols>
 __device__ __forceinline__ void conv_load(const DecodeParams& p, int64_t bos, int n,
                                           int64_t state_at, int channel, ConvIn& in) {
@@ -267,8 +267,8 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 // as 1024 threads x 4 pieces against 5.63 as 256 x 16 (B=128 tiles at random slots,
 // non-temporal loads, system-scope stores).
 // Waves per SIMD the register allocation aims at: 4 (four 4-wave workgroups per CU, or one
-// 16-wave workgroup for the conv-fused verify, whose conv arguments need the SGPRs that a
-// second one would take: at 8 it spilled 44 of them) or 8 (two 16-wave workgroups, the
+// 16-wave workgroup for the conv-fused verify: at 8, two per CU, it spilled 1-6 VGPRs and
+// ran 131.2 against 123.5 us cold at B=64, T=4) or 8 (two 16-wave workgroups, the
 // conv-fused single token included).
 constexpr int waves_per_simd(int waves, int conv_cols, int width) {
   return waves == kWaves || (conv_cols > 0 && width > 1) ? 4 : 8;
@@ -302,8 +302,8 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   static_assert(Waves == kWaves || Waves == 16, "4 or 16 waves");
   // The conv runs before the tile loads for several tokens or more than 4 state columns;
   // one token with 3..4 columns keeps it in registers while the tile streams in.
-  // The conv of a verify step with 16 waves: its inputs load before the tile, the arithmetic
-  // runs while the tile streams in (16 waves leave the registers for both).
+  // The conv of a verify step with 16 waves: one channel per thread (0..255 q/k, 256..383
+  // v), its inputs loaded before the tile and convolved while the tile streams in.
   constexpr bool kConvSplit = Conv && Width > 1 && Waves == 16;
   // One token, 3..4 state columns, 16 waves: one channel per thread (0..255 q/k, 256..383
   // v), its inputs loaded ahead of the tile and convolved while the tile streams in, in 6
@@ -426,22 +426,26 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // the lane layout of the tile (q, k at 4kq.. and 64+4kq..; v of the wave's 32 rows), the
   // MTP token `wave` for the shared staging, and the epilogue inputs of token `wave` ----
   TokenIn in0;
-  // Conv variant: this thread convolves q/k channel `conv_qk` and (tid < 128) v channel
-  // `conv_v`; it loads their input, conv-state columns (clamped to the last column past
-  // conv_len, so every load is in bounds), weights and bias.
-  // (with 16 waves, threads 256.. take the channels of threads tid & 255: their loads are
-  // the same as those threads', so every wave issues the same loads)
+  // Conv variant with 4 waves: this thread convolves q/k channel `conv_qk` and (tid < 128)
+  // v channel `conv_v`; it loads their input, conv-state columns (clamped to the last
+  // column past conv_len, so every load is in bounds), weights and bias.
   const int ctid = tid & (2 * kDim - 1);
   const int conv_qk = ctid < kDim ? q_col + ctid : k_col + (ctid - kDim);
   const int conv_v = v_col + (ctid & (kDim - 1));
   const int64_t conv_slot_at = static_cast<int64_t>(slot[0]) * p.conv_slot;
   int64_t cs_qk_at = conv_slot_at + conv_qk * p.conv_dim_stride;
   int64_t cs_v_at = conv_slot_at + conv_v * p.conv_dim_stride;
+  // kConvSplit: thread tid < 384 convolves one channel, q/k channel tid or v channel
+  // tid - 256 (waves 6..15 load no conv inputs; one channel per thread instead of a q/k and
+  // a v channel on every thread: 128.5 -> 123.5 us cold, 107.8 -> 104.5 hot at B=64, T=4,
+  // 94 -> 69 VGPRs, identical bits)
+  const int conv_ch3 = tid < 2 * kDim ? conv_qk : v_col + ((tid - 2 * kDim) & (kDim - 1));
+  const int64_t cs3_at = conv_slot_at + conv_ch3 * p.conv_dim_stride;
   uint16_t cx_qk = 0, cx_v = 0, cb_qk = 0, cb_v = 0;
   uint16_t cs_qk_raw[kConvLate ? 4 : 1], cs_v_raw[kConvLate ? 4 : 1];
   uint32_t cw_qk[2], cw_v[2];
   uint32_t arrived = 0;  // ticket count before this workgroup's increment (thread 0)
-  ConvIn ci_qk, ci_v;    // kConvSplit: the conv inputs, loaded ahead of the tile
+  ConvIn ci_qk;          // kConvSplit: the channel's conv inputs, loaded ahead of the tile
   // kConvOne16: the thread's channel (state columns as bf16 pairs, input, weights, bias)
   uint32_t c1_st[2] = {0u, 0u}, c1_w[2] = {0u, 0u};
   uint16_t c1_x = 0, c1_bias = 0;
@@ -487,8 +491,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     in0.a = p.a[static_cast<int64_t>(bos) * p.a_row + head];
     in0.b = p.b[static_cast<int64_t>(bos) * p.b_row + head];
   } else if constexpr (kConvSplit) {
-    conv_load<Width, kCols>(p, bos, num_tokens, cs_qk_at, conv_qk, ci_qk);
-    conv_load<Width, kCols>(p, bos, num_tokens, cs_v_at, conv_v, ci_v);
+    if (tid < 3 * kDim) conv_load<Width, kCols>(p, bos, num_tokens, cs3_at, conv_ch3, ci_qk);
   } else if constexpr (kConvOne16) {
     if (tid < 3 * kDim) {  // wave-uniform; every column clamped to the state's last
       const int ch = tid < kDim ? q_col + tid
@@ -605,17 +608,19 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // ---- staging, while the tile streams in ----
   uint16_t v_new_split[kConvSplit ? kCols : 1];
   if constexpr (kConvSplit) {
-    const bool convolves = tid < 2 * kDim;   // wave-uniform
-    uint16_t qk_new[kCols];
-    uint16_t (&v_new)[kCols] = v_new_split;
+    const bool convolves = tid < 3 * kDim;   // wave-uniform
     if (convolves) {
       const bool has_bias = p.conv_bias != nullptr;
+      uint16_t new_st[kCols];
       conv_compute<Width, kCols>(ci_qk, p.conv_len, num_tokens, conv_offset, has_bias,
-                                 &s_conv[0][tid], qk_new);
-      conv_compute<Width, kCols>(ci_v, p.conv_len, num_tokens, conv_offset, has_bias,
-                                 &s_conv[0][2 * kDim + (tid & (kDim - 1))], v_new);
+                                 &s_conv[0][tid], new_st);
+      if (tid < 2 * kDim) {
 #pragma unroll
-      for (int k = 0; k < kCols; ++k) s_conv_new[tid][k] = qk_new[k];
+        for (int k = 0; k < kCols; ++k) s_conv_new[tid][k] = new_st[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < kCols; ++k) v_new_split[k] = new_st[k];
+      }
     }
     // conv outputs visible to every wave; every conv-state read of the workgroup consumed
     // (the shifted v state and the ticket follow the tokens' staging, off its path)
@@ -787,10 +792,10 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   }
   if constexpr (kShared0) lds_barrier();  // every token staged
   if constexpr (kConvSplit) {
-    if (tid < 2 * kDim) {
+    if (tid >= 2 * kDim && tid < 3 * kDim) {
 #pragma unroll
       for (int k = 0; k < kCols; ++k)
-        p.conv_state[cs_v_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new_split[k];
+        p.conv_state[cs3_at + min(k, p.conv_len - 1) * p.conv_len_stride] = v_new_split[k];
     }
     if (p.group > 1 && tid == 0)
       arrived = count_in(&g_conv_ticket[static_cast<int64_t>(slot[0]) * p.num_k_heads + key_head],
