@@ -29,10 +29,14 @@ exact rounding makes the conv output a deterministic function of its inputs.
 
 State layout `[D, S]` per slot (dim-first); a dim-last pool is passed transposed.
 
-Parity of this function is pinned only definitionally (it is checked against
-torch.nn.functional.conv1d with groups = D, against an element loop, and the multi-token
-form against repeated single-token updates); no reference test or fixture covers the conv,
-so conv parity is "unpinned" in the reference's sense.
+The conv arithmetic is pinned: it is checked against torch.nn.functional.conv1d with
+groups = D, against an element loop and a brute-force single rounding to bf16, planted
+mistakes (reversed taps, a shifted window, a dropped bias, a missing SiLU) fail those
+checks, and the multi-token form matches repeated single-token updates.  What stays
+parity unpinned is vLLM's conv-state column convention under num_accepted_tokens (which
+columns hold the history of a step, and the state left after a multi-token step): it is
+restated from vLLM's published algorithm, and no reference test, fixture or vLLM run here
+checks it.
 """
 
 from __future__ import annotations
