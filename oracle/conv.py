@@ -32,11 +32,14 @@ State layout `[D, S]` per slot (dim-first); a dim-last pool is passed transposed
 The conv arithmetic is pinned: it is checked against torch.nn.functional.conv1d with
 groups = D, against an element loop and a brute-force single rounding to bf16, planted
 mistakes (reversed taps, a shifted window, a dropped bias, a missing SiLU) fail those
-checks, and the multi-token form matches repeated single-token updates.  What stays
-parity unpinned is vLLM's conv-state column convention under num_accepted_tokens (which
-columns hold the history of a step, and the state left after a multi-token step): it is
-restated from vLLM's published algorithm, and no reference test, fixture or vLLM run here
-checks it.
+checks, and the multi-token form matches repeated single-token updates.  The standard
+non-speculative layout (S = W - 1 = 3 columns, one token, offset 0) is also checked against
+transformers' Qwen3-Next statement of the update (modeling_qwen3_next.causal_conv1d_update,
+an independent implementation): same state bits, outputs its fp32 conv rounded to bf16.
+What stays parity unpinned is vLLM's column convention for speculative steps and longer
+states (num_accepted_tokens: which columns hold a step's history, the state left after a
+multi-token step): it is restated from vLLM's published algorithm, and no reference test,
+fixture or vLLM run here checks it.
 """
 
 from __future__ import annotations

@@ -1,11 +1,14 @@
-"""Pins the conv oracle (oracle/conv.py) definitionally: against
-torch.nn.functional.conv1d with groups = channels and against an element loop, plus the
-state shift.  No reference test or fixture covers the conv (it lives in vLLM), so the conv
-is "parity unpinned" beyond these definitional checks."""
+"""Pins the conv oracle (oracle/conv.py): against torch.nn.functional.conv1d with groups =
+channels, an element loop and planted mistakes, the multi-token form against repeated
+single-token updates, and the standard non-speculative layout (3 state columns, one token)
+against transformers' independent Qwen3-Next statement of the update.  No reference test or
+fixture covers the conv (it lives in vLLM), so vLLM's column convention for speculative
+steps (num_accepted_tokens, longer states) stays unpinned beyond these checks."""
 
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
 
@@ -166,3 +169,61 @@ def test_next_step_history_ends_at_each_accepted_token(offset):
         shifted = torch.cat([state[:, length:], x.t()], -1)  # planted mistake
         assert not all(torch.equal(shifted[:, n - 1:n + 2], seq[:, n:n + 3])
                        for n in range(1, length + 1))
+
+
+
+def transformers_update():
+    os.environ.setdefault("HF_HUB_OFFLINE", "1")   # the module import needs no network
+    os.environ.setdefault("TRANSFORMERS_OFFLINE", "1")
+    module = pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    return getattr(module.causal_conv1d_update, "__wrapped__", module.causal_conv1d_update)
+
+
+def agrees_with_transformers(update_tokens, seed):
+    """Whether `update_tokens` (conv_update_tokens' signature) matches transformers'
+    statement of the standard layout on random requests: the same new state bit for bit,
+    and outputs that are the bf16 rounding of its fp32 conv (within the fp32 error of two
+    summation orders)."""
+    update = transformers_update()
+    g = torch.Generator().manual_seed(seed)
+    batch, channels = 4, 64
+    for bias in (False, True):
+        x = torch.randn(batch, channels, generator=g).bfloat16()
+        state = torch.randn(batch, channels, 3, generator=g).bfloat16()
+        weight = (torch.randn(channels, 4, generator=g) / 2).bfloat16()
+        b = torch.randn(channels, generator=g).bfloat16() if bias else None
+        hf_state = state.float().clone()
+        hf_out = update(x.float()[:, :, None], hf_state, weight.float(),
+                        None if b is None else b.float(), "silu")[:, :, 0]
+        for r in range(batch):
+            y, new_state = update_tokens(x[r:r + 1], state[r], weight, b, offset=0)
+            if not torch.equal(new_state.float(), hf_state[r]):
+                return False
+            got, ref = y[0].float(), hf_out[r]
+            ulp = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(2.0**-126))) - 7)
+            if not ((got - ref).abs() <= 0.5 * ulp + 1e-5 * ref.abs() + 1e-30).all():
+                return False
+    return True
+
+
+def test_standard_layout_matches_transformers_conv_update():
+    """The standard non-speculative layout (a conv state of width - 1 = 3 columns, one token,
+    no accepted offset) is where vLLM's update and the causal_conv1d semantics coincide:
+    append the token, keep the last 3 columns, convolve the 4-column window, SiLU.
+    transformers' Qwen3-Next layer carries a pure-torch statement of that update
+    (modeling_qwen3_next.causal_conv1d_update, its fallback when no fused kernel is
+    installed), an implementation independent of this oracle, which must agree with it."""
+    assert agrees_with_transformers(conv.conv_update_tokens, seed=11)
+
+
+def test_transformers_check_catches_a_conv_after_the_shift():
+    """A planted mistake -- convolving the shifted state (history [s1, s2, x]) instead of the
+    state before the token -- fails the transformers check."""
+    transformers_update()
+
+    def shifted_first(x, state, weight, bias=None, offset=0):
+        _, new_state = conv.conv_update_tokens(x, state, weight, bias, offset)
+        y, _ = conv.conv_update(x, new_state[None], weight, bias)
+        return y, new_state
+
+    assert not agrees_with_transformers(shifted_first, seed=12)
