@@ -15,9 +15,10 @@
 //   `out`, and prefill_norm_kernel applies the gated RMSNorm in place afterwards, with the
 //   epilogue's arithmetic.
 //
-// Also here: the gated-RMSNorm pass over raw outputs (prefill_norm_kernel, used by the
-// row-split kernels and the chunked form) and the prefill entry points of the C ABI, which
-// choose between this form and the chunked one (prefill_chunked.hip).
+// Also here: the gated-RMSNorm pass over raw outputs (prefill_norm_kernel, or with 16-byte
+// accesses prefill_norm_wide_kernel; used by the row-split kernels and the chunked form) and
+// the prefill entry points of the C ABI, which choose between this form and the chunked one
+// (prefill_chunked.hip).
 #include <mutex>
 
 #include "gdn_step.h"
@@ -405,6 +406,67 @@ __global__ __launch_bounds__(kThreads) void prefill_norm_kernel(const DecodePara
   }
 }
 
+// The same norm with 16-byte accesses, for `gate` rows at 16-byte boundaries (the usual
+// layout; `out` is contiguous): lane (r, c) of a wave holds elements 8c .. 8c + 7 of item
+// 4j + r, j < kNormItems / 4.  The sum of squares runs in wave_sum's order (a lane's four
+// pairs as the four lanes of a quad would sum them, then the 16 lanes of the DPP row as
+// wave_sum's remaining levels), so the results are those of prefill_norm_kernel, bit for bit.
+template <bool WBf16>
+__global__ __launch_bounds__(kThreads) void prefill_norm_wide_kernel(const DecodeParams p,
+                                                                     int num_sequences) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane >> 4;
+  const int c = lane & 15;
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6)) *
+                        kNormItems;
+  const int64_t lo = static_cast<int64_t>(p.cu[0]) * p.num_v_heads;
+  const int64_t hi = static_cast<int64_t>(p.cu[num_sequences]) * p.num_v_heads;
+  if (first >= hi || first + kNormItems <= lo) return;  // no row of this wave (or none at all)
+  constexpr int kLoads = kNormItems / 4;
+  float w[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = load_param(p.norm_weight, 8 * c + e, WBf16);
+  u32x4 raw_bits[kLoads], gate_bits[kLoads];
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) {
+    const int64_t item = min(max(first + 4 * j + r, lo), hi - 1);  // in range; unused ones not stored
+    const int64_t token = item / p.num_v_heads;
+    const int head = static_cast<int>(item - token * p.num_v_heads);
+    raw_bits[j] = *reinterpret_cast<const u32x4*>(p.out + item * kDim + 8 * c);
+    gate_bits[j] = *reinterpret_cast<const u32x4*>(p.gate + token * p.gate_row + head * kDim + 8 * c);
+  }
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) {
+    const int64_t item = first + 4 * j + r;
+    float raw[8], gate[8];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      raw[2 * m] = __builtin_bit_cast(float, raw_bits[j][m] << 16);
+      raw[2 * m + 1] = __builtin_bit_cast(float, raw_bits[j][m] & 0xffff0000u);
+      gate[2 * m] = __builtin_bit_cast(float, gate_bits[j][m] << 16);
+      gate[2 * m + 1] = __builtin_bit_cast(float, gate_bits[j][m] & 0xffff0000u);
+    }
+    float pq[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) pq[m] = fmaf(raw[2 * m + 1], raw[2 * m + 1], raw[2 * m] * raw[2 * m]);
+    float ss = (pq[0] + pq[1]) + (pq[2] + pq[3]);
+    ss += dpp<kDppQuadXor1>(ss);
+    ss += dpp<kDppQuadXor2>(ss);
+    ss += dpp<kDppRowHalfMirror>(ss);
+    ss += dpp<kDppRowMirror>(ss);
+    const float rstd = fast_rsqrt(ss / static_cast<float>(kDim) + p.eps);
+    uint32_t y[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint16_t y0 = f32_to_bf16(((raw[2 * m] * rstd) * w[2 * m]) * silu(gate[2 * m]));
+      const uint16_t y1 = f32_to_bf16(((raw[2 * m + 1] * rstd) * w[2 * m + 1]) * silu(gate[2 * m + 1]));
+      y[m] = y0 | (static_cast<uint32_t>(y1) << 16);
+    }
+    if (item >= lo && item < hi)
+      *reinterpret_cast<u32x4*>(p.out + item * kDim + 8 * c) = u32x4{y[0], y[1], y[2], y[3]};
+  }
+}
+
 // The prefill of ld_gdn_prefill, with the chunked form's workspace passed separately
 // (`workspace`, `workspace_bytes`: the caller's, or the static scratch below).
 int prefill(const ld_gdn_prefill_args& a, void* workspace, int64_t workspace_bytes,
@@ -499,10 +561,15 @@ int prefill(const ld_gdn_prefill_args& a, void* workspace, int64_t workspace_byt
       const int64_t per_block = static_cast<int64_t>(kWaves) * kNormItems;
       const uint32_t norm_grid = static_cast<uint32_t>((items + per_block - 1) / per_block);
       const bool pairs = (reinterpret_cast<uintptr_t>(a.gate) & 3) == 0 && (a.gate_row_stride & 1) == 0;
+      const bool wide = (reinterpret_cast<uintptr_t>(a.gate) & 15) == 0 && (a.gate_row_stride & 7) == 0 &&
+                        (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
 #define LD_NORM_LAUNCH(W, P)                                                                  \
   hipLaunchKernelGGL((prefill_norm_kernel<W, P>), dim3(norm_grid), dim3(kThreads), 0, s, p,  \
                      a.num_sequences)
-      if (w_bf16) {
+      if (wide) {
+        hipLaunchKernelGGL(w_bf16 ? prefill_norm_wide_kernel<true> : prefill_norm_wide_kernel<false>,
+                           dim3(norm_grid), dim3(kThreads), 0, s, p, a.num_sequences);
+      } else if (w_bf16) {
         if (pairs) LD_NORM_LAUNCH(true, true); else LD_NORM_LAUNCH(true, false);
       } else {
         if (pairs) LD_NORM_LAUNCH(false, true); else LD_NORM_LAUNCH(false, false);

@@ -283,6 +283,37 @@ def test_chunked_unaligned_rows_match_aligned_rows(gpu, layout):
     assert torch.equal(case["pool"], ref_pool)
 
 
+@pytest.mark.parametrize("offset", [1, 2])
+def test_norm_paths_agree_on_gate_alignment(gpu, offset):
+    """The gated-RMSNorm pass after the chunked form reads `gate` with 16-byte pieces when
+    its rows are 16-byte aligned, else two elements at a time (4-byte aligned rows) or one:
+    gate rows shifted by `offset` elements (1: one element at a time, 2: pairs) give the
+    aligned run's bits."""
+    announce(test="prefill_norm_gate_alignment", offset=offset)
+    case = prefill_case(gpu, [130, 64, 7, 200, 0, 65], seed=23)
+    pool0 = case["pool"].clone()
+    saved = ops.prefill_algorithm()
+    ops.set_prefill_algorithm("chunked")
+    try:
+        run(case)
+        torch.cuda.synchronize()
+        ref_out, ref_pool = case["out"].clone(), case["pool"].clone()
+        n, hv, d = case["gate"].shape
+        storage = torch.empty(n, hv * d + offset, dtype=torch.bfloat16, device=gpu)
+        gate = storage[:, offset:].unflatten(1, (hv, d))
+        assert gate.data_ptr() % 16 != 0 and gate.stride(1) == d
+        gate.copy_(case["gate"])
+        case["gate"] = gate
+        case["pool"].copy_(pool0)
+        case["out"].zero_()
+        run(case)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_prefill_algorithm(saved)
+    assert torch.equal(case["out"], ref_out)
+    assert torch.equal(case["pool"], ref_pool)
+
+
 def test_rows_outside_every_sequence_are_left_alone(gpu, algorithm):
     """qkv rows that no sequence covers (all sequences empty here, or the tail after the
     last one): their outputs stay as they were; states are written back unchanged."""
