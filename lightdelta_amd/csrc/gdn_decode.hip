@@ -445,7 +445,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   uint16_t cs_qk_raw[kConvLate ? 4 : 1], cs_v_raw[kConvLate ? 4 : 1];
   uint32_t cw_qk[2], cw_v[2];
   uint32_t arrived = 0;  // ticket count before this workgroup's increment (thread 0)
-  ConvIn ci_qk;          // kConvSplit: the channel's conv inputs, loaded ahead of the tile
+  ConvIn ci;             // kConvSplit: the channel's conv inputs, loaded ahead of the tile
   // kConvOne16: the thread's channel (state columns as bf16 pairs, input, weights, bias)
   uint32_t c1_st[2] = {0u, 0u}, c1_w[2] = {0u, 0u};
   uint16_t c1_x = 0, c1_bias = 0;
@@ -491,7 +491,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     in0.a = p.a[static_cast<int64_t>(bos) * p.a_row + head];
     in0.b = p.b[static_cast<int64_t>(bos) * p.b_row + head];
   } else if constexpr (kConvSplit) {
-    if (tid < 3 * kDim) conv_load<Width, kCols>(p, bos, num_tokens, cs3_at, conv_ch3, ci_qk);
+    if (tid < 3 * kDim) conv_load<Width, kCols>(p, bos, num_tokens, cs3_at, conv_ch3, ci);
   } else if constexpr (kConvOne16) {
     if (tid < 3 * kDim) {  // wave-uniform; every column clamped to the state's last
       const int ch = tid < kDim ? q_col + tid
@@ -612,7 +612,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     if (convolves) {
       const bool has_bias = p.conv_bias != nullptr;
       uint16_t new_st[kCols];
-      conv_compute<Width, kCols>(ci_qk, p.conv_len, num_tokens, conv_offset, has_bias,
+      conv_compute<Width, kCols>(ci, p.conv_len, num_tokens, conv_offset, has_bias,
                                  &s_conv[0][tid], new_st);
       if (tid < 2 * kDim) {
 #pragma unroll
