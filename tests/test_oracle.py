@@ -1,11 +1,13 @@
 """Pins the CPU oracle (oracle/gdn.py, oracle/brute.py) before the parity tests rely on it:
 golden vectors written by the reference's own post_conv_gdn, the reference's closed-form
-scalar recurrence, an fp64 brute force, delta-rule invariants, and planted mistakes that
-each of those checks must catch."""
+scalar recurrence, an fp64 brute force, delta-rule invariants, transformers' independent
+Qwen3-Next statement of the recurrence, and planted mistakes that each of those checks must
+catch."""
 
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -194,3 +196,61 @@ def test_planted_mistakes_are_caught(monkeypatch, golden):
         monkeypatch.setattr(gdn, "recur", original_recur)
     _run_with(monkeypatch, "emit", no_raw_rounding, golden_check)
     monkeypatch.setattr(gdn, "emit", original_emit)
+
+
+def transformers_recurrence():
+    os.environ.setdefault("HF_HUB_OFFLINE", "1")   # the module import needs no network
+    os.environ.setdefault("TRANSFORMERS_OFFLINE", "1")
+    module = pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    return module.torch_recurrent_gated_delta_rule
+
+
+def agrees_with_transformers_recurrence(run_fn, seed=31):
+    """Whether `run_fn` (oracle.gdn.run's signature) gives, over 16 tokens at 2 qk / 4 v
+    heads, the final state and pre-rounding outputs of transformers' Qwen3-Next
+    torch_recurrent_gated_delta_rule (an independent fp32 statement of the gated delta
+    rule: state [K, V], l2-normalised q and k, q scaled by K^-1/2, g the log-decay) to
+    rtol 1e-4 / atol 1e-5 (the two sum in different orders)."""
+    rule = transformers_recurrence()
+    g = torch.Generator().manual_seed(seed)
+    batch, tokens, heads, v_heads, dim = 2, 16, 2, 4, 32
+    q = torch.randn(batch, tokens, heads, dim, generator=g).bfloat16()
+    k = torch.randn(batch, tokens, heads, dim, generator=g).bfloat16()
+    v = torch.randn(batch, tokens, v_heads, dim, generator=g).bfloat16()
+    a = torch.randn(batch, tokens, v_heads, generator=g).bfloat16()
+    b = torch.randn(batch, tokens, v_heads, generator=g).bfloat16()
+    a_log = torch.rand(v_heads, generator=g) * 2 - 1
+    dt_bias = torch.randn(v_heads, generator=g)
+    gate = torch.randn(batch, tokens, v_heads, dim, generator=g).bfloat16()
+    weight = torch.randn(dim, generator=g)
+    state0 = torch.randn(batch, v_heads, dim, dim, generator=g) * 0.02   # [B, Hv, V, K]
+    lengths = torch.full((batch,), tokens)
+    _, state, _, (raw_pre, _) = run_fn(q, k, v, a, b, a_log, dt_bias, gate, weight, state0,
+                                       lengths, return_pre=True)
+    group = v_heads // heads
+    log_decay = -a_log.exp() * torch.nn.functional.softplus(a.float() + dt_bias)
+    out, final = rule(q.float().repeat_interleave(group, 2), k.float().repeat_interleave(group, 2),
+                      v.float(), log_decay, b.float().sigmoid(), state0.transpose(-1, -2).clone(),
+                      True, use_qk_l2norm_in_kernel=True)
+    return (torch.allclose(state, final.transpose(-1, -2), rtol=1e-4, atol=1e-5)
+            and torch.allclose(raw_pre, out, rtol=1e-4, atol=1e-5))
+
+
+def test_oracle_matches_transformers_recurrence():
+    """The recurrence and its raw outputs agree with transformers' independent statement."""
+    assert agrees_with_transformers_recurrence(gdn.run)
+
+
+def test_transformers_recurrence_check_catches_late_decay(monkeypatch):
+    """A planted mistake -- the prediction taken from the state before the decay -- fails
+    the check above."""
+    transformers_recurrence()
+
+    def late_decay(state, k_t, v_t, decay_t, beta_t, live):
+        pred = (state * k_t[:, :, None, :]).sum(-1)
+        delta = (v_t - pred) * beta_t[..., None]
+        updated = state * decay_t[..., None, None] + delta[..., None] * k_t[:, :, None, :]
+        return torch.where(live[:, None, None, None], updated, state)
+
+    monkeypatch.setattr(gdn, "recur", late_decay)
+    assert not agrees_with_transformers_recurrence(gdn.run)
