@@ -8,15 +8,16 @@ launch over the batch.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
 
-Timed region: K steps captured in one HIP graph and replayed once, bracketed by
-torch.cuda.synchronize(); inputs are resident in HBM before it starts.  Printed: ONE JSON
-line with steps/s (`value`), tokens/s, the roofline of the decode kernel and a CPU
-baseline.
+Timed region: K steps captured in one HIP graph; each replay is bracketed by
+torch.cuda.synchronize() and timed with HIP events, and the figure is the median of 30 such
+replays (--samples), with their spread beside it; inputs are resident in HBM before it
+starts.  Printed: ONE JSON line with steps/s (`value`), tokens/s, the roofline of the decode
+kernel and a CPU baseline.
 
 Roofline: algorithmic bytes per launch = B * HV * 128 * 128 * 4 B * 2 (read + write of every
 state tile) = 134,217,728 B; `achieved` divides that by the average duration of one launch
 in the timed region (HIP events on the launch stream around the K back-to-back graph
-launches, so inter-kernel gaps count against it).  `traffic` (HBM bytes per launch from
+launches of the median replay, so inter-kernel gaps count against it).  `traffic` (HBM bytes per launch from
 rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the counters' reading on a plain copy of known
 size) is read from profiles/gdn_decode_b32_traffic.json when that measurement exists.
 The headline runs the "keep" state cache policy: the 64 MiB working set of one layer stays
@@ -39,7 +40,9 @@ Further figures in the same line:
                   pool, and the bf16 conv pool;
   stack48         48 layers captured as one HIP graph, batch 128, 1024 slots per layer =
                   96 GiB of state, slot ids reshuffled before every replay, 256 replays timed
-                  end to end (--no-stack skips it).
+                  end to end (--no-stack skips it);
+  stack48_conv    the same stack of conv-fused steps (decode_conv, one launch per layer, each
+                  layer with its own 1024-slot bf16 conv pool), the serving layer's step.
 
 CPU baseline: the reference's packed Torch path (index_select gather, unfused GDN,
 index_copy_ write-back; oracle/decode.py) on every host core this process may use, at the
@@ -90,6 +93,8 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=64)
     p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--samples", type=int, default=REPLAY_SAMPLES,
+                   help="timed replays of the headline and cold graphs (median reported)")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="bound on the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -98,6 +103,8 @@ def parse_args():
     p.add_argument("--no-stack", action="store_true",
                    help="skip the 48-layer, 96 GiB stack measurement")
     p.add_argument("--stack-steps", type=int, default=256)
+    p.add_argument("--no-stack-plain", action="store_true",
+                   help="skip the post-conv 48-layer stack (keep the conv-fused one)")
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-mtp", action="store_true", help="skip the B=64, T=4 verify + commit")
     p.add_argument("--no-copies", action="store_true", help="skip the state-pool copy kernels")
@@ -158,6 +165,30 @@ def timed_replay(graph):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / 1000.0
+
+
+# Timed replays per graph figure: the median is reported (the reference's benchmark takes the
+# median of 30 samples, benchmarks/gdn.py:53-65,73).
+REPLAY_SAMPLES = 30
+
+
+def replay_median(graph, samples=REPLAY_SAMPLES):
+    """Median seconds of `samples` timed replays of graph (each bracketed by
+    synchronisations), and all the samples."""
+    import statistics
+
+    times = [timed_replay(graph) for _ in range(samples)]
+    return statistics.median(times), times
+
+
+def spread_us(times, units):
+    """min / p10 / median / p90 / max of replay times, in us per unit (step or launch)."""
+    ordered = sorted(t * 1e6 / units for t in times)
+    pick = lambda q: ordered[min(len(ordered) - 1, int(q * len(ordered)))]  # noqa: E731
+    return {"samples": len(ordered), "min": round(ordered[0], 3), "p10": round(pick(0.1), 3),
+            "median": round(ordered[len(ordered) // 2] if len(ordered) % 2 else
+                            (ordered[len(ordered) // 2 - 1] + ordered[len(ordered) // 2]) / 2, 3),
+            "p90": round(pick(0.9), 3), "max": round(ordered[-1], 3)}
 
 
 def _cpu_model() -> str:
@@ -239,14 +270,15 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
-def _graph_us(fn, steps):
-    """us per call of `steps` calls of fn captured in one HIP graph, one timed replay."""
+def _graph_us(fn, steps, samples=REPLAY_SAMPLES):
+    """us per call of `steps` calls of fn captured in one HIP graph: the median of `samples`
+    timed replays."""
     import torch
 
     graph = capture(fn, steps)
     graph.replay()
     torch.cuda.synchronize()
-    return timed_replay(graph) * 1e6 / steps
+    return replay_median(graph, samples)[0] * 1e6 / steps
 
 
 def conv_fused(case, op_args, steps, device):
@@ -633,7 +665,7 @@ def copies(device):
     for name, (fn, nbytes) in runs.items():
         graph = capture(fn, launches)
         graph.replay()
-        us = timed_replay(graph) / launches * 1e6
+        us = replay_median(graph, 10)[0] / launches * 1e6
         result[name] = {"us": round(us, 2), "bytes": nbytes, "TBps": round(nbytes / us / 1e6, 3)}
         del graph
     result["workload"] = ("state-pool copies alone: 1024-slot fp32 pool (2 MiB per slot) and "
@@ -649,8 +681,8 @@ def mtp_verify(steps, device):
     [home, s1, s2, s3]; the commit copies the state at a random accepted length a in [1, 4]
     back to the home slot (copy_state from s_(a-1); nothing when a = 1).  `steps`
     (verify, commit) pairs, each with its own accepted lengths drawn on the device
-    beforehand, are captured as one HIP graph and replayed once, timed end to end; the
-    verify launches alone are also timed per launch (HIP events)."""
+    beforehand, are captured as one HIP graph, replayed 10 times, each timed end to end
+    (median reported); the verify launches alone are also timed per launch (HIP events)."""
     import torch
 
     from lightdelta_amd.workloads import decode_case
@@ -686,7 +718,7 @@ def mtp_verify(steps, device):
             verify()
             torch.ops.lightdelta.copy_state(case["pool"], src[step], dst[step])
     graph.replay()  # warm-up replay
-    seconds = timed_replay(graph)
+    seconds = replay_median(graph, 10)[0]
     step_us = seconds / steps * 1e6
     verify_bytes = batch * HV * 65536 * (1 + width)
     commit_bytes = int((accepted > 1).sum()) * HV * 65536 * 2 // steps
@@ -749,23 +781,36 @@ def mtp_verify_cold(device, passes=4):
     }
 
 
-def stack48(steps, device):
+def stack48(steps, device, conv=False):
     """48 GDN decode layers captured as one HIP graph, batch 128, 16 qk / 32 v heads, 1024
     slots per layer (96 GiB fp32 state), stream cache policy; the slot ids (shared by every
     layer) are reshuffled before every replay by a device-to-device copy from a table of
-    random distinct ids.  `steps` replays are timed end to end, reshuffles included."""
+    random distinct ids.  `steps` replays are timed end to end, reshuffles included.
+
+    conv=True runs the serving layer's step instead: each layer is one decode_conv launch
+    (the width-4 causal conv1d + SiLU on the pre-conv activations, fused in front of the
+    GDN step) over its own 1024-slot bf16 conv pool of 3 columns (48 MiB per layer), the
+    conv slot being the request's SSM slot."""
     import torch
 
     from lightdelta_amd import ops
     from lightdelta_amd.workloads import stack_case, stack_layer
 
     layers_n, batch, slots_n = 48, 128, 1024
-    case = stack_case(layers_n, batch, pool_slots=slots_n, seed=5, device=device)
+    conv_len = 3 if conv else 0
+    case = stack_case(layers_n, batch, pool_slots=slots_n, seed=5, device=device,
+                      conv_len=conv_len)
     layers = [stack_layer(case, layer) for layer in range(layers_n)]
 
-    def step():
-        for a in layers:
-            torch.ops.lightdelta.decode(*[a[k] for k in ORDER], 1e-6)
+    if conv:
+        def step():
+            for a in layers:
+                torch.ops.lightdelta.decode_conv(a["qkv"], a["conv_state"], a["conv_weight"],
+                                                 None, *[a[k] for k in ORDER[1:]], 1e-6)
+    else:
+        def step():
+            for a in layers:
+                torch.ops.lightdelta.decode(*[a[k] for k in ORDER], 1e-6)
 
     policy = ops.state_cache_policy()
     ops.set_state_cache_policy("stream")
@@ -789,10 +834,17 @@ def stack48(steps, device):
     end.record()
     torch.cuda.synchronize()
     elapsed = start.elapsed_time(end) / 1000.0
-    step_bytes = layers_n * batch * HV * DIM * DIM * 4 * 2
+    ssm_bytes = layers_n * batch * HV * DIM * DIM * 4 * 2
+    conv_bytes = layers_n * batch * case["qkv"].shape[-1] * conv_len * 2 * 2
+    step_bytes = ssm_bytes + conv_bytes
     rate = steps / elapsed
-    return {
-        "workload": "48-layer stack of decode steps in one HIP graph, batch 128, 16 qk / 32 v "
+    del case, layers, graph
+    torch.cuda.empty_cache()
+    what = ("conv-fused decode steps (decode_conv: causal conv1d + SiLU in front of the GDN "
+            "step, a 3-column bf16 conv pool of 1024 slots per layer)" if conv else
+            "decode steps")
+    result = {
+        "workload": f"48-layer stack of {what} in one HIP graph, batch 128, 16 qk / 32 v "
                     "heads, 1024 slots per layer (96 GiB fp32 state), slot ids reshuffled "
                     "before every replay, stream cache policy",
         "steps": steps,
@@ -803,6 +855,9 @@ def stack48(steps, device):
         "state_TBps": round(step_bytes * rate / 1e12, 3),
         "frac": round(step_bytes * rate / 1e9 / HBM_PEAK_GBS, 4),
     }
+    if conv:
+        result["conv_state_bytes_per_step"] = conv_bytes
+    return result
 
 
 def main():
@@ -858,11 +913,13 @@ def main():
         end.record()
         torch.cuda.synchronize()
         elapsed = start.elapsed_time(end) / 1000.0
+        samples = [elapsed]
     else:
         graph = capture(step, args.steps)
         graph.replay()  # upload + warm the graph (untimed)
         torch.cuda.synchronize()
-        elapsed = timed_replay(graph)  # exactly K steps
+        # each sample times exactly K steps; the median sample is the figure
+        elapsed, samples = replay_median(graph, args.samples)
     ms_per_step = elapsed * 1000.0 / args.steps
     steps_per_s = args.steps / elapsed
 
@@ -892,6 +949,11 @@ def main():
                         + ("eager launches" if args.no_graph else "HIP-graph replay"),
             "batch": BATCH, "qk_heads": H, "v_heads": HV, "head_dim": DIM, "pool_slots": POOL,
         },
+        "timing": {"method": ("eager launches, one timed run" if args.no_graph else
+                              f"one {args.steps}-step HIP graph replayed {len(samples)} times, "
+                              "each replay timed with HIP events between synchronisations; "
+                              "value = K / the median replay"),
+                   "us_per_step": spread_us(samples, args.steps)},
         "tokens_per_s": round(steps_per_s * BATCH, 1),
         "state_TBps": round(STATE_BYTES * steps_per_s / 1e12, 3),
         "roofline": {
@@ -929,7 +991,7 @@ def main():
         cold_graph = capture(cold_pass, max(1, args.steps // 16))
         ops.set_state_cache_policy(keep_policy)
         cold_graph.replay()
-        cold_elapsed = timed_replay(cold_graph)
+        cold_elapsed, cold_samples = replay_median(cold_graph, args.samples)
         cold_steps = 16 * max(1, args.steps // 16)
         cold_rate = cold_steps / cold_elapsed
         result["cold"] = {
@@ -937,9 +999,13 @@ def main():
                         "pool; working set exceeds the 256 MB Infinity Cache",
             "cache_policy": "stream",
             "steps_per_s": round(cold_rate, 1),
+            "us_per_step": spread_us(cold_samples, cold_steps),
             "state_TBps": round(STATE_BYTES * cold_rate / 1e12, 3),
             "frac": round(STATE_BYTES * cold_rate / 1e9 / HBM_PEAK_GBS, 4),
         }
+        # the HBM-bound figure of the same kernel family, beside the cache-resident headline
+        result["roofline"]["cold_frac"] = result["cold"]["frac"]
+        result["roofline"]["cold_us_per_step"] = round(1e6 / cold_rate, 3)
         del big
 
     if not args.no_conv:
@@ -963,7 +1029,10 @@ def main():
     if not args.no_stack:
         case = op_args = graph = None  # noqa: F841  (release the B=32 pools first)
         torch.cuda.empty_cache()
-        result["stack48"] = stack48(args.stack_steps, device)
+        if not args.no_stack_plain:
+            result["stack48"] = stack48(args.stack_steps, device)
+        if not args.no_conv:
+            result["stack48_conv"] = stack48(args.stack_steps, device, conv=True)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 9
+#define LD_ABI_VERSION 10
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -138,11 +138,15 @@ typedef struct ld_conv_args {
  * are invalid for the GDN step, or whose conv columns would fall outside the state
  * (accepted - 1 + 2 > state_len - 1, or accepted > n < state_len), or whose conv slot
  * indices[r, 0] is padding, get zero outputs and leave both pools untouched.  Conv slots
- * must be distinct within one launch, and launches that touch the same slots must be
- * stream-ordered: the v-heads of a k-head group decide which of them writes the shared q/k
- * conv state with one ticket per (slot, k-head) in library-owned device memory (slots x
- * k-heads at most 2^20).  Either violation makes that launch's conv states undefined; the
- * tickets themselves return to their state, so later launches are unaffected.
+ * must be distinct within one launch, and launches that use the same slot id must be
+ * stream-ordered, whatever conv pools they pass: the v-heads of a k-head group decide which
+ * of them writes the shared q/k conv state with one ticket per (slot id, k-head) in
+ * library-owned device memory (slots x k-heads at most 2^20), and the tickets are keyed by
+ * slot id alone, so every layer and every conv pool of the process shares them.  Launches of
+ * different layers on one stream (the serving step, a captured graph of it) are ordered
+ * already; two launches in flight at once on different streams must use disjoint slot ids
+ * even when their pools differ.  Either violation makes those launches' conv states
+ * undefined; the tickets themselves return to their state, so later launches are unaffected.
  * No counterpart in the reference, whose conv is vLLM's causal_conv1d_update run before
  * lightdelta::decode (python/lightdelta/integration/vllm_layer.py:150-172, 199-220).
  */
@@ -282,6 +286,19 @@ int ld_state_scatter(const void* packed, int64_t packed_row_stride_bytes,
 int ld_state_copy(void* pool, int64_t pool_slot_stride_bytes, const int32_t* src_slots,
                   const int32_t* dst_slots, int64_t pairs, int64_t slot_bytes,
                   void* stream);
+
+/*
+ * ld_state_copy that also reports which pairs it rejected: rejected[p] (device int32, one
+ * entry per pair) becomes 1 for a pair rejected for overlapping another live pair, and 0 for
+ * a pair that was copied or is padding.  Every entry is written on every call, so the array
+ * needs no clearing (no memset node in a captured graph); sum it for a count.  slot_bytes
+ * must be positive.  No counterpart in the reference: the commit copy is additive (see
+ * ld_state_copy), and this variant gives callers whose pair sets may chain, swap or share a
+ * destination a graph-safe signal instead of a silent skip.
+ */
+int ld_state_copy_checked(void* pool, int64_t pool_slot_stride_bytes, const int32_t* src_slots,
+                          const int32_t* dst_slots, int64_t pairs, int64_t slot_bytes,
+                          int32_t* rejected, void* stream);
 
 /*
  * Zero-fill `count` whole slots of a pool in place:

@@ -233,6 +233,42 @@ __device__ __forceinline__ void conv_channel_tokens(const DecodeParams& p, int64
 }
 
 
+// The LDS arrays of one gdn_decode_kernel workgroup, as types, so that the kernel declares
+// them from here and the launch can bound their total at compile time (kBytes: every array
+// rounded up to 16 bytes; arrays a kernel does not use are dropped by the compiler, so its
+// static LDS is at most this).  Token 0 staged per wave (or, for verify steps with 16 waves,
+// once), MTP tokens 1..W-1, the raw outputs of every row for the epilogue.
+template <int Width, int ConvCols, int Waves, bool Packed>
+struct DecodeLds {
+  static constexpr bool kShared0 = Width > 1 && Waves == 16;
+  static constexpr bool kConv = ConvCols > 0;
+  static constexpr int kCols = kConv ? ConvCols : 1;
+  using Qk0 = f32x4[kShared0 ? 1 : Waves][2][kDim / 4];  // token 0: q^, k^ in the lane layout
+  using V0 = float[kShared0 ? 1 : Waves][kDim / Waves];  // token 0: v of the wave's rows
+  using Db0 = float[kShared0 ? 1 : Waves][2];            // token 0: decay, beta
+  using Qkt = f32x4[Width][2][kDim / 4];                 // token t (shared staging)
+  using Vt = float[Width][kDim];
+  using Dbt = float[Width][2];
+  using O = float[Width][kDim];                          // raw outputs of token t
+  // Epilogue inputs, parked here once they arrive so that no register holds them through the
+  // recurrence: silu(gate) of token t (written by wave t) and the norm weight (wave 0).
+  using Sg = float[Width][kDim];
+  using W = float[kDim];
+  // Conv variant: bf16 conv outputs of the 256 q/k channels and 128 v channels per token,
+  // and the shifted q/k conv state kept for the end-of-kernel write.
+  using Conv = uint16_t[kConv ? Width : 1][kConv ? 3 * kDim : 2];
+  using ConvNew = uint16_t[kConv && !Packed ? 2 * kDim : 1][kCols];
+  // Packed conv state: per wave, the 16-byte pieces of its q/k ([0]) and v ([1]) channels'
+  // columns, then their shifted columns.
+  using Cpk = u32x4[Packed ? Waves : 1][2][32];
+  static constexpr size_t up16(size_t n) { return (n + 15) / 16 * 16; }
+  static constexpr size_t kBytes =
+      up16(sizeof(Qk0)) + up16(sizeof(V0)) + up16(sizeof(Db0)) + up16(sizeof(Qkt)) +
+      up16(sizeof(Vt)) + up16(sizeof(Dbt)) + up16(sizeof(O)) + up16(sizeof(Sg)) +
+      up16(sizeof(W)) + up16(sizeof(Conv)) + up16(sizeof(ConvNew)) + up16(sizeof(uint32_t)) +
+      up16(sizeof(Cpk));
+};
+
 // Four waves per SIMD (<= 128 VGPRs) keep four workgroups, i.e. four tiles, resident per CU.
 // DtBf16 / WBf16: dt_bias / norm_weight stored as bf16 (else fp32).  LoadPol / StorePol: cache
 // policy bits of the state loads and stores (kPolPlain, kPolNT, kPolSys; never a change of
@@ -391,25 +427,21 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // recurrence): q^ and k^ (128 each), v of the wave's 32 rows, decay and beta.  MTP tokens
   // t >= 1 are staged once, by wave t, in the shared area (one barrier, after chunk 0's
   // token 0).  s_o collects the raw outputs of all rows for the epilogue.
-  __shared__ f32x4 s_qk0[kShared0 ? 1 : Waves][2][kDim / 4];
-  __shared__ float s_v0[kShared0 ? 1 : Waves][kRows];
-  __shared__ float s_db0[kShared0 ? 1 : Waves][2];
-  __shared__ f32x4 s_qkt[Width][2][kDim / 4];
-  __shared__ float s_vt[Width][kDim];
-  __shared__ float s_dbt[Width][2];
-  __shared__ float s_o[Width][kDim];
-  // Epilogue inputs, parked here once they arrive so that no register holds them through the
-  // recurrence: silu(gate) of token t (written by wave t) and the norm weight (wave 0).
-  __shared__ float s_sg[Width][kDim];
-  __shared__ float s_w[kDim];
-  // Conv variant: bf16 conv outputs of the 256 q/k channels and 128 v channels per token,
-  // and the shifted q/k conv state kept for the end-of-kernel write.
-  __shared__ uint16_t s_conv[Conv ? Width : 1][Conv ? 3 * kDim : 2];
-  __shared__ uint16_t s_conv_new[Conv && !Packed ? 2 * kDim : 1][kCols];
+  // (the array types, and what each holds, are DecodeLds')
+  using Lds = DecodeLds<Width, ConvCols, Waves, Packed>;
+  __shared__ typename Lds::Qk0 s_qk0;
+  __shared__ typename Lds::V0 s_v0;
+  __shared__ typename Lds::Db0 s_db0;
+  __shared__ typename Lds::Qkt s_qkt;
+  __shared__ typename Lds::Vt s_vt;
+  __shared__ typename Lds::Dbt s_dbt;
+  __shared__ typename Lds::O s_o;
+  __shared__ typename Lds::Sg s_sg;
+  __shared__ typename Lds::W s_w;
+  __shared__ typename Lds::Conv s_conv;
+  __shared__ typename Lds::ConvNew s_conv_new;
   __shared__ uint32_t s_arrived;
-  // Packed conv state: per wave, the 16-byte pieces of its q/k ([0]) and v ([1]) channels'
-  // columns, then their shifted columns.
-  __shared__ u32x4 s_cpk[Packed ? Waves : 1][2][32];
+  __shared__ typename Lds::Cpk s_cpk;
 
   const int key_head = head / p.group;
   const int kq = lane & 15;
@@ -868,7 +900,10 @@ struct Shape {
   static constexpr int kWaveCount = Waves;
   static constexpr bool kSolo = Solo;
 };
-constexpr size_t kSoloLds = 96 * 1024;
+#ifndef LD_SOLO_LDS_BYTES
+#define LD_SOLO_LDS_BYTES (96 * 1024)
+#endif
+constexpr size_t kSoloLds = LD_SOLO_LDS_BYTES;
 constexpr size_t kLdsPerWorkgroup = 160 * 1024;
 
 // Whether `kernel`'s static LDS plus `dynamic` bytes fit a workgroup (checked once per kernel
@@ -884,7 +919,15 @@ template <typename S, int Width, int ConvCols, bool Packed, bool DtBf16, bool WB
 int launch_one(const DecodeParams& p, uint32_t blocks, hipStream_t stream) {
   constexpr int LP = S::kLoad, SP = S::kStore, W = S::kWaveCount;
   const auto kernel = gdn_decode_kernel<DtBf16, WBf16, LP, SP, Width, ConvCols, W, Packed>;
+  // The declared LDS plus the one-workgroup-per-CU request must fit a workgroup: checked for
+  // every solo shape the library instantiates when it is built.
+  static_assert(!S::kSolo ||
+                    DecodeLds<Width, ConvCols, W, Packed>::kBytes + kSoloLds <= kLdsPerWorkgroup,
+                "decode kernel: its LDS plus the one-workgroup-per-CU request exceed a "
+                "workgroup's 160 KiB");
   if constexpr (S::kSolo) {
+    // Backstop for LDS the compiler adds beyond the declared struct (a private aggregate it
+    // places in LDS): read from the built kernel once.
     static const bool fits = lds_fits(kernel, kSoloLds);
     if (!fits)
       return fail(LD_ERR_LAUNCH, "decode kernel: static LDS plus the one-workgroup-per-CU "

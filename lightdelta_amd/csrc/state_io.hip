@@ -28,6 +28,7 @@ struct CopyParams {
   int64_t slot_stride;    // elements between consecutive slots entries (gather/scatter)
   const int32_t* dst_slots;  // copy only
   const uint8_t* valid;   // gather only; NULL = all valid
+  int32_t* rejected;      // copy only, optional: per pair, 1 = rejected for overlap, else 0
   int64_t rows;           // rows (copy: pairs)
   int64_t vecs;           // 16-byte vectors per row
   uint32_t chunks;        // chunks per row
@@ -70,6 +71,15 @@ __device__ __forceinline__ bool copy_conflicts(const CopyParams& p, uint32_t row
   return __syncthreads_or(conflict);
 }
 
+// Copy: the conflict verdict of live pair `row` (uniform over the workgroup), recorded in
+// the optional per-pair status by the workgroup of the row's first chunk: every pair's entry
+// is written on every call, so the array needs no clearing beforehand.
+__device__ __forceinline__ bool copy_rejected(const CopyParams& p, uint32_t row, uint32_t chunk) {
+  const bool conflict = copy_conflicts(p, row, p.slots[row], p.dst_slots[row]);
+  if (p.rejected != nullptr && chunk == 0 && threadIdx.x == 0) p.rejected[row] = conflict ? 1 : 0;
+  return conflict;
+}
+
 // One workgroup moves one 16 KiB chunk of one row: 4 128-bit loads per thread in flight,
 // then 4 stores.  Every branch below is uniform over the workgroup.
 template <int M>
@@ -94,7 +104,10 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
   } else if (M == kCopy) {
     const int from = p.slots[row];
     const int to = p.dst_slots[row];
-    if (from <= 0 || to <= 0) return;
+    if (from <= 0 || to <= 0) {  // padding pair: not copied, not rejected
+      if (p.rejected != nullptr && chunk == 0 && threadIdx.x == 0) p.rejected[row] = 0;
+      return;
+    }
     src = reinterpret_cast<const u32x4*>(p.src + from * p.src_stride);
     dst = reinterpret_cast<u32x4*>(p.dst + to * p.dst_stride);
   } else {  // zero fill of a slot (reuse by a new sequence)
@@ -122,7 +135,7 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
       v[i] = load_row<M>(src + first + i * kThreads);
     // copy: the pair-conflict scan's loads go out right behind the chunk's (L2 hits), so the
     // scan adds little to the time the stores wait for the chunk anyway
-    if (M == kCopy && copy_conflicts(p, row, p.slots[row], p.dst_slots[row])) return;
+    if (M == kCopy && copy_rejected(p, row, chunk)) return;
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i)
       store_row<M>(v[i], dst + first + i * kThreads);
@@ -134,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void slot_copy_kernel(const CopyParams p)
     const int64_t idx = first + i * kThreads;
     v[i] = load_row<M>(src + (idx < p.vecs ? idx : 0));
   }
-  if (M == kCopy && copy_conflicts(p, row, p.slots[row], p.dst_slots[row])) return;
+  if (M == kCopy && copy_rejected(p, row, chunk)) return;
 #pragma unroll
   for (int i = 0; i < kVecsPerThread; ++i) {
     const int64_t idx = first + i * kThreads;
@@ -207,10 +220,12 @@ extern "C" int ld_state_scatter(const void* packed, int64_t packed_row_stride_by
   return launch("ld_state_scatter", kScatter, p, rows, row_bytes, stream);
 }
 
-extern "C" int ld_state_copy(void* pool, int64_t pool_slot_stride_bytes, const int32_t* src_slots,
-                             const int32_t* dst_slots, int64_t pairs, int64_t slot_bytes,
-                             void* stream) {
-  using namespace ld;
+namespace ld {
+namespace {
+
+int state_copy(const char* what, void* pool, int64_t pool_slot_stride_bytes,
+               const int32_t* src_slots, const int32_t* dst_slots, int64_t pairs,
+               int64_t slot_bytes, int32_t* rejected, void* stream) {
   if (pairs > 0 && (!pool || !src_slots || !dst_slots))
     return fail(LD_ERR_INVALID_ARGUMENT, "ld_state_copy: NULL pointer");
   CopyParams p{};
@@ -220,7 +235,30 @@ extern "C" int ld_state_copy(void* pool, int64_t pool_slot_stride_bytes, const i
   p.dst_stride = pool_slot_stride_bytes;
   p.slots = src_slots;
   p.dst_slots = dst_slots;
-  return launch("ld_state_copy", kCopy, p, pairs, slot_bytes, stream);
+  p.rejected = rejected;
+  return launch(what, kCopy, p, pairs, slot_bytes, stream);
+}
+
+}  // namespace
+}  // namespace ld
+
+extern "C" int ld_state_copy(void* pool, int64_t pool_slot_stride_bytes, const int32_t* src_slots,
+                             const int32_t* dst_slots, int64_t pairs, int64_t slot_bytes,
+                             void* stream) {
+  return ld::state_copy("ld_state_copy", pool, pool_slot_stride_bytes, src_slots, dst_slots,
+                        pairs, slot_bytes, nullptr, stream);
+}
+
+extern "C" int ld_state_copy_checked(void* pool, int64_t pool_slot_stride_bytes,
+                                     const int32_t* src_slots, const int32_t* dst_slots,
+                                     int64_t pairs, int64_t slot_bytes, int32_t* rejected,
+                                     void* stream) {
+  if (pairs > 0 && rejected == nullptr)
+    return ld::fail(LD_ERR_INVALID_ARGUMENT, "ld_state_copy_checked: rejected is NULL");
+  if (pairs > 0 && slot_bytes == 0)  // nothing would launch, so no status would be written
+    return ld::fail(LD_ERR_INVALID_ARGUMENT, "ld_state_copy_checked: slot_bytes must be positive");
+  return ld::state_copy("ld_state_copy_checked", pool, pool_slot_stride_bytes, src_slots,
+                        dst_slots, pairs, slot_bytes, rejected, stream);
 }
 
 extern "C" int ld_state_zero(void* pool, int64_t pool_slot_stride_bytes, const int32_t* slots,

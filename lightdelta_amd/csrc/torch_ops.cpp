@@ -291,7 +291,7 @@ void scatter_slots(const at::Tensor& packed, const at::Tensor& slots, at::Tensor
   scatter(packed, slots, pool);
 }
 
-void copy_state(at::Tensor pool, const at::Tensor& src, const at::Tensor& dst) {
+void check_copy(const at::Tensor& pool, const at::Tensor& src, const at::Tensor& dst) {
   TORCH_CHECK(pool.is_cuda() && pool.dim() >= 1 && dense_inner(pool),
               "pool must be a CUDA tensor with dense inner dimensions");
   for (const at::Tensor* t : {&src, &dst})
@@ -299,6 +299,10 @@ void copy_state(at::Tensor pool, const at::Tensor& src, const at::Tensor& dst) {
                     t->is_contiguous(),
                 "src and dst must be contiguous CUDA int32 vectors");
   TORCH_CHECK(src.numel() == dst.numel(), "src and dst must have the same length");
+}
+
+void copy_state(at::Tensor pool, const at::Tensor& src, const at::Tensor& dst) {
+  check_copy(pool, src, dst);
   if (src.numel() == 0) return;
   const c10::DeviceGuard guard(pool.device());
   const int rc = ld_state_copy(pool.data_ptr(),
@@ -306,6 +310,23 @@ void copy_state(at::Tensor pool, const at::Tensor& src, const at::Tensor& dst) {
                                static_cast<const int32_t*>(src.data_ptr()),
                                static_cast<const int32_t*>(dst.data_ptr()), src.numel(),
                                row_bytes(pool), stream_of(pool));
+  TORCH_CHECK(rc == LD_OK, ld_last_error());
+}
+
+void copy_state_checked(at::Tensor pool, const at::Tensor& src, const at::Tensor& dst,
+                        at::Tensor rejected) {
+  check_copy(pool, src, dst);
+  TORCH_CHECK(rejected.device() == pool.device() && rejected.scalar_type() == at::kInt &&
+                  rejected.dim() == 1 && rejected.is_contiguous() &&
+                  rejected.numel() == src.numel(),
+              "rejected must be a contiguous CUDA int32 vector with one entry per pair");
+  if (src.numel() == 0) return;
+  TORCH_CHECK(row_bytes(pool) > 0, "pool slots must not be empty");
+  const c10::DeviceGuard guard(pool.device());
+  const int rc = ld_state_copy_checked(
+      pool.data_ptr(), pool.stride(0) * static_cast<int64_t>(pool.element_size()),
+      static_cast<const int32_t*>(src.data_ptr()), static_cast<const int32_t*>(dst.data_ptr()),
+      src.numel(), row_bytes(pool), static_cast<int32_t*>(rejected.data_ptr()), stream_of(pool));
   TORCH_CHECK(rc == LD_OK, ld_last_error());
 }
 
@@ -334,6 +355,7 @@ TORCH_LIBRARY_IMPL(lightdelta, CUDA, m) {
   m.impl("gather_slots", &gather_slots);
   m.impl("scatter_slots", &scatter_slots);
   m.impl("copy_state", &copy_state);
+  m.impl("copy_state_checked", &copy_state_checked);
   m.impl("zero_slots", &zero_slots);
 }
 

@@ -13,6 +13,11 @@ Additive ops (no reference counterpart):
                                         a pair that overlaps another (its source another's
                                         destination, its destination another's source or
                                         destination) is rejected and writes nothing
+  copy_state_checked(pool, src, dst, rejected)
+                                        copy_state that also writes, per pair, 1 to
+                                        rejected (int32 [pairs]) if it was rejected for
+                                        overlap, else 0 (every entry on every call, so no
+                                        clearing is needed; graph-safe)
   zero_slots(pool, slots)               zero whole slots in place (a slot reused by a new
                                         sequence), any dtype, padding slot <= 0 skipped
   decode_conv(mixed_qkv, conv_state, conv_weight, conv_bias, <decode args without qkv>)
@@ -33,8 +38,8 @@ Additive ops (no reference counterpart):
 
 Every kernel launches on the caller's current stream and reads no device memory on the host,
 so it can be captured in a HIP graph.  None allocates, except prefill's chunked form, which
-keeps one workspace per device and stream for later calls (release_prefill_workspaces frees
-them).  The kernels of every op but prefill are C++ (csrc/torch_ops.cpp,
+keeps one workspace per device and stream for later eager calls (release_prefill_workspaces
+frees them) and gives a call under graph capture a workspace the graph keeps.  The kernels of every op but prefill are C++ (csrc/torch_ops.cpp,
 liblightdelta_torch.so); the check_* functions below restate their argument checks so they
 can run without a GPU.
 """
@@ -58,6 +63,9 @@ SCHEMAS = {
     "gather_state": "gather_state(Tensor pool, Tensor slots, Tensor valid, Tensor(o!) out) -> ()",
     "scatter_state": "scatter_state(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
     "copy_state": "copy_state(Tensor(p!) pool, Tensor src, Tensor dst) -> ()",
+    "copy_state_checked": (
+        "copy_state_checked(Tensor(p!) pool, Tensor src, Tensor dst, Tensor(r!) rejected) -> ()"
+    ),
     "zero_slots": "zero_slots(Tensor(p!) pool, Tensor slots) -> ()",
     "prefill": (
         "prefill(Tensor qkv, Tensor a, Tensor b, Tensor a_log, Tensor dt_bias, Tensor slots, "
@@ -280,15 +288,25 @@ def prefill_algorithm() -> str:
     return next(k for k, v in _PREFILL_ALGORITHMS.items() if v == _prefill_algorithm)
 
 
-# Chunked-prefill workspaces, one per (device, stream), kept and grown to the largest prefill
-# seen (ld_gdn_prefill_workspace_bytes: 115,712 bytes per 64-token chunk and v-head, e.g.
-# 2.0 GB for 32 x 1024 tokens at 32 v-heads).  Calls on one stream run in order, so they can
-# share one; the buffer comes from torch's allocator once (under a graph capture, from the
-# graph's pool) instead of on every call.  release_prefill_workspaces() drops them.
+# Chunked-prefill workspaces of eager calls, one per (device, stream), kept and grown to the
+# largest prefill seen (ld_gdn_prefill_workspace_bytes: 115,712 bytes per 64-token chunk and
+# v-head, e.g. 2.0 GB for 32 x 1024 tokens at 32 v-heads).  Eager calls on one stream run in
+# order, so they can share one; the buffer comes from torch's allocator once instead of on
+# every call.  release_prefill_workspaces() drops them.
+#
+# A call under HIP-graph capture never touches this cache: the graph records the raw pointer
+# and writes through it on every replay, so its workspace must stay the graph's for the
+# graph's lifetime.  It gets a buffer of its own, allocated during the capture, which torch
+# takes from the graph's private memory pool; that memory stays reserved for the graph's
+# replays after the tensor is dropped (later allocations of the same capture may reuse it,
+# which is stream-ordered after this call), and no eager call, cache growth or release can
+# hand it to other tensors while the graph exists.
 _workspaces: dict = {}
 
 
 def _prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
     key = (device.index, _stream(device))
     buffer = _workspaces.get(key)
     if buffer is None or buffer.numel() < nbytes:
@@ -299,8 +317,8 @@ def _prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 
 def release_prefill_workspaces() -> None:
-    """Frees the cached chunked-prefill workspaces (the next chunked prefill allocates
-    again)."""
+    """Frees the cached chunked-prefill workspaces of eager calls (the next chunked prefill
+    allocates again).  Captured graphs hold workspaces of their own and are unaffected."""
     _workspaces.clear()
 
 
@@ -441,6 +459,15 @@ def check_copy(pool, src, dst):
     _require(src.numel() == dst.numel(), "src and dst must have the same length")
 
 
+def check_copy_checked(pool, src, dst, rejected):
+    check_copy(pool, src, dst)
+    _require(
+        rejected.device == pool.device and rejected.dtype == torch.int32 and rejected.dim() == 1
+        and rejected.is_contiguous() and rejected.numel() == src.numel(),
+        "rejected must be a contiguous CUDA int32 vector with one entry per pair",
+    )
+
+
 def check_zero(pool, slots):
     _require(
         _is_gpu(pool) and pool.dim() >= 1 and _dense_inner(pool),
@@ -461,7 +488,7 @@ def check_zero(pool, slots):
 # path is on every decode step.  prefill's kernel is the Python function below (it keeps the
 # chunked form's workspace cache and the algorithm choice).
 _CXX_KERNELS = ("decode", "decode_conv", "gather_state", "scatter_state", "gather_slots",
-                "scatter_slots", "copy_state", "zero_slots")
+                "scatter_slots", "copy_state", "copy_state_checked", "zero_slots")
 _IMPLS = {
     "prefill": _prefill_impl,
 }

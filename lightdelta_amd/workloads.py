@@ -78,11 +78,16 @@ def decode_case(
 
 
 def stack_case(layers: int, batch: int, *, num_k_heads: int = 16, num_v_heads: int = 32,
-               pool_slots: int = 1024, seed: int = 0, device="cuda") -> dict:
+               pool_slots: int = 1024, seed: int = 0, device="cuda", conv_len: int = 0) -> dict:
     """A stack of `layers` GDN decode layers, one token per request: per-layer activations,
     parameters and state pool (one [layers, pool_slots, HV, 128, 128] fp32 tensor), and one
     slots/cu/accepted set shared by every layer (a request keeps its slot id in every
-    layer).  Same distributions as decode_case; generated on `device`."""
+    layer).  Same distributions as decode_case; generated on `device`.
+
+    conv_len > 0 adds each layer's causal-conv parameters for the conv-fused step (the
+    activations are then its pre-conv input): conv_state [layers, pool_slots, conv_dim,
+    conv_len] bf16 ~ N(0, 1), dim-first as vLLM allocates it, and conv_weight [layers,
+    conv_dim, 4] bf16 ~ N(0, 1/4); no bias.  A request's conv slot is its SSM slot."""
     dev = torch.device(device)
     gen = torch.Generator(device=dev).manual_seed(seed)
     qkv_cols = (2 * num_k_heads + num_v_heads) * HEAD_DIM
@@ -94,7 +99,7 @@ def stack_case(layers: int, batch: int, *, num_k_heads: int = 16, num_v_heads: i
         pool[layer].normal_(0.0, 0.02, generator=gen)
     cpu_gen = torch.Generator().manual_seed(seed)
     slots = (torch.randperm(pool_slots - 1, generator=cpu_gen)[:batch] + 1).to(torch.int32)
-    return dict(
+    case = dict(
         qkv=qkvz[:, :, :qkv_cols],
         a=ba[:, :, num_v_heads:],
         b=ba[:, :, :num_v_heads],
@@ -108,6 +113,16 @@ def stack_case(layers: int, batch: int, *, num_k_heads: int = 16, num_v_heads: i
         weight=1 + 0.1 * torch.randn(layers, HEAD_DIM, generator=gen, device=dev),
         out=torch.zeros(layers, batch, num_v_heads, HEAD_DIM, dtype=torch.bfloat16, device=dev),
     )
+    if conv_len > 0:
+        conv_state = torch.empty(layers, pool_slots, qkv_cols, conv_len, dtype=torch.bfloat16,
+                                 device=dev)
+        for layer in range(layers):  # one layer at a time: the fp32 draw is 4 x the pool
+            conv_state[layer] = torch.randn(pool_slots, qkv_cols, conv_len, generator=gen,
+                                            device=dev).bfloat16()
+        case["conv_state"] = conv_state
+        case["conv_weight"] = (torch.randn(layers, qkv_cols, 4, generator=gen, device=dev)
+                               / 2).bfloat16()
+    return case
 
 
 STACK_SHARED = ("slots", "cu", "accepted")

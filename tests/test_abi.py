@@ -25,7 +25,8 @@ def test_header_declares_the_entry_points():
         "ld_gdn_decode", "ld_gdn_decode_conv", "ld_gdn_prefill", "ld_gdn_prefill_static",
         "ld_gdn_prefill_workspace_bytes", "ld_gdn_prefill_auto_chunked", "ld_state_gather",
         "ld_state_scatter",
-        "ld_state_copy", "ld_state_zero", "ld_last_error", "ld_abi_version",
+        "ld_state_copy", "ld_state_copy_checked", "ld_state_zero", "ld_last_error",
+        "ld_abi_version",
     }
 
 
@@ -76,6 +77,7 @@ def test_empty_work_is_a_no_op():
     args.eps = 1e-6
     assert lib.ld_gdn_decode(ctypes.byref(args), None) == 0
     assert lib.ld_state_copy(None, 0, None, None, 0, 2048, None) == 0
+    assert lib.ld_state_copy_checked(None, 0, None, None, 0, 2048, None, None) == 0
     assert lib.ld_state_zero(None, 0, None, 0, 2048, None) == 0
     assert lib.ld_state_gather(None, 0, None, 1, None, None, 0, 2048, 0, None) == 0
 
@@ -109,6 +111,14 @@ def test_copy_rejects_misaligned_rows():
     assert code == 1 and "16-byte aligned" in lib.ld_last_error().decode()
     code = lib.ld_state_zero(16, 2048, 32, 1, 24, None)
     assert code == 1 and "16-byte aligned" in lib.ld_last_error().decode()
+
+
+def test_checked_copy_needs_a_status_array_and_nonempty_slots():
+    lib = _lib.load()
+    assert lib.ld_state_copy_checked(16, 2048, 32, 48, 1, 2048, None, None) == 1
+    assert b"rejected is NULL" in lib.ld_last_error()
+    assert lib.ld_state_copy_checked(16, 2048, 32, 48, 1, 0, 64, None) == 1
+    assert b"slot_bytes must be positive" in lib.ld_last_error()
 
 
 def test_prefill_rejects_bad_arguments_without_launching():

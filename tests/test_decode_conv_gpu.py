@@ -267,7 +267,7 @@ def test_verify_graph_replay(gpu):
         case["pool"].copy_(expected[1].to(case["pool"].device))
 
 
-@pytest.mark.parametrize("batch,width,steps", [(32, 1, 32), (8, 3, 16)])
+@pytest.mark.parametrize("batch,width,steps", [(32, 1, 64), (8, 3, 16)])
 def test_drift_without_resync(gpu, batch, width, steps, policy):
     """The GPU carries its own SSM and conv pools for `steps` consecutive steps (no copy of
     the oracle's state back into the GPU pool), the oracle its own trajectory from the same

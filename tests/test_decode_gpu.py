@@ -182,11 +182,13 @@ def test_invalid_and_empty_requests(gpu, policy):
     torch.cuda.synchronize()
 
 
-def test_workload_64_steps(gpu):
+def test_workload_64_steps(gpu, policy):
     """Qwen3-Next-shape layer: B=32, 16 qk / 32 v heads, 256-slot pool, random distinct
     slots, 64 consecutive in-place steps.  States and every step's outputs against the
-    oracle's own 64-step trajectory (the reference's packed Torch path)."""
-    announce(test="workload_64_steps")
+    oracle's own 64-step trajectory (the reference's packed Torch path).  Under each cache
+    policy: keep runs the headline kernel (4 waves, plain loads and stores), stream the
+    16-wave kernel."""
+    announce(test="workload_64_steps", policy=policy)
     case = decode_case(32, 1, pool_slots=256, seed=0, device=gpu)
     cpu = {k: v.cpu().clone() for k, v in case.items()}
     gen = torch.Generator().manual_seed(11)
@@ -205,7 +207,7 @@ def test_workload_64_steps(gpu):
         flips += assert_bf16_outputs(case["out"], cpu["out"], raw[2], label=f"step {step}")["flips"]
         del before
     assert_states(case["pool"], cpu["pool"], label="pool after 64 steps")
-    print(f"rounding flips over 64 steps: {flips} of {64 * case['out'].numel()}")
+    print(f"rounding flips over 64 steps ({policy}): {flips} of {64 * case['out'].numel()}")
 
 
 def test_mtp_verify_and_commit(gpu):

@@ -22,7 +22,7 @@ def decode_args(device, n=4, h=16, hv=32, width=1, slots=10):
 
     qkvz = t(n, (2 * h + hv) * 128 + hv * 128)
     ba = t(n, 2 * hv)
-    return dict(
+    args = dict(
         qkv=qkvz[:, : (2 * h + hv) * 128], a=ba[:, hv:], b=ba[:, :hv],
         a_log=t(hv, dtype=torch.float32), dt_bias=t(hv, dtype=torch.float32),
         indices=t(n // width, width, dtype=torch.int32), cu=t(n // width + 1, dtype=torch.int32),
@@ -30,6 +30,29 @@ def decode_args(device, n=4, h=16, hv=32, width=1, slots=10):
         gate=qkvz[:, (2 * h + hv) * 128:].view(n, hv, 128), weight=t(128), out=t(n, hv, 128),
         eps=1e-6,
     )
+    if torch.device(device).type != "meta":
+        # Metadata that is safe even if a case were launched: every request's slots are
+        # padding, so a kernel would only zero its outputs.
+        args["indices"].zero_()
+        args["cu"].copy_(torch.arange(0, n + 1, width, dtype=torch.int32))
+        args["accepted"].fill_(1)
+    return args
+
+
+def conv_args(device, length=3, bias=True, **kw):
+    """decode_conv's arguments: decode_args with qkv as the pre-conv activations, then the conv
+    pool [slots, conv_dim, length], weight [conv_dim, 4] and bias [conv_dim], all bf16."""
+    args = decode_args(device, **kw)
+    conv_dim = args["qkv"].shape[1]
+    slots = args["state"].shape[0]
+    conv = dict(
+        mixed_qkv=args.pop("qkv"),
+        conv_state=torch.zeros(slots, conv_dim, length, dtype=torch.bfloat16, device=device),
+        conv_weight=torch.zeros(conv_dim, 4, dtype=torch.bfloat16, device=device),
+        conv_bias=(torch.zeros(conv_dim, dtype=torch.bfloat16, device=device) if bias else None),
+    )
+    conv.update(args)
+    return conv
 
 
 def check(args):
@@ -84,6 +107,65 @@ def test_decode_validation_messages(meta, mutate, message):
     mutate(args, meta)
     with pytest.raises(RuntimeError, match=message):
         check(args)
+
+
+# Invalid decode_conv arguments (on top of decode's) and the message each must raise.
+CONV_DIM = (2 * 16 + 32) * 128
+CONV_STATE_MSG = r"conv_state must be CUDA BF16 \[slots, conv_dim, 3..8\]"
+CONV_WEIGHT_MSG = r"conv_weight must be contiguous CUDA BF16 \[conv_dim, 4\]"
+CONV_BIAS_MSG = r"conv_bias must be contiguous CUDA BF16 \[conv_dim\]"
+CONV_CASES = [
+    (lambda d, m: d.update(conv_state=torch.zeros(10, CONV_DIM, 2, dtype=torch.bfloat16, device=m)),
+     CONV_STATE_MSG),
+    (lambda d, m: d.update(conv_state=torch.zeros(10, CONV_DIM, 9, dtype=torch.bfloat16, device=m)),
+     CONV_STATE_MSG),
+    (lambda d, m: d.update(conv_state=d["conv_state"].float()), CONV_STATE_MSG),
+    (lambda d, m: d.update(conv_state=torch.zeros(10, CONV_DIM - 128, 3, dtype=torch.bfloat16,
+                                                  device=m)), CONV_STATE_MSG),
+    (lambda d, m: d.update(conv_state=d["conv_state"][:, :, 0]), CONV_STATE_MSG),
+    (lambda d, m: d.update(conv_weight=d["conv_weight"].float()), CONV_WEIGHT_MSG),
+    (lambda d, m: d.update(conv_weight=torch.zeros(4, CONV_DIM, dtype=torch.bfloat16,
+                                                   device=m).t()), CONV_WEIGHT_MSG),
+    (lambda d, m: d.update(conv_weight=torch.zeros(CONV_DIM, 3, dtype=torch.bfloat16, device=m)),
+     CONV_WEIGHT_MSG),
+    (lambda d, m: d.update(conv_bias=torch.zeros(CONV_DIM - 1, dtype=torch.bfloat16, device=m)),
+     CONV_BIAS_MSG),
+    (lambda d, m: d.update(conv_bias=d["conv_bias"].float()), CONV_BIAS_MSG),
+    (lambda d, m: d.update(conv_bias=torch.zeros(2 * CONV_DIM, dtype=torch.bfloat16,
+                                                 device=m)[::2]), CONV_BIAS_MSG),
+    # decode's own checks still apply to the pre-conv activations
+    (lambda d, m: d.update(mixed_qkv=d["mixed_qkv"].float()), "qkv must be CUDA BF16"),
+]
+
+
+def test_decode_conv_valid_arguments(meta):
+    assert ops.check_decode_conv(*conv_args(meta).values()) == (16, 32)
+    assert ops.check_decode_conv(*conv_args(meta, length=8, bias=False).values()) == (16, 32)
+    dim_last = conv_args(meta)
+    dim_last["conv_state"] = torch.zeros(10, 3, CONV_DIM, dtype=torch.bfloat16,
+                                         device=meta).transpose(1, 2)
+    assert ops.check_decode_conv(*dim_last.values()) == (16, 32)
+
+
+@pytest.mark.parametrize("mutate,message", CONV_CASES)
+def test_decode_conv_validation_messages(meta, mutate, message):
+    args = conv_args(meta)
+    mutate(args, meta)
+    with pytest.raises(RuntimeError, match=message):
+        ops.check_decode_conv(*args.values())
+
+
+def test_copy_state_checked_validation_messages(meta):
+    pool = torch.empty(8, 4, 128, 128, device=meta)
+    src = torch.empty(3, dtype=torch.int32, device=meta)
+    ops.check_copy_checked(pool, src, src, torch.empty(3, dtype=torch.int32, device=meta))
+    for bad in (torch.empty(2, dtype=torch.int32, device=meta),
+                torch.empty(3, dtype=torch.int64, device=meta),
+                torch.empty(6, dtype=torch.int32, device=meta)[::2]):
+        with pytest.raises(RuntimeError, match="rejected must be a contiguous CUDA int32 vector"):
+            ops.check_copy_checked(pool, src, src, bad)
+    with pytest.raises(RuntimeError, match="same length"):
+        ops.check_copy_checked(pool, src, src[:2], src)
 
 
 def test_state_io_validation_messages(meta):
@@ -164,6 +246,39 @@ def test_state_op_kernel_validation_messages(gpu):
         ops_.zero_slots(pool, slots.long())
     with pytest.raises(RuntimeError, match="dense inner dimensions"):
         ops_.zero_slots(torch.zeros(8, 4, 128, 256, device=gpu)[..., :128], slots)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mutate,message", CONV_CASES + [
+    # a weight view 2 bytes into a buffer: contiguous, but not 8-byte aligned
+    (lambda d, m: d.update(conv_weight=torch.zeros(CONV_DIM * 4 + 1, dtype=torch.bfloat16,
+                                                   device=m)[1:].view(CONV_DIM, 4)),
+     CONV_WEIGHT_MSG)])
+def test_decode_conv_kernel_validation_messages(gpu, mutate, message):
+    """The decode_conv cases through torch.ops.lightdelta.decode_conv on the GPU: the C++
+    kernel (csrc/torch_ops.cpp) raises the same messages, before any launch (the metadata
+    marks every request as padding, so even a launch would only zero the outputs)."""
+    args = conv_args(gpu)
+    mutate(args, gpu)
+    with pytest.raises(RuntimeError, match=message):
+        torch.ops.lightdelta.decode_conv(*args.values())
+    torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_copy_state_checked_kernel_validation_messages(gpu):
+    pool = torch.zeros(8, 4, 128, 128, device=gpu)
+    src = torch.tensor([1, -1, 3], dtype=torch.int32, device=gpu)
+    dst = torch.tensor([2, 4, -1], dtype=torch.int32, device=gpu)
+    for bad in (torch.zeros(2, dtype=torch.int32, device=gpu),
+                torch.zeros(3, dtype=torch.int64, device=gpu),
+                torch.zeros(6, dtype=torch.int32, device=gpu)[::2]):
+        with pytest.raises(RuntimeError, match="rejected must be a contiguous CUDA int32 vector"):
+            torch.ops.lightdelta.copy_state_checked(pool, src, dst, bad)
+    with pytest.raises(RuntimeError, match="same length"):
+        torch.ops.lightdelta.copy_state_checked(pool, src, dst[:2].contiguous(),
+                                                torch.zeros(3, dtype=torch.int32, device=gpu))
     torch.cuda.synchronize()
 
 

@@ -9,7 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from lightdelta_amd import ops
+from lightdelta_amd import _lib, ops
 from lightdelta_amd.workloads import decode_case
 from oracle.decode import expected_prefill
 from tests.parity import assert_bf16_outputs, assert_states
@@ -158,6 +158,51 @@ def test_prefill_graph_capture(gpu, algorithm):
         torch.cuda.synchronize()
         assert_bf16_outputs(case["out"], exp_out, pre, label=f"replay {replay}")
         assert_states(case["pool"], exp_pool, label=f"replay {replay}")
+
+
+def test_captured_chunked_workspace_outlives_the_eager_cache(gpu):
+    """The chunked form under graph capture on a stream whose eager workspace is cached: after
+    the capture, a larger eager prefill on that stream (which replaces the cached buffer) and
+    release_prefill_workspaces() (which drops it), new tensors of the freed sizes are
+    allocated on that stream and filled; the replays must still match the oracle and leave those tensors
+    untouched (the graph's workspace is its own, not the cache's)."""
+    announce(test="prefill_graph_workspace")
+    saved = ops.prefill_algorithm()
+    ops.set_prefill_algorithm("chunked")
+    try:
+        case = prefill_case(gpu, [100, 70], seed=11)
+        big = prefill_case(gpu, [300, 260, 200], seed=12)
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            run(case)  # eager: caches a workspace for this stream
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            run(case)
+        with torch.cuda.stream(stream):
+            run(big)  # eager, larger: the cached buffer is replaced
+        torch.cuda.synchronize()
+        ops.release_prefill_workspaces()
+        lib = _lib.load()
+        sizes = [lib.ld_gdn_prefill_workspace_bytes(170, 2, 32)] * 4 + \
+            [lib.ld_gdn_prefill_workspace_bytes(760, 3, 32)] * 2
+        with torch.cuda.stream(stream):  # the allocator reuses a stream's own freed blocks
+            fillers = [torch.full((n,), 0x5A, dtype=torch.uint8, device=gpu) for n in sizes]
+        torch.cuda.synchronize()
+        gen = torch.Generator().manual_seed(13)
+        for replay in range(3):
+            case["slots"].copy_((torch.randperm(case["pool"].shape[0] - 1, generator=gen)[:2] + 1)
+                                .to(torch.int32))
+            exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6,
+                                                      return_pre=True)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert_bf16_outputs(case["out"], exp_out, pre, label=f"replay {replay}")
+            assert_states(case["pool"], exp_pool, label=f"replay {replay}")
+            for i, f in enumerate(fillers):
+                assert bool((f == 0x5A).all()), f"replay {replay}: filler {i} was overwritten"
+    finally:
+        ops.set_prefill_algorithm(saved)
 
 
 @pytest.mark.parametrize("sequences", [16, 32])

@@ -95,6 +95,55 @@ def test_copy_state_overlapping_pairs(gpu):
     assert np.array_equal(expected[[2, 3, 4, 5, 6, 12]], host[[2, 3, 4, 5, 6, 12]])
 
 
+def test_copy_state_checked_reports_rejected_pairs(gpu):
+    """copy_state_checked on pair sets with a chain (1->2, 2->3), a swap (4<->5), a shared
+    destination (7->9, 8->9), a self pair, padding and independent pairs, on 2 MiB slots:
+    the pool is bit-exact against the oracle (as copy_state), and `rejected` holds 1 exactly
+    for the pairs the oracle rejects and 0 for the others, padding included.  The status
+    array starts full of garbage (every entry is written), and a HIP-graph replay with new
+    pairs reports them the same way."""
+    announce(test="copy_state_checked")
+    gen = torch.Generator().manual_seed(6)
+    pool = torch.randn(24, 32, 128, 128, generator=gen).to(gpu)
+    src = torch.tensor([1, 2, 4, 5, 7, 8, 10, -1, 13, 15, 0, 18], dtype=torch.int32)
+    dst = torch.tensor([2, 3, 5, 4, 9, 9, 10, 11, 14, -1, 16, 19], dtype=torch.int32)
+    rejected = torch.full((len(src),), 7, dtype=torch.int32, device=gpu)
+    host = row_bytes(pool)
+    src_d, dst_d = src.to(gpu), dst.to(gpu)
+    torch.ops.lightdelta.copy_state_checked(pool, src_d, dst_d, rejected)
+    torch.cuda.synchronize()
+    expected_rejected = oracle.copy_rejected(src.numpy(), dst.numpy())
+    assert list(expected_rejected) == [True, True, True, True, True, True, False, False, False,
+                                       False, False, False]
+    assert np.array_equal(rejected.cpu().numpy(), expected_rejected.astype(np.int32))
+    assert int(rejected.sum()) == 6
+    assert np.array_equal(row_bytes(pool), oracle.copy(host, src.numpy(), dst.numpy()))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        torch.ops.lightdelta.copy_state_checked(pool, src_d, dst_d, rejected)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        torch.ops.lightdelta.copy_state_checked(pool, src_d, dst_d, rejected)
+    for replay, (s_new, d_new) in enumerate((
+            ([3, 6, 20, 21, -1, 12, 1, 2, 9, 22, 23, 17], [6, 20, 21, 3, 4, 13, 2, 1, 8, 23, 22, 12]),
+            ([1, 3, 5, 7, 9, 11, 13, 15, 17, 19, 21, 23], [2, 4, 6, 8, 10, 12, 14, 16, 18, 20, 22, 0]))):
+        s_t = torch.tensor(s_new, dtype=torch.int32)
+        d_t = torch.tensor(d_new, dtype=torch.int32)
+        src_d.copy_(s_t)
+        dst_d.copy_(d_t)
+        rejected.fill_(-3)
+        host = row_bytes(pool)
+        graph.replay()
+        torch.cuda.synchronize()
+        exp = oracle.copy_rejected(s_t.numpy(), d_t.numpy()).astype(np.int32)
+        assert np.array_equal(rejected.cpu().numpy(), exp), f"replay {replay}"
+        assert np.array_equal(row_bytes(pool), oracle.copy(host, s_t.numpy(), d_t.numpy()))
+        assert int(exp.sum()) == (10, 0)[replay]  # a 4-cycle, two swaps, a chain 17->12->13
+
+
 def test_gather_into_strided_rows(gpu):
     """The packed backend gathers into scratch[1:].view(B, W, ...)[:, 0] (row stride W)."""
     announce(test="gather_strided_rows")
