@@ -259,8 +259,9 @@ struct DecodeLds {
   using Conv = uint16_t[kConv ? Width : 1][kConv ? 3 * kDim : 2];
   using ConvNew = uint16_t[kConv && !Packed ? 2 * kDim : 1][kCols];
   // Packed conv state: per wave, the 16-byte pieces of its q/k ([0]) and v ([1]) channels'
-  // columns, then their shifted columns.
-  using Cpk = u32x4[Packed ? Waves : 1][2][32];
+  // columns (4 waves), or of its one run of 64 channels (16 waves: waves 0..5), then their
+  // shifted columns.
+  using Cpk = u32x4[Packed ? (Waves == 16 ? 6 : Waves) : 1][Waves == 16 ? 1 : 2][32];
   static constexpr size_t up16(size_t n) { return (n + 15) / 16 * 16; }
   static constexpr size_t kBytes =
       up16(sizeof(Qk0)) + up16(sizeof(V0)) + up16(sizeof(Db0)) + up16(sizeof(Qkt)) +
@@ -295,7 +296,9 @@ struct DecodeLds {
 // a wave's q/k (or v) conv state are one run of 128 * len bytes: the wave reads it with one
 // 16-byte load per lane, redistributes it through wave-private LDS, and writes the shifted
 // state back the same way (16-byte stores), instead of one 2-byte access per channel and
-// column (B=32, 3 columns: 22.04 -> 21.41 us, bit-identical results).
+// column (B=32, 3 columns: 22.04 -> 21.41 us, bit-identical results).  With 16 waves, waves
+// 0..5 each own one run, the 64 channels they convolve (B=32 cache-cold: 27.35 -> 26.84 us;
+// B=128: 94.05 -> 93.71 us; bit-identical).
 //
 // Waves: 4 (32 V rows and 16 tile pieces per wave), or 16 (8 rows, 4 pieces) for the
 // single-token step under the stream policy and for every verify step.  A
@@ -343,13 +346,15 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   constexpr bool kConvSplit = Conv && Width > 1 && Waves == 16;
   // One token, 3..4 state columns, 16 waves: one channel per thread (0..255 q/k, 256..383
   // v), its inputs loaded ahead of the tile and convolved while the tile streams in, in 6
-  // registers, so that two workgroups fit a CU.
+  // registers, so that two workgroups fit a CU; Packed: each of waves 0..5 moves its 64
+  // channels' columns as one run of 16-byte pieces.
   constexpr bool kConvOne16 = Conv && Width == 1 && kCols <= 4 && Waves == 16;
   constexpr bool kConvFirst = Conv && (Width > 1 || kCols > 4) && !kConvSplit;
   constexpr bool kConvLate = Conv && !kConvFirst && !kConvSplit && !kConvOne16;
   static_assert(!kConvLate || kCols == 4, "the in-flight conv holds 4 state columns");
   static_assert(!kConvLate || Waves == kWaves, "the in-flight conv runs with 4 waves");
-  static_assert(!Packed || (kConvLate && Waves == 4), "the packed conv state: one token, 4 waves");
+  static_assert(!Packed || (kConvLate && Waves == 4) || kConvOne16,
+                "the packed conv state: one token with 3..4 columns");
   // Every kernel argument, then all request metadata, is loaded before the first branch:
   // two dependent scalar round trips (kernel-argument segment; cu/accepted/indices) instead
   // of the compiler's default of sinking each load to its first use behind the early exits.
@@ -362,6 +367,10 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  // The same as a scalar the compiler knows to be wave-uniform, for branches on the wave's
+  // role (a per-lane compare of tid kept its 64-bit mask alive across the conv, which spilled
+  // SGPRs in the 16-wave single-token conv).
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
 
   // Request metadata in one round trip: token range, accepted count and the (at most 4)
   // slots of the request, read before any state store.
@@ -486,9 +495,12 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   // waves 2, 3: the k channels; the v channels of waves 2, 3 repeat those of 0, 1), and the
   // lane's 16-byte piece of a 128 * len-byte run (lanes past its 8 * len pieces repeat the
   // last one; lanes 0..31 read the q/k run, 32..63 the v run).
-  const int pk_qk0 = wave < 2 ? q_col + 64 * wave : k_col + 64 * (wave - 2);
+  // 16 waves (kConvOne16): wave w < 6 owns one run, the 64 channels it convolves (waves 0, 1
+  // the q channels, 2, 3 the k channels, 4, 5 the v channels): pk_qk0 is its first channel
+  // for w < 4, pk_v0 for w = 4, 5; lane l holds piece min(l, 8 * len - 1) of the run.
+  const int pk_qk0 = wave < 2 ? q_col + 64 * wave : k_col + 64 * ((wave - 2) & 1);
   const int pk_v0 = v_col + 64 * (wave & 1);
-  const int pk_piece = min(lane & 31, 8 * p.conv_len - 1);
+  const int pk_piece = min(Waves == 16 ? lane : lane & 31, 8 * p.conv_len - 1);
   u32x4 pk_raw = {0u, 0u, 0u, 0u};
   if constexpr (kConvFirst) {
     // Several tokens (speculative verify), or a long conv state: the conv runs to
@@ -525,17 +537,23 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
   } else if constexpr (kConvSplit) {
     if (tid < 3 * kDim) conv_load<Width, kCols>(p, bos, num_tokens, cs3_at, conv_ch3, ci);
   } else if constexpr (kConvOne16) {
-    if (tid < 3 * kDim) {  // wave-uniform; every column clamped to the state's last
+    if (wave_s < 6) {  // every column clamped to the state's last
       const int ch = tid < kDim ? q_col + tid
                                 : (tid < 2 * kDim ? k_col + (tid - kDim) : v_col + (tid - 2 * kDim));
       c1_at = conv_slot_at + ch * p.conv_dim_stride;
       c1_x = p.conv_x[static_cast<int64_t>(bos) * p.conv_x_row + ch];
-      uint32_t st[4];
+      if constexpr (Packed) {  // the wave's run, one 16-byte piece per lane
+        pk_raw = *reinterpret_cast<const u32x4*>(
+            p.conv_state + conv_slot_at + static_cast<int64_t>(wave < 4 ? pk_qk0 : pk_v0) *
+                                              p.conv_len + 8 * pk_piece);
+      } else {
+        uint32_t st[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        st[j] = p.conv_state[c1_at + min(j, p.conv_len - 1) * p.conv_len_stride];
-      c1_st[0] = st[0] | (st[1] << 16);
-      c1_st[1] = st[2] | (st[3] << 16);
+        for (int j = 0; j < 4; ++j)
+          st[j] = p.conv_state[c1_at + min(j, p.conv_len - 1) * p.conv_len_stride];
+        c1_st[0] = st[0] | (st[1] << 16);
+        c1_st[1] = st[2] | (st[3] << 16);
+      }
       const uint32_t* wsrc = reinterpret_cast<const uint32_t*>(p.conv_weight + ch * kConvWidth);
       c1_w[0] = wsrc[0];
       c1_w[1] = wsrc[1];
@@ -660,17 +678,41 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     conv_token_w();
   }
   if constexpr (kConvOne16) {
-    if (tid < 3 * kDim) {
+    if (wave_s < 6) {
       const int len = p.conv_len;
-      const uint16_t st[4] = {static_cast<uint16_t>(c1_st[0]), static_cast<uint16_t>(c1_st[0] >> 16),
-                              static_cast<uint16_t>(c1_st[1]), static_cast<uint16_t>(c1_st[1] >> 16)};
+      uint16_t st[4];
+      if constexpr (Packed) {  // the lane's channel's columns out of the wave's run
+        // lanes with the same piece index hold the same piece: their writes agree
+        s_cpk[wave][0][pk_piece] = pk_raw;
+        lds_order();
+        const uint16_t* run = reinterpret_cast<const uint16_t*>(s_cpk[wave][0]) + lane * len;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) st[j] = run[min(j, len - 1)];
+      } else {
+        st[0] = static_cast<uint16_t>(c1_st[0]);
+        st[1] = static_cast<uint16_t>(c1_st[0] >> 16);
+        st[2] = static_cast<uint16_t>(c1_st[1]);
+        st[3] = static_cast<uint16_t>(c1_st[1] >> 16);
+      }
       s_conv[0][tid] = conv_output(c1_x, st, c1_w, c1_bias, p.conv_bias != nullptr);
       // shifted state: columns 1..len-1, then the new input; q/k kept for the end-of-kernel
       // write, the thread's own v channel shifted in place (only it reads that channel)
       uint16_t shifted[kCols];
 #pragma unroll
       for (int j = 0; j < kCols; ++j) shifted[j] = j + 1 < len ? st[j + 1 < kCols ? j + 1 : j] : c1_x;
-      if (tid < 2 * kDim) {
+      if constexpr (Packed) {  // shifted columns into the run (its old values were read above)
+        uint16_t* run = reinterpret_cast<uint16_t*>(s_cpk[wave][0]) + lane * len;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (j < len) run[j] = shifted[j];
+        lds_order();
+        // waves 4, 5: the v run back to the pool, one 16-byte piece per lane (lanes past the
+        // run's last piece repeat it with the same bytes)
+        if (wave_s >= 4)
+          *reinterpret_cast<u32x4*>(p.conv_state + conv_slot_at +
+                                    static_cast<int64_t>(pk_v0) * len + 8 * pk_piece) =
+              s_cpk[wave][0][pk_piece];
+      } else if (wave_s < 4) {
 #pragma unroll
         for (int j = 0; j < kCols; ++j) s_conv_new[tid][j] = shifted[j];
       } else {
@@ -690,6 +732,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     const bool has_bias = p.conv_bias != nullptr;
     if constexpr (Packed) {  // the lane's channels' columns out of the wave's runs
       s_cpk[wave][lane >> 5][lane & 31] = pk_raw;
+      lds_order();
       const uint16_t* run_qk = reinterpret_cast<const uint16_t*>(s_cpk[wave][0]) + lane * len;
       const uint16_t* run_v = reinterpret_cast<const uint16_t*>(s_cpk[wave][1]) + lane * len;
 #pragma unroll
@@ -717,6 +760,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
           run_qk[j] = qk_new[j];
           run_v[j] = v_new[j];
         }
+      lds_order();
     } else {
 #pragma unroll
       for (int j = 0; j < kCols; ++j) s_conv_new[tid][j] = qk_new[j];
@@ -872,9 +916,10 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     if (p.group == 1 || s_arrived == static_cast<uint32_t>(p.group - 1)) {
       const int64_t slot_at = static_cast<int64_t>(slot[0]) * p.conv_slot;
       if constexpr (Packed) {  // each wave its 64 q or k channels, one 16-byte piece per lane
-        *reinterpret_cast<u32x4*>(p.conv_state + slot_at +
-                                  static_cast<int64_t>(pk_qk0) * p.conv_len + 8 * pk_piece) =
-            s_cpk[wave][0][pk_piece];
+        if (Waves == kWaves || wave_s < 4)
+          *reinterpret_cast<u32x4*>(p.conv_state + slot_at +
+                                    static_cast<int64_t>(pk_qk0) * p.conv_len + 8 * pk_piece) =
+              s_cpk[wave][0][pk_piece];
       } else {
         for (int c = tid; c < 2 * kDim; c += kBlock) {
           const int ch = c < kDim ? q_col + c : k_col + (c - kDim);
@@ -959,10 +1004,8 @@ int launch_decode(const DecodeParams& p, bool conv, bool dt_bf16, bool w_bf16,
   if (conv) {
     switch (p.width) {
       case 1:  // conv state of 3..4 columns (the usual width - 1 = 3), or up to 8
-        if constexpr (ConvOne::kWaveCount == kWaves) {  // the packed state: 4 waves
-          if (p.conv_len <= 4 && p.conv_packed)
-            return launch_kernel<ConvOne, 1, 4, true>(p, dt_bf16, w_bf16, blocks, stream);
-        }
+        if (p.conv_len <= 4 && p.conv_packed)  // dense dim-first pool: 16-byte pieces
+          return launch_kernel<ConvOne, 1, 4, true>(p, dt_bf16, w_bf16, blocks, stream);
         if (p.conv_len <= 4) return launch_kernel<ConvOne, 1, 4>(p, dt_bf16, w_bf16, blocks, stream);
         return launch_kernel<ConvLong, 1, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);
       case 2: return launch_kernel<ConvVerify, 2, kMaxConvLen>(p, dt_bf16, w_bf16, blocks, stream);

@@ -212,6 +212,12 @@ __device__ __forceinline__ void chunk_step(f32x4 (&s)[N], const Vectors& x, floa
 // kernel-argument or metadata load) cannot be sunk past later branches.  Input-only: the
 // value itself, and for pointers their global address space, stay visible to the compiler.
 
+// Keeps the compiler from moving LDS accesses across this point: a wave's packed conv runs are
+// written as 16-byte pieces and read back as 2-byte columns (or the reverse), which type-based
+// alias analysis would otherwise let it reorder.  The hardware runs a wave's LDS operations in
+// program order, so no wait is needed.
+__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
+
 // Waits for this wave's LDS traffic, then joins the workgroup barrier.  Global loads that
 // are still in flight stay in flight (a __syncthreads() fence would drain them).
 __device__ __forceinline__ void lds_barrier() {

@@ -199,12 +199,13 @@ def test_ragged_verify_and_rejected_requests(gpu):
 @pytest.mark.parametrize("length,heads,bias", [(3, (16, 32), False), (4, (4, 8), True),
                                                  (3, (16, 48), True)])
 def test_packed_and_per_element_conv_paths_agree(gpu, length, heads, bias, policy):
-    """Under the keep policy a dense, 16-byte aligned dim-first conv pool takes the kernel's
-    packed path (each wave moves its channels' columns as 16-byte pieces); the same data one
-    element into a larger buffer (2-byte aligned) takes the per-element path.  Under the
-    stream policy both pools take the one-channel-per-thread path, which loads each column as
-    one element and needs no alignment beyond the element's.  Over 3 steps both give the same bits for
-    the conv state, the SSM pool and the outputs, and the aligned run matches the oracle."""
+    """A dense, 16-byte aligned dim-first conv pool takes the kernel's packed path (each wave
+    moves its channels' columns as 16-byte pieces: 4 waves with a q/k and a v run each under
+    the keep policy, waves 0..5 of 16 with one run each under the stream policy); the same
+    data one element into a larger buffer (2-byte aligned) takes the per-element path, which
+    loads each column as one element and needs no alignment beyond the element's.  Over 3
+    steps both give the same bits for the conv state, the SSM pool and the outputs, and the
+    aligned run matches the oracle."""
     announce(test="conv_packed_vs_per_element", length=length, heads=heads, bias=bias,
              policy=policy)
     case = conv_case(gpu, 8, heads, pool_slots=10, length=length, bias=bias, seed=90 + length)
