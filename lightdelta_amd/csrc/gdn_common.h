@@ -65,6 +65,7 @@ struct DecodeParams {
 constexpr int kPolPlain = 0;
 constexpr int kPolNT = 2;
 constexpr int kPolSys = 1 | 16;
+constexpr int kPolNTSys = kPolNT | kPolSys;  // streaming, written through to memory
 constexpr int kTileBytes = kDim * kDim * 4;
 
 // A raw (untyped) buffer resource over `bytes` bytes at `base`.  Accesses at byte offsets at

@@ -1105,8 +1105,8 @@ int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, b
   const uint32_t n = static_cast<uint32_t>(blocks);
   int rc;
   if (a.cache_policy == LD_CACHE_STREAM)
-    rc = launch_decode<Shape<kPolNT, kPolSys, 16>, Shape<kPolNT, kPolSys, 16, true>,
-                       Shape<kPolNT, kPolNT, 16>, Shape<kPolPlain, kPolNT, 16, true>>(
+    rc = launch_decode<Shape<kPolNTSys, kPolNTSys, 16>, Shape<kPolNTSys, kPolNTSys, 16, true>,
+                       Shape<kPolNTSys, kPolNTSys, 16>, Shape<kPolNTSys, kPolNTSys, 16, true>>(
         p, conv, dt_bf16, w_bf16, n, s);
   else
     rc = launch_decode<Shape<kPolPlain, kPolPlain, kWaves>, Shape<kPolPlain, kPolNT, 16, true>,
