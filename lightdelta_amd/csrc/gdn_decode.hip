@@ -1079,29 +1079,20 @@ int launch(const ld_gdn_decode_args& a, const DecodeParams& p, int64_t blocks, b
   const bool dt_bf16 = a.dt_bias_dtype == LD_DTYPE_BF16;
   const bool w_bf16 = a.norm_weight_dtype == LD_DTYPE_BF16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  // Measured on MI355X (B=32 and B=128 single-token steps, B=64 4-token verify, B=32
-  // conv-fused step; hot = the same slots every step, cold = slot sets rotated through a pool
-  // far beyond the 256 MB Infinity Cache):
-  //   one token, keep:   4 waves, plain loads and stores (B=32 hot 19.98 us; 16 waves with
-  //                      the same hints 20.21, the stream kernel 20.90).
-  //   one token, stream: 16 waves, non-temporal loads, system-scope stores (B=128 cold
-  //                      89.3 us = 6.01 TB/s; with non-temporal stores 90.9, the keep
-  //                      kernel 107.6; B=32 cold 24.8 against 29.8).
+  // Measured on MI355X (B=32 and B=128 single-token steps, B=64 4-token verify, B=32 and
+  // B=128 conv-fused steps; hot = the same slots every step, cold = slot sets rotated
+  // through a pool far beyond the 256 MB Infinity Cache):
+  //   one token, keep:   4 waves, plain loads and stores (B=32 hot 19.9 us; 16 waves with
+  //                      the same hints 20.2, the stream kernel 20.9).
   //   verify, keep:      16 waves, plain loads, non-temporal stores, one workgroup per CU
-  //                      (B=64, T=4: 98.7 us hot, 120.8 cold; two per CU 98.8 and 124.4;
-  //                      4 waves 105.1 and 138.9).
-  //   verify, stream:    16 waves, non-temporal loads, system-scope stores, one workgroup
-  //                      per CU (B=64, T=4 cold: 114.4 us = 5.87 TB/s; two per CU 116.0;
-  //                      the keep kernel 120.8).
-  //   conv-fused, one token: 4 waves, plain loads and stores (keep; 21.4 us hot); under
-  //                      stream 16 waves, one conv channel per thread, non-temporal loads
-  //                      and stores, two workgroups per CU (27.1 us cold, against 27.7 with
-  //                      4 waves and 27.6 with system-scope stores).
-  //   conv-fused verify, either: 16 waves, the conv's inputs loaded ahead of the tile,
-  //                      plain loads, non-temporal stores, one workgroup per CU (B=64, T=4,
-  //                      6 conv columns: 105.5 us hot, 127.4 cold, against 108.8 and 143.2
-  //                      with 4 waves and the conv run before the tile loads; non-temporal
-  //                      loads 128.9 and 129.0).
+  //                      (B=64, T=4: 98.7-101 us hot, 120.8 cold; two per CU 98.8 and
+  //                      124.4; 4 waves 105.1 and 138.9).
+  //   conv-fused, keep:  one token 4 waves, plain loads and stores (21.3 us hot); verify as
+  //                      the verify above (102-105 us hot).
+  //   stream, all:       16 waves (verify steps one workgroup per CU), non-temporal
+  //                      system-scope loads and stores (cold: B=128 single token 88.8 us =
+  //                      6.04 TB/s, B=32 24.6; conv-fused 90.6 and 25.3; verify 112.4,
+  //                      conv-fused verify 114.7; 4-wave forms 10-20% slower).
   const uint32_t n = static_cast<uint32_t>(blocks);
   int rc;
   if (a.cache_policy == LD_CACHE_STREAM)
