@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 10
+#define LD_ABI_VERSION 11
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -311,6 +311,27 @@ int ld_state_copy_checked(void* pool, int64_t pool_slot_stride_bytes, const int3
  */
 int ld_state_zero(void* pool, int64_t pool_slot_stride_bytes, const int32_t* slots,
                   int64_t count, int64_t slot_bytes, void* stream);
+
+/*
+ * The packed state-access path's bookkeeping for `batch` requests with `width` slots each,
+ * in one launch (all arrays device memory; slots [batch, width] contiguous, cu [batch + 1],
+ * accepted [batch]; outputs source [batch], valid [batch] (0/1 bytes), indices
+ * [batch, width], destinations [batch * width]):
+ *   source[r]   = slots[r, clamp(accepted[r], 1, width) - 1]
+ *   valid[r]    = 1 <= accepted[r] <= width and source[r] > 0
+ *   indices[r, t] = valid[r] ? 1 + r * width + t : 0   (request r's rows of a scratch pool
+ *                                                       whose row 0 is padding)
+ *   destinations[r * width + t] = t < cu[r + 1] - cu[r] and valid[r] and slots[r, t] > 0
+ *                                 ? slots[r, t] : 0
+ * Then ld_state_gather(pool -> scratch[1 + r * width], source, valid), ld_gdn_decode on the
+ * scratch with `indices` and accepted = 1, and ld_state_scatter(scratch[1:] ->
+ * destinations) make the packed step.  Replaces the Torch index arithmetic of the
+ * reference's packed path (python/lightdelta/backend.py:39-47, 87-91); no allocation, no
+ * host read of device memory (graph-capturable).
+ */
+int ld_packed_plan(const int32_t* slots, const int32_t* cu, const int32_t* accepted,
+                   int32_t batch, int32_t width, int32_t* source, uint8_t* valid,
+                   int32_t* indices, int32_t* destinations, void* stream);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
 const char* ld_last_error(void);

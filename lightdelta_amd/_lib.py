@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must precede the CDLL load (see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("liblightdelta_hip.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 CACHE_KEEP = 0
@@ -142,6 +142,7 @@ SIGNATURES = {
     "ld_state_copy": ([_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _vp], ctypes.c_int),
     "ld_state_copy_checked": ([_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _vp, _vp], ctypes.c_int),
     "ld_state_zero": ([_vp, _c_i64, _vp, _c_i64, _c_i64, _vp], ctypes.c_int),
+    "ld_packed_plan": ([_vp, _vp, _vp, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
     "ld_last_error": ([], ctypes.c_char_p),
     "ld_abi_version": ([], ctypes.c_int),
 }

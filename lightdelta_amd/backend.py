@@ -8,6 +8,7 @@
 * state_io = "packed": the source state of every request is gathered into a cached scratch
   buffer (row 0 reserved, request r's T rows at 1 + r*T), the step runs on the scratch, and
   the per-token states are written back to their slots.  With compute = "cuda_fused" the
+  bookkeeping (sources, validity, scratch rows, destinations: one packed_plan launch), the
   gather, the step and the write-back are the gfx950 HIP kernels; with "torch_reference"
   (an eager ablation) they are plain torch index ops plus the unfused Torch GDN.
 
@@ -52,22 +53,26 @@ class GDNBackend:
             )
             return
 
-        scratch, compact, ones, offsets = self._scratch(pool, batch, width)
-        source = slots.gather(1, (accepted.clamp(1, width) - 1)[:, None].long()).flatten()
-        valid = (accepted > 0) & (accepted <= width) & (source > 0)
+        scratch, ones, offsets, plan = self._scratch(pool, batch, width)
         initial = scratch[1:].view(batch, width, *pool.shape[1:])[:, 0]
-        lengths = cu[1:] - cu[:-1]
-        live = offsets < lengths[:, None]
-        destinations = torch.where(live & valid[:, None] & (slots > 0), slots, 0).flatten()
 
         if self.config.compute == "cuda_fused":
+            # source, valid, indices and destinations of the semantics above, in one launch
+            source, valid, indices, destinations = plan
+            torch.ops.lightdelta.packed_plan(slots, cu, accepted, source, valid, indices,
+                                             destinations)
             torch.ops.lightdelta.gather_state(pool, source, valid, initial)
-            indices = torch.where(valid[:, None], compact, 0)
             torch.ops.lightdelta.decode(
                 qkv, a, b, a_log, dt_bias, indices, cu, ones, scratch, gate, weight, out, eps
             )
             torch.ops.lightdelta.scatter_state(scratch[1:], destinations, pool)
             return
+
+        source = slots.gather(1, (accepted.clamp(1, width) - 1)[:, None].long()).flatten()
+        valid = (accepted > 0) & (accepted <= width) & (source > 0)
+        lengths = cu[1:] - cu[:-1]
+        live = offsets < lengths[:, None]
+        destinations = torch.where(live & valid[:, None] & (slots > 0), slots, 0).flatten()
 
         # compute == "torch_reference": eager torch ops end to end.
         torch.index_select(pool, 0, source.clamp_min(0).long(), out=initial)
@@ -86,11 +91,14 @@ class GDNBackend:
             device = pool.device
             cached = (
                 pool.new_empty((1 + batch * width, *pool.shape[1:])),
-                torch.arange(1, 1 + batch * width, device=device, dtype=torch.int32).view(
-                    batch, width
-                ),
                 torch.ones(batch, device=device, dtype=torch.int32),
                 torch.arange(width, device=device, dtype=torch.int32)[None, :],
+                # the fused path's bookkeeping outputs (packed_plan): source, valid,
+                # indices, destinations
+                (torch.empty(batch, device=device, dtype=torch.int32),
+                 torch.empty(batch, device=device, dtype=torch.bool),
+                 torch.empty(batch, width, device=device, dtype=torch.int32),
+                 torch.empty(batch * width, device=device, dtype=torch.int32)),
             )
             self._packed[key] = cached
         return cached

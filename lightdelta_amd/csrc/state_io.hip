@@ -185,6 +185,56 @@ int launch(const char* what, int mode, CopyParams p, int64_t rows, int64_t row_b
 }  // namespace
 }  // namespace ld
 
+namespace ld {
+namespace {
+
+// The packed path's bookkeeping for a batch of `batch` requests of `width` slots each, one
+// thread per (request r, token t) (python/lightdelta/backend.py:39-47, 87-91):
+//   source[r]       = slots[r, clamp(accepted[r], 1, width) - 1]
+//   valid[r]        = 1 <= accepted[r] <= width and source[r] > 0
+//   indices[r, t]   = valid[r] ? 1 + r * width + t : 0       (the request's scratch rows)
+//   destinations[r * width + t] = t < cu[r+1] - cu[r] and valid[r] and slots[r, t] > 0
+//                                 ? slots[r, t] : 0
+__global__ __launch_bounds__(kThreads) void packed_plan_kernel(
+    const int32_t* slots, const int32_t* cu, const int32_t* accepted, int32_t batch,
+    int32_t width, int32_t* source, uint8_t* valid, int32_t* indices, int32_t* destinations) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= static_cast<int64_t>(batch) * width) return;
+  const int32_t r = static_cast<int32_t>(i / width);
+  const int32_t t = static_cast<int32_t>(i - static_cast<int64_t>(r) * width);
+  const int32_t acc = accepted[r];
+  const int32_t src = slots[static_cast<int64_t>(r) * width + min(max(acc, 1), width) - 1];
+  const bool ok = acc >= 1 && acc <= width && src > 0;
+  if (t == 0) {
+    source[r] = src;
+    valid[r] = ok ? 1 : 0;
+  }
+  const int32_t slot = slots[i];
+  const bool live = t < cu[r + 1] - cu[r];
+  indices[i] = ok ? static_cast<int32_t>(1 + i) : 0;
+  destinations[i] = live && ok && slot > 0 ? slot : 0;
+}
+
+}  // namespace
+}  // namespace ld
+
+extern "C" int ld_packed_plan(const int32_t* slots, const int32_t* cu, const int32_t* accepted,
+                              int32_t batch, int32_t width, int32_t* source, uint8_t* valid,
+                              int32_t* indices, int32_t* destinations, void* stream) {
+  using namespace ld;
+  if (batch < 0 || width < 1 || width > LD_MAX_TOKENS)
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_packed_plan: batch must be >= 0 and width 1..4");
+  if (batch == 0) return LD_OK;
+  if (!slots || !cu || !accepted || !source || !valid || !indices || !destinations)
+    return fail(LD_ERR_INVALID_ARGUMENT, "ld_packed_plan: NULL pointer");
+  const int64_t items = static_cast<int64_t>(batch) * width;
+  const uint32_t blocks = static_cast<uint32_t>((items + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(packed_plan_kernel, dim3(blocks), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), slots, cu, accepted, batch, width, source,
+                     valid, indices, destinations);
+  return check_launch("ld_packed_plan");
+}
+
 extern "C" int ld_state_gather(const void* pool, int64_t pool_slot_stride_bytes,
                                const int32_t* slots, int64_t slot_stride, const uint8_t* valid,
                                void* out, int64_t out_row_stride_bytes, int64_t row_bytes,

@@ -345,6 +345,36 @@ void zero_slots(at::Tensor pool, const at::Tensor& slots) {
   TORCH_CHECK(rc == LD_OK, ld_last_error());
 }
 
+void packed_plan(const at::Tensor& slots, const at::Tensor& cu, const at::Tensor& accepted,
+                 at::Tensor source, at::Tensor valid, at::Tensor indices,
+                 at::Tensor destinations) {
+  TORCH_CHECK(slots.is_cuda() && slots.scalar_type() == at::kInt && slots.dim() == 2 &&
+                  slots.is_contiguous() && slots.size(1) >= 1 && slots.size(1) <= LD_MAX_TOKENS,
+              "slots must be a contiguous CUDA int32 [batch, 1..4] tensor");
+  const int64_t batch = slots.size(0);
+  const int64_t width = slots.size(1);
+  const std::pair<const at::Tensor*, std::vector<int64_t>> ints[] = {
+      {&cu, {batch + 1}}, {&accepted, {batch}}, {&source, {batch}},
+      {&indices, {batch, width}}, {&destinations, {batch * width}}};
+  for (const auto& [t, shape] : ints)
+    TORCH_CHECK(t->device() == slots.device() && t->scalar_type() == at::kInt &&
+                    t->sizes() == at::IntArrayRef(shape) && t->is_contiguous(),
+                "packed_plan tensors must be contiguous CUDA int32 of the batch's shapes");
+  TORCH_CHECK(valid.device() == slots.device() && valid.scalar_type() == at::kBool &&
+                  valid.dim() == 1 && valid.size(0) == batch && valid.is_contiguous(),
+              "valid must be a contiguous CUDA bool vector");
+  TORCH_CHECK(batch <= INT32_MAX, "batch too large");
+  if (batch == 0) return;
+  const c10::DeviceGuard guard(slots.device());
+  const int rc = ld_packed_plan(
+      static_cast<const int32_t*>(slots.data_ptr()), static_cast<const int32_t*>(cu.data_ptr()),
+      static_cast<const int32_t*>(accepted.data_ptr()), static_cast<int32_t>(batch),
+      static_cast<int32_t>(width), static_cast<int32_t*>(source.data_ptr()),
+      static_cast<uint8_t*>(valid.data_ptr()), static_cast<int32_t*>(indices.data_ptr()),
+      static_cast<int32_t*>(destinations.data_ptr()), stream_of(slots));
+  TORCH_CHECK(rc == LD_OK, ld_last_error());
+}
+
 }  // namespace
 
 TORCH_LIBRARY_IMPL(lightdelta, CUDA, m) {
@@ -357,6 +387,7 @@ TORCH_LIBRARY_IMPL(lightdelta, CUDA, m) {
   m.impl("copy_state", &copy_state);
   m.impl("copy_state_checked", &copy_state_checked);
   m.impl("zero_slots", &zero_slots);
+  m.impl("packed_plan", &packed_plan);
 }
 
 // The state cache policy these kernels pass (LD_CACHE_KEEP / LD_CACHE_STREAM), set from

@@ -35,6 +35,11 @@ Additive ops (no reference counterpart):
                                         outputs, final state to slots[n]
   gather_slots / scatter_slots          dtype-generic gather_state / scatter_state, for the
                                         bf16 conv-state pool and any dense-inner pool
+  packed_plan(slots, cu, accepted, source, valid, indices, destinations)
+                                        the packed path's bookkeeping (GDNBackend,
+                                        state_io = "packed") in one launch: each request's
+                                        source slot and validity, its scratch rows, and the
+                                        slots its per-token states go back to
 
 Every kernel launches on the caller's current stream and reads no device memory on the host,
 so it can be captured in a HIP graph.  None allocates, except prefill's chunked form, which
@@ -79,6 +84,10 @@ SCHEMAS = {
         "Tensor(o!) out, float eps) -> ()"
     ),
     "gather_slots": "gather_slots(Tensor pool, Tensor slots, Tensor valid, Tensor(o!) out) -> ()",
+    "packed_plan": (
+        "packed_plan(Tensor slots, Tensor cu, Tensor accepted, Tensor(s!) source, "
+        "Tensor(v!) valid, Tensor(i!) indices, Tensor(d!) destinations) -> ()"
+    ),
     "scatter_slots": "scatter_slots(Tensor packed, Tensor slots, Tensor(p!) pool) -> ()",
 }
 
@@ -468,6 +477,30 @@ def check_copy_checked(pool, src, dst, rejected):
     )
 
 
+def check_packed_plan(slots, cu, accepted, source, valid, indices, destinations):
+    """Validation of packed_plan: int32 metadata [B, W] / [B + 1] / [B], outputs source [B]
+    int32, valid [B] bool, indices [B, W] int32, destinations [B * W] int32, all contiguous
+    on one device."""
+    _require(
+        _is_gpu(slots) and slots.dtype == torch.int32 and slots.dim() == 2
+        and slots.is_contiguous() and 1 <= slots.shape[1] <= _lib.MAX_TOKENS,
+        "slots must be a contiguous CUDA int32 [batch, 1..4] tensor",
+    )
+    batch, width = slots.shape
+    for t, shape in ((cu, (batch + 1,)), (accepted, (batch,)), (source, (batch,)),
+                     (indices, (batch, width)), (destinations, (batch * width,))):
+        _require(
+            t.device == slots.device and t.dtype == torch.int32 and tuple(t.shape) == shape
+            and t.is_contiguous(),
+            "packed_plan tensors must be contiguous CUDA int32 of the batch's shapes",
+        )
+    _require(
+        valid.device == slots.device and valid.dtype == torch.bool
+        and tuple(valid.shape) == (batch,) and valid.is_contiguous(),
+        "valid must be a contiguous CUDA bool vector",
+    )
+
+
 def check_zero(pool, slots):
     _require(
         _is_gpu(pool) and pool.dim() >= 1 and _dense_inner(pool),
@@ -488,7 +521,7 @@ def check_zero(pool, slots):
 # path is on every decode step.  prefill's kernel is the Python function below (it keeps the
 # chunked form's workspace cache and the algorithm choice).
 _CXX_KERNELS = ("decode", "decode_conv", "gather_state", "scatter_state", "gather_slots",
-                "scatter_slots", "copy_state", "copy_state_checked", "zero_slots")
+                "scatter_slots", "copy_state", "copy_state_checked", "zero_slots", "packed_plan")
 _IMPLS = {
     "prefill": _prefill_impl,
 }

@@ -25,8 +25,8 @@ def test_header_declares_the_entry_points():
         "ld_gdn_decode", "ld_gdn_decode_conv", "ld_gdn_prefill", "ld_gdn_prefill_static",
         "ld_gdn_prefill_workspace_bytes", "ld_gdn_prefill_auto_chunked", "ld_state_gather",
         "ld_state_scatter",
-        "ld_state_copy", "ld_state_copy_checked", "ld_state_zero", "ld_last_error",
-        "ld_abi_version",
+        "ld_state_copy", "ld_state_copy_checked", "ld_state_zero", "ld_packed_plan",
+        "ld_last_error", "ld_abi_version",
     }
 
 
@@ -119,6 +119,17 @@ def test_checked_copy_needs_a_status_array_and_nonempty_slots():
     assert b"rejected is NULL" in lib.ld_last_error()
     assert lib.ld_state_copy_checked(16, 2048, 32, 48, 1, 0, 64, None) == 1
     assert b"slot_bytes must be positive" in lib.ld_last_error()
+
+
+def test_packed_plan_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    assert lib.ld_packed_plan(None, None, None, 0, 1, None, None, None, None, None) == 0
+    for batch, width in ((-1, 1), (4, 0), (4, 5)):
+        assert lib.ld_packed_plan(None, None, None, batch, width, None, None, None, None,
+                                  None) == 1
+        assert b"width 1..4" in lib.ld_last_error()
+    assert lib.ld_packed_plan(16, None, 16, 4, 1, 16, 16, 16, 16, None) == 1
+    assert b"NULL pointer" in lib.ld_last_error()
 
 
 def test_prefill_rejects_bad_arguments_without_launching():

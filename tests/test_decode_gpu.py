@@ -182,6 +182,36 @@ def test_invalid_and_empty_requests(gpu, policy):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("batch,width", [(1, 1), (7, 2), (33, 3), (100, 4)])
+def test_packed_plan_matches_the_reference_bookkeeping(gpu, batch, width):
+    """packed_plan (the fused packed path's bookkeeping in one launch) against the reference
+    backend's Torch index arithmetic (python/lightdelta/backend.py:39-47, 87-91), on random
+    metadata with every edge: accepted 0, -1 and past the width, padding slots 0 and -1
+    (also as the source), and requests of 0 .. width tokens."""
+    announce(test="packed_plan", batch=batch, width=width)
+    gen = torch.Generator().manual_seed(batch * 10 + width)
+    slots = torch.randint(-1, 50, (batch, width), generator=gen, dtype=torch.int32)
+    accepted = torch.randint(-1, width + 2, (batch,), generator=gen, dtype=torch.int32)
+    lengths = torch.randint(0, width + 1, (batch,), generator=gen, dtype=torch.int32)
+    cu = torch.zeros(batch + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lengths, 0)
+    source = slots.gather(1, (accepted.clamp(1, width) - 1)[:, None].long()).flatten()
+    valid = (accepted > 0) & (accepted <= width) & (source > 0)
+    live = torch.arange(width)[None, :] < lengths[:, None]
+    destinations = torch.where(live & valid[:, None] & (slots > 0), slots, 0).flatten()
+    indices = torch.where(valid[:, None], torch.arange(1, 1 + batch * width,
+                                                       dtype=torch.int32).view(batch, width), 0)
+    out = (torch.full((batch,), -7, dtype=torch.int32, device=gpu),
+           torch.ones(batch, dtype=torch.bool, device=gpu),
+           torch.full((batch, width), -7, dtype=torch.int32, device=gpu),
+           torch.full((batch * width,), -7, dtype=torch.int32, device=gpu))
+    torch.ops.lightdelta.packed_plan(slots.to(gpu), cu.to(gpu), accepted.to(gpu), *out)
+    torch.cuda.synchronize()
+    for name, got, want in zip(("source", "valid", "indices", "destinations"), out,
+                               (source, valid, indices, destinations)):
+        assert torch.equal(got.cpu(), want.to(got.dtype)), name
+
+
 def test_workload_64_steps(gpu, policy):
     """Qwen3-Next-shape layer: B=32, 16 qk / 32 v heads, 256-slot pool, random distinct
     slots, 64 consecutive in-place steps.  States and every step's outputs against the

@@ -168,6 +168,32 @@ def test_copy_state_checked_validation_messages(meta):
         ops.check_copy_checked(pool, src, src[:2], src)
 
 
+def test_packed_plan_validation_messages(meta):
+    def plan(batch=4, width=2, **over):
+        t = dict(slots=torch.empty(batch, width, dtype=torch.int32, device=meta),
+                 cu=torch.empty(batch + 1, dtype=torch.int32, device=meta),
+                 accepted=torch.empty(batch, dtype=torch.int32, device=meta),
+                 source=torch.empty(batch, dtype=torch.int32, device=meta),
+                 valid=torch.empty(batch, dtype=torch.bool, device=meta),
+                 indices=torch.empty(batch, width, dtype=torch.int32, device=meta),
+                 destinations=torch.empty(batch * width, dtype=torch.int32, device=meta))
+        t.update(over)
+        return t
+    ops.check_packed_plan(*plan().values())
+    with pytest.raises(RuntimeError, match=r"slots must be a contiguous CUDA int32 \[batch, 1..4\]"):
+        ops.check_packed_plan(*plan(width=5).values())
+    with pytest.raises(RuntimeError, match="slots must be"):
+        ops.check_packed_plan(*plan(slots=torch.empty(4, 2, dtype=torch.int64, device=meta)).values())
+    for name, bad in (("cu", torch.empty(4, dtype=torch.int32, device=meta)),
+                      ("source", torch.empty(4, dtype=torch.int64, device=meta)),
+                      ("indices", torch.empty(8, dtype=torch.int32, device=meta)),
+                      ("destinations", torch.empty(4, 2, dtype=torch.int32, device=meta))):
+        with pytest.raises(RuntimeError, match="packed_plan tensors must be"):
+            ops.check_packed_plan(*plan(**{name: bad}).values())
+    with pytest.raises(RuntimeError, match="valid must be a contiguous CUDA bool vector"):
+        ops.check_packed_plan(*plan(valid=torch.empty(4, dtype=torch.uint8, device=meta)).values())
+
+
 def test_state_io_validation_messages(meta):
     pool = torch.empty(8, 4, 128, 128, device=meta)
     slots = torch.empty(3, dtype=torch.int32, device=meta)
@@ -279,6 +305,24 @@ def test_copy_state_checked_kernel_validation_messages(gpu):
     with pytest.raises(RuntimeError, match="same length"):
         torch.ops.lightdelta.copy_state_checked(pool, src, dst[:2].contiguous(),
                                                 torch.zeros(3, dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_packed_plan_kernel_validation_messages(gpu):
+    i32 = dict(dtype=torch.int32, device=gpu)
+    good = dict(slots=torch.zeros(4, 2, **i32), cu=torch.zeros(5, **i32),
+                accepted=torch.zeros(4, **i32), source=torch.zeros(4, **i32),
+                valid=torch.zeros(4, dtype=torch.bool, device=gpu),
+                indices=torch.zeros(4, 2, **i32), destinations=torch.zeros(8, **i32))
+    for name, bad, message in (
+            ("slots", torch.zeros(4, 5, **i32), "slots must be a contiguous CUDA int32"),
+            ("cu", torch.zeros(4, **i32), "packed_plan tensors must be"),
+            ("destinations", torch.zeros(4, 2, **i32), "packed_plan tensors must be"),
+            ("valid", torch.zeros(4, dtype=torch.uint8, device=gpu), "valid must be")):
+        args = dict(good, **{name: bad})
+        with pytest.raises(RuntimeError, match=message):
+            torch.ops.lightdelta.packed_plan(*args.values())
     torch.cuda.synchronize()
 
 
