@@ -628,16 +628,24 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     inw = load_token(p, token_w, q_col, k_col, v_col + 2 * lane, head, kq);
     vw_hi = p.qkv[token_w * p.qkv_row + v_col + 2 * lane + 1];
   }
+  // The epilogue's inputs (gate row of token `wave`, norm weight).  Without a conv and with
+  // one token they are loaded behind the tile and parked in LDS after the chunks, so that
+  // nothing but the token's own inputs stands in front of the tile's loads (B=32 hot
+  // 19.76 -> 19.38 us, cold 24.65 -> 24.57 us, bit-identical); the conv-fused and verify
+  // kernels load them ahead, as they stage them before the recurrence (the conv-fused
+  // single token measured 21.36 -> 21.52 us the other way).
   uint16_t gh[2];
   float w[2];
-  {
+  constexpr bool kLate = Width == 1 && !Conv;
+  auto load_epi = [&]() {
     const uint16_t* grow = p.gate + token_w * p.gate_row + head * kDim;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       gh[e] = grow[2 * lane + e];
       w[e] = load_param(p.norm_weight, 2 * lane + e, WBf16);
     }
-  }
+  };
+  if constexpr (!kLate) load_epi();
   const float dt_bias = load_param(p.dt_bias, head, DtBf16);
   const float a_log = p.a_log[head];
   __builtin_amdgcn_sched_barrier(0);
@@ -654,6 +662,8 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     s[j] = load_tile_piece<LoadPol>(src_tile, lane_bytes + tile_piece_bytes<kPair>(j));
     __builtin_amdgcn_sched_barrier(0);  // keep program order: chunk c's loads issue first
   }
+  if constexpr (kLate) load_epi();  // after the tile's loads
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- staging, while the tile streams in ----
   uint16_t v_new_split[kConvSplit ? kCols : 1];
@@ -810,14 +820,17 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
       s_db0[wave][1] = x.beta;
     }
   }
-  if (wave < Width) {
+  auto stage_epi = [&]() {
+    if (wave < Width) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) s_sg[wave][2 * lane + e] = silu(bf16_to_f32(gh[e]));
-  }
-  if (wave == 0) {
+      for (int e = 0; e < 2; ++e) s_sg[wave][2 * lane + e] = silu(bf16_to_f32(gh[e]));
+    }
+    if (wave == 0) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) s_w[2 * lane + e] = w[e];
-  }
+      for (int e = 0; e < 2; ++e) s_w[2 * lane + e] = w[e];
+    }
+  };
+  if constexpr (!kLate) stage_epi();
   if (stages_mtp) {
     const Staged x = stage_token(inw, a_log, dt_bias, p.scale);
     if (rsub == 0) {
@@ -884,6 +897,7 @@ void gdn_decode_kernel(const int32_t* md_indices, const int32_t* md_cu,
     LD_CHUNK(3)
   }
 #undef LD_CHUNK
+  if constexpr (kLate) stage_epi();  // read after the barrier below
   if constexpr (Conv) {
     if (tid == 0) s_arrived = arrived;
   }
