@@ -562,8 +562,8 @@ def host_cost(device, calls=2000):
 def prefill(device):
     """Prefill of 32 prompts x 1024 tokens, of one 4096-token prompt and of 1024 prompts x 32
     tokens (16 qk / 32 v heads, states from pool slots), timed over a few eager launches
-    each, under both algorithms (token-serial recurrence; 64-token chunks in the WY form on
-    the matrix cores); `auto_selects` is the form the default picks."""
+    each, under every algorithm (token-serial recurrence; 64- or 32-token chunks in the WY
+    form on the matrix cores); `auto_selects` is the form the default picks."""
     import torch
 
     from lightdelta_amd import _lib, ops
@@ -593,10 +593,10 @@ def prefill(device):
             out=torch.empty(total, HV, DIM, dtype=torch.bfloat16, device=device),
         )
         run = lambda: torch.ops.lightdelta.prefill(*[case[k] for k in order], 1e-6)  # noqa: E731
-        entry = {"auto_selects": "chunked" if _lib.load().ld_gdn_prefill_auto_chunked(
-            total, seqs, HV) else "token_serial"}
+        auto = _lib.load().ld_gdn_prefill_auto_chunked(total, seqs, HV)
+        entry = {"auto_selects": {0: "token_serial", 64: "chunked", 32: "chunked_32"}[auto]}
         try:
-            for algorithm in ("token_serial", "chunked"):
+            for algorithm in ("token_serial", "chunked", "chunked_32"):
                 ops.set_prefill_algorithm(algorithm)
                 run()
                 torch.cuda.synchronize()
@@ -609,12 +609,15 @@ def prefill(device):
                 torch.cuda.synchronize()
                 ms = start.elapsed_time(end) / reps
                 entry[algorithm] = {"ms": round(ms, 3), "tokens_per_s": round(total / ms * 1e3, 1)}
-                if algorithm == "chunked":
-                    # matrix-core work of the WY form per (64-token chunk, v-head): the scan's
-                    # 3,584 fp32 16x16x4 products and the prep's 640 fp32 16x16x4 (forward
-                    # substitution) and 80 bf16 16x16x32 ones (the q.k and k.k tiles)
-                    chunk_flop = (3584 + 640) * 2048 + 80 * 16384
-                    flop = seqs * -(-length // 64) * HV * chunk_flop
+                if algorithm != "token_serial":
+                    # matrix-core work of the WY form per (chunk, v-head): for 64 tokens the
+                    # scan's 3,584 fp32 16x16x4 products and the prep's 640 fp32 16x16x4
+                    # (forward substitution) and 80 bf16 16x16x32 ones (the q.k and k.k
+                    # tiles); for 32 tokens 1,664, 192 and 24
+                    c, scan, subst, tiles = ((64, 3584, 640, 80) if algorithm == "chunked"
+                                             else (32, 1664, 192, 24))
+                    chunk_flop = (scan + subst) * 2048 + tiles * 16384
+                    flop = seqs * -(-length // c) * HV * chunk_flop
                     entry[algorithm]["mfma_TFLOPs"] = round(flop / ms / 1e9, 1)
         finally:
             ops.set_prefill_algorithm(saved)

@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define LD_ABI_VERSION 11
+#define LD_ABI_VERSION 12
 
 #define LD_OK 0
 #define LD_ERR_INVALID_ARGUMENT 1
@@ -161,12 +161,12 @@ int ld_gdn_decode_conv(const ld_gdn_decode_args* args, const ld_conv_args* conv,
  * state[slots[n]] when slots[n] > 0 (an empty sequence writes its initial state back).
  * Layouts as ld_gdn_decode (qkv, a, b, gate, out row strides; state [slots, HV, 128,
  * 128]); has_initial is one byte per sequence; cu_seqlens is trusted device metadata
- * (non-decreasing, sequences contiguous from cu_seqlens[0]).  Two algorithms with the same
+ * (non-decreasing, sequences contiguous from cu_seqlens[0]).  Algorithms with the same
  * contract: token-serial (the decode's arithmetic, token by token; a head's state rows are
  * split over several workgroups when sequences x heads are too few to fill the GPU) and
- * chunked (64-token chunks in the WY form on the matrix cores; faster unless the prompts
- * are many and short; results within rounding of the token-serial ones).  Either may run
- * the norm as a second launch on the same stream.
+ * chunked (chunks of 64 or 32 tokens in the WY form on the matrix cores; faster unless the
+ * prompts are very short; results within rounding of the token-serial ones).  Either may
+ * run the norm as a second launch on the same stream.
  * Replaces the reference's prefill composition (python/lightdelta/integration/
  * vllm_layer.py:93-135: fused_post_conv_prep, gather_state with has_initial_state,
  * chunk_gated_delta_rule, scatter_state, gated RMSNorm) in one launch.
@@ -197,14 +197,15 @@ typedef struct ld_gdn_prefill_args {
   int32_t num_v_heads;
   float scale;
   float eps;
-  int32_t algorithm;       /* LD_PREFILL_AUTO / _TOKEN_SERIAL / _CHUNKED */
+  int32_t algorithm;       /* LD_PREFILL_AUTO / _TOKEN_SERIAL / _CHUNKED / _CHUNKED_32 */
   void* workspace;         /* device memory for the chunked form (NULL: not used) */
   int64_t workspace_bytes;
 } ld_gdn_prefill_args;
 
-#define LD_PREFILL_AUTO 0         /* chunked when ld_gdn_prefill_auto_chunked and the workspace fits */
+#define LD_PREFILL_AUTO 0         /* the form ld_gdn_prefill_auto_chunked names, if the workspace fits */
 #define LD_PREFILL_TOKEN_SERIAL 1 /* the decode recurrence token by token */
 #define LD_PREFILL_CHUNKED 2      /* chunks of 64 tokens in the WY form (needs the workspace) */
+#define LD_PREFILL_CHUNKED_32 3   /* chunks of 32 tokens in the WY form (needs the workspace) */
 
 int ld_gdn_prefill(const ld_gdn_prefill_args* args, void* stream);
 
@@ -232,16 +233,18 @@ int ld_gdn_prefill_static(const ld_gdn_prefill_args* args, void* stream);
  * Workspace bytes the chunked prefill needs for num_tokens rows in num_sequences sequences
  * and num_v_heads heads: one 115,712-byte record per chunk of 64 tokens and head (chunks
  * bounded by num_tokens / 64 + num_sequences), then a chunk index of num_sequences + 1
- * int32 rounded up to 256 bytes.  0 for negative arguments.
+ * int32 rounded up to 256 bytes; the 32-token form's 54,272-byte records per 32 tokens fit
+ * in the same bytes.  0 for negative arguments.
  */
 int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t num_sequences,
                                        int32_t num_v_heads);
 
 /*
- * 1 if LD_PREFILL_AUTO takes the chunked form for this shape (given a workspace), else 0:
- * prompts of 52 tokens or more on average (num_v_heads does not enter the rule on MI355X).
- * Callers use it to decide whether to provide the workspace.  No
- * counterpart in the reference (its prefill always runs chunk_gated_delta_rule).
+ * The tokens per chunk LD_PREFILL_AUTO runs for this shape (given a workspace), 64 or 32, or
+ * 0 when it runs the token-serial form.  With L = num_tokens / num_sequences: 0 for L < 20
+ * and for 32 < L <= 40; 64 for L >= 256 in fewer than 64 (sequence, head) pairs; else 32.
+ * Callers use it to decide whether to provide the workspace.  No counterpart in the
+ * reference (its prefill always runs chunk_gated_delta_rule).
  */
 int32_t ld_gdn_prefill_auto_chunked(int64_t num_tokens, int32_t num_sequences,
                                     int32_t num_v_heads);

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must precede the CDLL load (see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("liblightdelta_hip.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 CACHE_KEEP = 0
@@ -116,7 +116,7 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
-PREFILL_AUTO, PREFILL_TOKEN_SERIAL, PREFILL_CHUNKED = 0, 1, 2
+PREFILL_AUTO, PREFILL_TOKEN_SERIAL, PREFILL_CHUNKED, PREFILL_CHUNKED_32 = 0, 1, 2, 3
 PREFILL_STATIC_SCRATCH_BYTES = 64 << 20
 
 

@@ -117,20 +117,31 @@ __device__ __forceinline__ float softplus(float x) {
 // Chunked prefill (prefill_chunked.hip): workspace bytes for num_tokens rows in
 // num_sequences sequences and num_v_heads heads, and the launch of its three phases; the
 // raw outputs go to p.out for prefill_norm_kernel.
-// The shapes for which the chunked prefill beats the token-serial one on MI355X, measured
-// over 1 x 64 .. 1024 x 16 tokens at 32 v heads: every shape with prompts of 56 tokens or
-// more (1.07x at 512 x 56, 1.2x at 512 x 64 .. 10x at 1 x 4096), none with 48 or fewer but
-// 16 x 48 (a full 64-token record per chunk and head makes short prompts costly: 0.94x at
-// 1024 x 48, 0.68x at 1024 x 32, 0.40x at 1024 x 16).  The rule takes the midpoint.
-inline bool prefill_auto_chunked(int64_t num_tokens, int64_t num_sequences, int64_t num_v_heads) {
-  (void)num_v_heads;
-  if (num_sequences <= 0 || num_tokens <= 0) return false;
-  return num_tokens / num_sequences >= 52;
+// The form AUTO runs, from the mean prompt length L = num_tokens / num_sequences, measured
+// on MI355X over 1 x 64 .. 4096 x 16 tokens at 32 v heads (ms, token-serial / 64-token
+// chunks / 32-token chunks):
+//   * token-serial below 20 tokens (1024 x 16: 1.50 / 3.46 / 1.88) and for 33 .. 40, where a
+//     second 32-token chunk would hold few tokens (1024 x 36: 2.86 / 3.60 / 3.27; at 44:
+//     3.44 / 3.67 / 3.31);
+//   * 64-token chunks for long prompts in fewer than 64 (sequence, head) pairs, where the
+//     chunk-by-chunk chain is the time and 64-token chunks halve it (1 x 4096: 2.72 / 0.25 /
+//     0.39; 1 x 512: 0.36 / 0.059 / 0.067; 2 x 2048, 64 pairs: 1.40 / 0.247 / 0.237);
+//   * 32-token chunks otherwise (1024 x 32: 2.61 / 3.56 / 2.07; 32 x 1024: 2.65 / 1.59 /
+//     1.48; 1 x 64: 0.054 / 0.034 / 0.031).
+// Returns the tokens per chunk (64 or 32), or 0 for the token-serial form.
+inline int prefill_auto_chunk_tokens(int64_t num_tokens, int64_t num_sequences,
+                                     int64_t num_v_heads) {
+  if (num_sequences <= 0 || num_tokens <= 0) return 0;
+  const int64_t mean = num_tokens / num_sequences;
+  if (mean < 20 || (mean > 32 && mean <= 40)) return 0;
+  if (num_sequences * num_v_heads < 64 && mean >= 256) return 64;
+  return 32;
 }
 
 int64_t prefill_chunked_workspace_bytes(int64_t num_tokens, int64_t num_sequences,
                                         int64_t num_v_heads);
+// chunk_tokens: 64 or 32
 int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num_tokens,
-                           bool dt_bf16, void* workspace, hipStream_t stream);
+                           bool dt_bf16, int chunk_tokens, void* workspace, hipStream_t stream);
 
 }  // namespace ld

@@ -1,16 +1,16 @@
-// Chunked prefill for gfx950: the delta rule over chunks of 64 tokens in the WY form, with
-// every product on the matrix cores: products with an fp32 operand on the fp32 ones
+// Chunked prefill for gfx950: the delta rule over chunks of 64 or 32 tokens in the WY form,
+// with every product on the matrix cores: products with an fp32 operand on the fp32 ones
 // (v_mfma_f32_16x16x4_f32: fp32 operands, fp32 accumulation, so the arithmetic is the
 // vector ALUs' up to summation order), the dot products of the bf16 inputs q . k and k . k
 // on the bf16 ones (v_mfma_f32_16x16x32_bf16: the inputs as they are, exact products, fp32
 // sums; the norms are applied to the sums).
 //
-// Per chunk (tokens i = 0 .. n-1, n <= 64), with g_i the log decay, G_i = g_0 + .. + g_i,
-// Gam_ij = exp(G_i - G_j), beta_i, normalised q^_i (scaled) and k^_i, and S the state at
-// the chunk's start ([V, K], row v):
-//   A_im = beta_i Gam_im (k^_i . k^_m) for m < i            (strictly lower, 64 x 64)
+// Per chunk (tokens i = 0 .. n-1, n <= C, C = 64 or 32), with g_i the log decay,
+// G_i = g_0 + .. + g_i, Gam_ij = exp(G_i - G_j), beta_i, normalised q^_i (scaled) and k^_i,
+// and S the state at the chunk's start ([V, K], row v):
+//   A_im = beta_i Gam_im (k^_i . k^_m) for m < i            (strictly lower, C x C)
 //   (I + A) W = rows beta_i exp(G_i) k^_i,  (I + A) U = rows beta_i v_i   (forward subst.)
-//   V_new = U - W S^T                                        (64 x 128)
+//   V_new = U - W S^T                                        (C x 128)
 //   O     = (q^_i exp(G_i)) S^T + P V_new,  P_ij = Gam_ij (q^_i . k^_j) for j <= i
 //   S'    = exp(G_{n-1}) S + V_new^T (k^_j exp(G_{n-1} - G_j))
 // which equals the token-by-token recurrence of the decode kernel (checked against it in
@@ -21,11 +21,15 @@
 //                      forward substitution for W and U, and q and k with their per-token
 //                      scales; everything to workspace records.
 //   chunk_scan_kernel  one workgroup per (sequence, v-head, block of 16 or 32 state rows),
-//                      the only sequential part: chunk by chunk, V_new, the raw outputs of
+//   (64-token chunks)  the only sequential part: chunk by chunk, V_new, the raw outputs of
 //                      its columns (rounded to bf16 into `out`, the reference's rounding
 //                      point before the gated RMSNorm, which prefill_norm_kernel applies
 //                      afterwards) and the state update.  Rows evolve independently, so a
 //                      head's 128 rows spread over 8 or 4 workgroups.
+//   chunk_scan32_kernel  the same for 32-token chunks, 32 state rows per workgroup.
+// A 64-token chunk costs the same whether it holds 64 tokens or 20, so prompts shorter than
+// a chunk waste the difference; 32-token chunks halve that waste (and the scan's products
+// per token: P V_new grows with the square of the chunk), at twice the sequential steps.
 //
 // MFMA fragments (16 x 16 x 4, wave64): for lane l, li = l % 16 and lg = l / 16.  One
 // instruction takes a = A[li][kk = lg] and b = B[kk = lg][li] from every lane and adds
@@ -37,33 +41,46 @@
 namespace ld {
 namespace {
 
-constexpr int kC = 64;                          // tokens per chunk
-
-// Workspace record of one (chunk, v-head), offsets in floats.  Every operand of the scan is
-// stored in the order its loads read it -- [scan wave or tile][step group][lane][16 bytes]
-// -- so that one 16-byte-per-lane load of a wave reads 1 KiB of consecutive memory.  q and
-// k go as the bf16 inputs themselves (exact), their norms and decays as per-token scales
-// applied by the scan.  With li, lg the lane's fragment coordinates:
-//   W    [w][q < 8][lane][e]  = W[16 w + li][32 lg + 4 q + e]       (W: 64 token x 128 k)
-//   U    [b][w][lane][r]      = U[16 w + 4 lg + r][16 b + li]        (b: block of 16 v rows)
-//   P    [w][q < 4][lane][e]  = P[16 w + li][16 lg + 4 q + e]
+// Workspace record of one (chunk, v-head) for chunks of C = 16 TT tokens (TT = 4 or 2
+// token tiles), offsets in floats.  Every operand of the scan is stored in the order its
+// loads read it -- [scan wave or tile][step group][lane][16 bytes] -- so that one
+// 16-byte-per-lane load of a wave reads 1 KiB of consecutive memory.  q and k go as the
+// bf16 inputs themselves (exact), their norms and decays as per-token scales applied by the
+// scan.  With li, lg the lane's fragment coordinates:
+//   W    [w][q < 8][lane][e]   = W[16 w + li][32 lg + 4 q + e]       (W: C token x 128 k)
+//   U    [b][w][lane][r]       = U[16 w + 4 lg + r][16 b + li]        (b: block of 16 v rows)
+//   P    [w][q < TT][lane][e]  = P[16 w + li][4 TT lg + 4 q + e]
 //   Qr   [w][qq < 4][lane][e < 8] = q_i[32 lg + 8 qq + e] (bf16), i = 16 w + li
-//   Kr   [t][qq < 2][lane][e < 8] = k_j[16 t + li] (bf16), j = 16 lg + 8 qq + e
+//   Kr   [t][qq < TT/2][lane][e < 8] = k_j[16 t + li] (bf16), j = 4 TT lg + 8 qq + e
 //   misc [0] exp(G_n-1); [64 + i] sq_i = rq_i scale exp(G_i); [128 + j] ck_j = rk_j exp(G_n-1 - G_j)
-// with rq, rk the inverse L2 norms; rows past the chunk's end hold zeros.  So the scan's
-// operands are Qg = diag(sq) Qr (applied to the product's rows) and Kd = diag(ck) Kr
-// (applied to V_new's rows in the update).  Qr and Kr depend on the k-head alone: only the
-// record of a group's first v-head holds them (the others leave that space unwritten), and
-// the scans of all the group's v-heads read them there.
-constexpr int64_t kOffW = 0;
-constexpr int64_t kOffU = kOffW + kC * kDim;
-constexpr int64_t kOffP = kOffU + kDim * kC;
-constexpr int64_t kOffQr = kOffP + kC * kC;          // bf16 pairs: kC * kDim / 2 floats
-constexpr int64_t kOffKr = kOffQr + kC * kDim / 2;
-constexpr int64_t kOffMisc = kOffKr + kC * kDim / 2;
+// with w a token tile, rq, rk the inverse L2 norms; rows past the chunk's end hold zeros.
+// So the scan's operands are Qg = diag(sq) Qr (applied to the product's rows) and
+// Kd = diag(ck) Kr (applied to V_new's rows in the update).  Qr and Kr depend on the k-head
+// alone: only the record of a group's first v-head holds them (the others leave that space
+// unwritten), and the scans of all the group's v-heads read them there.
+template <int TT>
+struct Rec {
+  static constexpr int kC = 16 * TT;                         // tokens per chunk
+  static constexpr int64_t kOffW = 0;
+  static constexpr int64_t kOffU = kOffW + kC * kDim;
+  static constexpr int64_t kOffP = kOffU + kDim * kC;
+  static constexpr int64_t kOffQr = kOffP + kC * kC;         // bf16 pairs: kC * kDim / 2 floats
+  static constexpr int64_t kOffKr = kOffQr + kC * kDim / 2;
+  static constexpr int64_t kOffMisc = kOffKr + kC * kDim / 2;
+  static constexpr int64_t kSize = kOffMisc + 256;           // floats (a multiple of 64: 256 B)
+};
 constexpr int64_t kMiscSq = 64;
 constexpr int64_t kMiscCk = 128;
-constexpr int64_t kRecord = kOffMisc + 256;          // floats (a multiple of 64: 256 B)
+// the 64-token form's layout, which chunk_scan_kernel reads
+using R64 = Rec<4>;
+constexpr int kC = R64::kC;
+constexpr int64_t kOffW = R64::kOffW;
+constexpr int64_t kOffU = R64::kOffU;
+constexpr int64_t kOffP = R64::kOffP;
+constexpr int64_t kOffQr = R64::kOffQr;
+constexpr int64_t kOffKr = R64::kOffKr;
+constexpr int64_t kOffMisc = R64::kOffMisc;
+constexpr int64_t kRecord = R64::kSize;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -79,9 +96,10 @@ __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// chunk_start[n] = sum over m < n of ceil(L_m / 64) for n = 0 .. num_sequences: where the
+// chunk_start[n] = sum over m < n of ceil(L_m / C) for n = 0 .. num_sequences: where the
 // chunks of sequence n begin in the global chunk order.  One workgroup, a block-wide scan per
 // 256 sequences.
+template <int C>
 __global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int32_t* cu,
                                                                int num_sequences,
                                                                int32_t* chunk_start) {
@@ -93,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int32_t* cu
   int carry = 0;
   for (int base = 0; base < num_sequences; base += kThreads) {
     const int n = base + tid;
-    int c = n < num_sequences ? (cu[n + 1] - cu[n] + kC - 1) / kC : 0;
+    int c = n < num_sequences ? (cu[n + 1] - cu[n] + C - 1) / C : 0;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const int up = __shfl_up(c, d);
@@ -118,7 +136,8 @@ __global__ __launch_bounds__(kThreads) void chunk_index_kernel(const int32_t* cu
 // (empty sequences come before it), by a 64-way search with one wave-wide load per level
 // (one level up to 64 sequences, two up to 4096; a binary search took one dependent load per
 // halving); false past the last chunk.  Called by every lane of a wave; the results are
-// uniform.
+// uniform.  C: tokens per chunk.
+template <int C>
 __device__ bool find_chunk(const int32_t* cu, const int32_t* chunk_start, int num_sequences,
                            int g, int& seq, int& t0, int& len) {
   if (g >= chunk_start[num_sequences]) return false;
@@ -138,8 +157,8 @@ __device__ bool find_chunk(const int32_t* cu, const int32_t* chunk_start, int nu
     const int k = 63 - __clzll(static_cast<long long>(__ballot(in && start <= g)));
     if (step == 1) {
       seq = lo + k;
-      t0 = __builtin_amdgcn_readlane(row0, k) + (g - __builtin_amdgcn_readlane(start, k)) * kC;
-      len = min(kC, __builtin_amdgcn_readlane(row1, k) - t0);
+      t0 = __builtin_amdgcn_readlane(row0, k) + (g - __builtin_amdgcn_readlane(start, k)) * C;
+      len = min(C, __builtin_amdgcn_readlane(row1, k) - t0);
       return true;
     }
     lo += k * step;
@@ -154,7 +173,19 @@ constexpr uint32_t tile_code(int is_p, int mt, int nt) { return (is_p << 4) | (m
 constexpr uint32_t tiles3(uint32_t a, uint32_t b, uint32_t c = 0) {
   return a | (b << 5) | (c << 10);
 }
+// With 32-token chunks the 6 tiles go one each to waves 0-5.
+template <int TT>
 __device__ __forceinline__ uint32_t prep_tiles(int wave) {
+  if constexpr (TT == 2) {
+    switch (wave) {
+      case 0: return tile_code(0, 0, 0);
+      case 1: return tile_code(0, 1, 0);
+      case 2: return tile_code(0, 1, 1);
+      case 3: return tile_code(1, 0, 0);
+      case 4: return tile_code(1, 1, 0);
+      default: return tile_code(1, 1, 1);
+    }
+  }
   switch (wave) {
     case 0: return tiles3(tile_code(0, 0, 0), tile_code(1, 0, 0), tile_code(0, 3, 0));
     case 1: return tiles3(tile_code(0, 1, 0), tile_code(0, 1, 1), tile_code(1, 1, 0));
@@ -167,9 +198,24 @@ __device__ __forceinline__ uint32_t prep_tiles(int wave) {
   }
 }
 
+template <int TT>
+__device__ __forceinline__ int prep_tile_count(int wave) {
+  return TT == 4 ? (wave < 4 ? 3 : 2) : (wave < 6 ? 1 : 0);
+}
+
+// Offset (floats, from P's start) of the 16-byte piece of P holding P[16 mt + li][c .. c + 3],
+// c = 16 nt + 4 lg: piece [mt][q][lane (lg', li)] with 4 TT lg' + 4 q = c, so (lg', q) =
+// (nt, lg) for 64-token chunks and (2 nt + lg / 2, lg % 2) for 32-token ones.
+template <int TT>
+__device__ __forceinline__ int p_piece(int mt, int nt, int lg, int li) {
+  if constexpr (TT == 4)
+    return ((mt * 4 + lg) * 64 + nt * 16 + li) * 4;
+  else
+    return ((mt * 2 + (lg & 1)) * 64 + (2 * nt + (lg >> 1)) * 16 + li) * 4;
+}
+
 constexpr int kPrepThreads = 512;
 constexpr int kPrepWaves = kPrepThreads / 64;
-constexpr int kPrepTokens = kC / kPrepWaves;   // tokens normalised per wave
 
 // ---- phase 1: per (chunk, k-head), then per v-head of its group -----------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -183,16 +229,25 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // Wide: qkv rows at 16-byte alignment, so q, k and v come in 16-byte pieces (8 bf16 of one
 // row) instead of one or two bf16 per load: a quarter of the q / k loads and an eighth of
 // the v loads, v then transposed through LDS.  Same values, same arithmetic.
-template <bool DtBf16, bool Wide>
-__global__ __launch_bounds__(kPrepThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
+// 32-token chunks with 16-byte loads fit 80 VGPRs: three workgroups per CU instead of two
+// (the other forms need more registers and keep two).
+template <int TT, bool DtBf16, bool Wide>
+__global__ __launch_bounds__(kPrepThreads)
+__attribute__((amdgpu_waves_per_eu(TT == 2 && Wide ? 6 : 4, TT == 2 && Wide ? 6 : 4)))
 void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
                        const int32_t* chunk_start, int records) {
+  using R = Rec<TT>;
+  constexpr int kC = R::kC;
+  constexpr int64_t kOffW = R::kOffW, kOffU = R::kOffU, kOffP = R::kOffP;
+  constexpr int64_t kOffQr = R::kOffQr, kOffKr = R::kOffKr, kOffMisc = R::kOffMisc;
+  constexpr int64_t kRecord = R::kSize;
+  constexpr int kPrepTokens = kC / kPrepWaves;   // tokens normalised per wave
   const int64_t unit = blockIdx.x;   // chunk * H + k-head
   const int g = static_cast<int>(unit / p.num_k_heads);   // global chunk
   if (g >= records) return;
   const int key_head = static_cast<int>(unit - static_cast<int64_t>(g) * p.num_k_heads);
   int seq = 0, t0 = 0, len = 0;
-  if (!find_chunk(p.cu, chunk_start, num_sequences, g, seq, t0, len)) return;
+  if (!find_chunk<kC>(p.cu, chunk_start, num_sequences, g, seq, t0, len)) return;
   // the wave index in a scalar register: the tile table, the A / P choice and the W / U
   // role are then scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -204,26 +259,28 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   constexpr int kARow = kC + 4;    // padded LDS row of -A
   constexpr int kTRow = 20;        // padded LDS row of a diagonal block's inverse
   constexpr int kVCol = kC / 2 + 2;  // padded column of the v staging (token pairs, dwords)
-  // q and k (the bf16 inputs, [64][136] each) for the whole workgroup; per v-head, -A
-  // ([64][68] fp32) and above it (Wide) the U waves' v, column-major ([128][68] bf16, while
-  // they form U's right-hand side), then W ([64][132] fp32) in their place on its way to
-  // the workspace; the four inverses [4][16][20] have their own 5 KiB.
+  // q and k (the bf16 inputs, [C][136] each) for the whole workgroup; per v-head, -A
+  // ([C][C + 4] fp32) and above it (Wide) the U waves' v, column-major ([128][C + 4] bf16,
+  // while they form U's right-hand side), then W ([C][132] fp32) in their place on its way
+  // to the workspace; the inverses [TT][16][20] have their own TT * 1.25 KiB.
   constexpr int kHalfBytes = kC * kHRow * 2;
-  constexpr int kApBytes = 2 * kC * kARow * 4;
-  static_assert(kC * kRow * 4 <= kApBytes && kDim * kVCol * 4 <= kApBytes / 2, "LDS plan");
+  constexpr int kABytes = kC * kARow * 4;
+  constexpr int kVBytes = kDim * kVCol * 4;
+  constexpr int kWBytes = kC * kRow * 4;
+  constexpr int kApBytes = kWBytes > kABytes + kVBytes ? kWBytes : kABytes + kVBytes;
   __shared__ __attribute__((aligned(16))) uint8_t sQk[2 * kHalfBytes];
   __shared__ __attribute__((aligned(16))) uint8_t sAp[kApBytes];
-  __shared__ __attribute__((aligned(16))) float sT[4 * 16 * kTRow];
+  __shared__ __attribute__((aligned(16))) float sT[TT * 16 * kTRow];
   // a v-head's gates, double-buffered (v-head m in buffer m & 1): G_i, beta_i, exp(G_i),
-  // exp(G_n-1 - G_i)
-  __shared__ float sGates[2][4][kC];
+  // exp(G_n-1 - G_i), one entry per lane of the wave that forms them
+  __shared__ float sGates[2][4][64];
   __shared__ float sRq[kC];     // rq_i scale (zero past the end)
   __shared__ float sRk[kC];     // rk_i (zero past the end)
   uint16_t (*const sQh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sQk);
   uint16_t (*const sKh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sQk + kHalfBytes);
   float* const sA = reinterpret_cast<float*>(sAp);
   float* const sW = reinterpret_cast<float*>(sAp);
-  uint32_t* const sV = reinterpret_cast<uint32_t*>(sAp + kApBytes / 2);
+  uint32_t* const sV = reinterpret_cast<uint32_t*>(sAp + kABytes);
 
   // Waves 0-3 solve for W's columns 32w .. 32w + 31, waves 4-7 for U's (2 column tiles
   // each).
@@ -236,8 +293,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   // fragment layout, vr[rb][nt][r] = v of token 16 rb + 4 lg + r, column n0 + 16 nt + li,
   // or (Wide) as vw[pr][h] = columns n0 + 8 (lane & 3) .. + 7 of token 2 a + h, token pair
   // a = lane / 4 + 16 pr.
-  uint16_t vr[4][kNt][4];
-  u32x4 vw[2][2];
+  uint16_t vr[TT][kNt][4];
+  u32x4 vw[TT / 2][2];
   uint16_t gate_a = 0, gate_b = 0;
   float gate_a_log = 0.0f, gate_dt_bias = 0.0f;
   auto fetch_v = [&](int head, int li, int lg) __attribute__((always_inline)) {
@@ -245,7 +302,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     if constexpr (Wide) {
       const int lane = 16 * lg + li;
 #pragma unroll
-      for (int pr = 0; pr < 2; ++pr)
+      for (int pr = 0; pr < TT / 2; ++pr)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int64_t tok = t0 + min(2 * ((lane >> 2) + 16 * pr) + h, len - 1);
@@ -254,7 +311,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         }
     } else {
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
+      for (int rb = 0; rb < TT; ++rb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int64_t tok = t0 + min(16 * rb + 4 * lg + r, len - 1);
@@ -289,7 +346,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       if (lane >= d) G += up;
     }
     const float glast = __shfl(G, len - 1);
-    float (*const gb)[kC] = sGates[member & 1];
+    float (*const gb)[64] = sGates[member & 1];
     gb[0][lane] = G;
     gb[1][lane] = beta;
     gb[2][lane] = __expf(G);
@@ -307,9 +364,10 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     const int lane = threadIdx.x & 63;
     const int l16 = lane & 15;
     const int quarter = lane >> 4;
-    u32x4 qv[2], kv[2];
+    constexpr int kH = kPrepTokens / 4;
+    u32x4 qv[kH], kv[kH];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kH; ++h) {
       const int64_t tok = t0 + min(wave * kPrepTokens + 4 * h + quarter, len - 1);
       const uint16_t* row = p.qkv + tok * p.qkv_row;
       qv[h] = *reinterpret_cast<const u32x4*>(row + q_col + 8 * l16);
@@ -318,7 +376,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     // v of the first v-head behind q and k (loads return in order; the norms come first)
     if (solves_u) fetch_v(key_head * p.group, threadIdx.x & 15, (threadIdx.x >> 4) & 3);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kH; ++h) {
       const int i = wave * kPrepTokens + 4 * h + quarter;
       float pq[4], pk[4];
 #pragma unroll
@@ -396,8 +454,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       const int i = 16 * (item >> 8) + (l & 15);
       const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
       qdst[item] = *reinterpret_cast<const u32x4*>(&sQh[i][c0]);
-      const int k = 16 * (item >> 7) + (l & 15);
-      const int j = 16 * (l >> 4) + 8 * ((item >> 6) & 1);
+      const int k = 16 * (item >> (TT == 4 ? 7 : 6)) + (l & 15);
+      const int j = 4 * TT * (l >> 4) + 8 * ((item >> 6) & (TT / 2 - 1));
       kdst[item] = u32x4{sKh[j][k] | (static_cast<uint32_t>(sKh[j + 1][k]) << 16),
                          sKh[j + 2][k] | (static_cast<uint32_t>(sKh[j + 3][k]) << 16),
                          sKh[j + 4][k] | (static_cast<uint32_t>(sKh[j + 5][k]) << 16),
@@ -429,8 +487,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     // X[row li][32 s + 8 lg + e]), 4 steps of 32 per tile; the third tile for waves 0-3 only
     // (a uniform branch).  Recomputed for each v-head (12 products), so that no register
     // carries them from one v-head to the next.
-    const uint32_t codes = prep_tiles(wave);
-    const int tiles = wave < 4 ? 3 : 2;
+    const uint32_t codes = prep_tiles<TT>(wave);
+    const int tiles = prep_tile_count<TT>(wave);
     f32x4 prod[3];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
@@ -456,14 +514,14 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 
     // the right-hand sides in the fragment layout: x[rb][nt][r] = B[16 rb + 4 lg + r][n0 + 16 nt + li]
     // (one uniform branch around two straight-line loops)
-    f32x4 x[4][kNt];
+    f32x4 x[TT][kNt];
     if (solves_u) {
       if constexpr (Wide) {
         // the wave's 32 columns of v to LDS column by column, a dword per token pair, and
         // back in the fragment layout (4 tokens of one column per 8-byte read); the wave's
         // own region, so program order is the only ordering needed
 #pragma unroll
-        for (int pr = 0; pr < 2; ++pr) {
+        for (int pr = 0; pr < TT / 2; ++pr) {
           const int a = (lane >> 2) + 16 * pr;
           const int c0 = n0 + 8 * (lane & 3);
 #pragma unroll
@@ -475,7 +533,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
           }
         }
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+        for (int rb = 0; rb < TT; ++rb)
 #pragma unroll
           for (int nt = 0; nt < kNt; ++nt) {
             const uint2 t4 = *reinterpret_cast<const uint2*>(
@@ -488,7 +546,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
           }
       } else {
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+        for (int rb = 0; rb < TT; ++rb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float beta = sBeta[16 * rb + 4 * lg + r];  // zero past the end
@@ -498,7 +556,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
     } else {
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
+      for (int rb = 0; rb < TT; ++rb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * rb + 4 * lg + r;
@@ -515,8 +573,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     else if (tid < 2 * kC)
       rec[kOffMisc + kMiscCk + tid - kC] = sRk[tid - kC] * sEk[tid - kC];
 
-    // scale the tiles: A (negated) to LDS; P straight to the record, where its piece
-    // [row tile mt][q = lg][lane (li, column tile nt)] holds P[16 mt + li][16 nt + 4 lg + r]
+    // scale the tiles: A (negated) to LDS; P straight to the record, a lane's four results
+    // P[16 mt + li][16 nt + 4 lg + r] being one 16-byte piece of it (p_piece)
     // (the products are of the raw inputs: q^_i . k^_m = (rq_i scale rk_m) (q_i . k_m))
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
@@ -535,7 +593,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
           const float gam = __expf(gi - sG[m]);
           piece[r] = (m <= i && i < len) ? gam * ((rqi * sRk[m]) * prod[t][r]) : 0.0f;
         }
-        *reinterpret_cast<f32x4*>(rec + kOffP + ((mt * 4 + lg) * 64 + nt * 16 + li) * 4) = piece;
+        *reinterpret_cast<f32x4*>(rec + kOffP + p_piece<TT>(mt, nt, lg, li)) = piece;
       } else {
         const int m = 16 * nt + li;
         const float gm = sG[m];
@@ -548,22 +606,21 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         }
       }
     }
-    // P's six tiles above the diagonal, (row tile, column tile) = (0, 1..3), (1, 2..3),
-    // (2, 3): zeros, one 16-byte piece per thread
-    if (tid < 6 * 64) {
+    // P's tiles above the diagonal, (row tile, column tile) = (0, 1..3), (1, 2..3), (2, 3)
+    // (64-token chunks) or (0, 1): zeros, one 16-byte piece per thread
+    if (tid < TT * (TT - 1) / 2 * 64) {
       const int z = tid >> 6;
       const int mt = z < 3 ? 0 : (z < 5 ? 1 : 2);
       const int nt = z < 3 ? z + 1 : (z < 5 ? z - 1 : 3);
-      *reinterpret_cast<f32x4*>(rec + kOffP + ((mt * 4 + lg) * 64 + nt * 16 + li) * 4) =
-          f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      *reinterpret_cast<f32x4*>(rec + kOffP + p_piece<TT>(mt, nt, lg, li)) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     __syncthreads();
     if (wave == 4 && next) gates(member + 1, lane);
     // the U waves are idle here; the next v-head forms its right-hand side from these
     if (solves_u && next) fetch_v(head + 1, li, lg);
     // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
-    // (block w by wave w < 4)
-    if (wave < 4 && lane < 16) {
+    // (block w by wave w < TT)
+    if (wave < TT && lane < 16) {
       const float* ab = sA + (16 * wave) * kARow + 16 * wave;
       // row by row: col[i] = delta(i, li) + sum over m < i of (-A)[i][m] col[m], the terms in
       // order of m (row i of -A read as it is needed)
@@ -583,7 +640,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 
     // blocked forward substitution: X_rb = T_rb (B_rb - sum over j < rb of A_rb,j X_j)
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < TT; ++rb) {
       f32x4 y[kNt];
 #pragma unroll
       for (int nt = 0; nt < kNt; ++nt) y[nt] = x[rb][nt];
@@ -615,16 +672,16 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     // the region of -A and the v staging)
     if (solves_u) {
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
+      for (int rb = 0; rb < TT; ++rb)
 #pragma unroll
         for (int nt = 0; nt < kNt; ++nt)
-          *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * 4 + rb) * 256 + lane * 4) =
+          *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * TT + rb) * 256 + lane * 4) =
               x[rb][nt];
     }
     __syncthreads();
     if (!solves_u) {
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
+      for (int rb = 0; rb < TT; ++rb)
 #pragma unroll
         for (int nt = 0; nt < kNt; ++nt)
 #pragma unroll
@@ -680,6 +737,20 @@ struct OutputOperands {
 // pressure.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t record_resource(const float* r, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(r), 0, bytes, 0x00020000);
+}
+
+// The state tile of (slot, head) as a buffer resource: over its 64 KiB when the sequence
+// starts from it, else over 0 bytes, whose loads return zeros without touching memory.  Its
+// loads then need no branch and go out together (a branch per load, as `from_slot ? load :
+// 0` compiles, waited for each load before the next was issued).  Callers pass the whole
+// offset per lane, so the range check sees all of it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t state_resource(const DecodeParams& p, int slot,
+                                                                 int head, bool from_slot) {
+  // (uniform: readfirstlane keeps the resource in scalar registers, where a vector-held one
+  // would put each load in a loop over its distinct values)
+  return record_resource(
+      p.state + static_cast<int64_t>(slot) * p.state_slot + static_cast<int64_t>(head) * kDim * kDim,
+      __builtin_amdgcn_readfirstlane(from_slot ? kDim * kDim * 4 : 0));
 }
 
 // bf16 by the hardware's round-to-nearest-even conversion (v_cvt_pk_bf16_f32): the same
@@ -851,16 +922,18 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
     // st[t][h][r] = S[row0 + 16 h + li][16 (2w + t) + 4 lg + r]
     float* tile_base = p.state + static_cast<int64_t>(slot) * p.state_slot +
                        static_cast<int64_t>(head) * kDim * kDim + (row0 + li) * kDim;
+    const __amdgpu_buffer_rsrc_t srs = state_resource(p, slot, head, from_slot);
+    const uint32_t soff = static_cast<uint32_t>(((row0 + li) * kDim + 32 * w + 4 * lg) * 4);
     f32x4 st[2][RT];
 #pragma unroll
     for (int h = 0; h < RT; ++h)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int k = 16 * (2 * w + t) + 4 * lg;
-        st[t][h] = from_slot ? *reinterpret_cast<const f32x4*>(tile_base + 16 * h * kDim + k)
-                             : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        *reinterpret_cast<f32x4*>(&sS[16 * h + li][k]) = st[t][h];
-      }
+      for (int t = 0; t < 2; ++t) st[t][h] = load16(srs, soff + (16 * h * kDim + 16 * t) * 4, 0);
+#pragma unroll
+    for (int h = 0; h < RT; ++h)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        *reinterpret_cast<f32x4*>(&sS[16 * h + li][16 * (2 * w + t) + 4 * lg]) = st[t][h];
     // Operands of later chunks are loaded while chunk c computes: into a ring of three
     // register sets (the loop is unrolled by three, so no set is copied: each is waited for
     // only where it is used), or into the one set as its pieces fall free.
@@ -1079,42 +1152,319 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   }
 }
 
+// ---- phase 2, 32-token chunks: per (sequence, v-head, block of 32 state rows) ----------
+// Eight waves, two per SIMD, each on one (token tile a, row tile h) = (w & 1, w >> 1) of the
+// chunk: state wave w (0..3) forms V_new of that tile, then updates k tiles 2w and 2w + 1 of
+// both row tiles; output wave 4 + w forms the raw outputs of that tile.  Per chunk and SIMD
+// that is 104 products of 16 x 16 x 4 for 32 tokens, against 224 for 64 tokens in
+// chunk_scan_kernel<2> (P V_new grows with the square of the chunk).
+struct Scan32State {
+  f32x4 w[8];   // W [16 a + li][32 lg + 4 q + e]
+  u32x4 kr[2];  // Kr^T [16 (2w + t) + li][8 lg + e] (bf16)
+  f32x4 u;      // U [16 a + 4 lg + r][row0 + 16 h + li]
+  f32x4 ck;     // ck of tokens 16 a + 4 lg + r
+  float gamma;  // exp(G_n-1)
+};
+
+struct Scan32Output {
+  u32x4 qr[4];  // Qr [16 a + li][32 lg + 8 qq + e] (bf16)
+  f32x4 sq;     // sq of tokens 16 a + 4 lg + r
+  f32x4 p[2];   // P [16 a + li][8 lg + 4 q + e]
+};
+
+// The operand loads in pieces, as in chunk_scan_kernel: a state wave's W, U and ck pieces
+// (q < 2: W step groups 2q, 2q + 1, 2q + 4, 2q + 5, with U and ck at q = 0) are refilled
+// for the next chunk during the update, its Kr pieces and gamma (piece 2) during this
+// chunk's V_new products; an output wave's P (piece 2) during this chunk's q S^T products,
+// its Qr and sq (q < 2: step groups 2q, 2q + 1, with sq at q = 0) during P V_new.
+__device__ __forceinline__ void load_state32(Scan32State& o, __amdgpu_buffer_rsrc_t rs, int own,
+                                             int w, int a, int utile, uint32_t lane16,
+                                             uint32_t lg16, int piece) {
+  using R = Rec<2>;
+  if (piece < 2) {
+    const int wbase = own + static_cast<int>(R::kOffW * 4) + a * 8 * 1024;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int q = 2 * piece + e;
+      o.w[q] = load16(rs, lane16, wbase + q * 1024);
+      o.w[q + 4] = load16(rs, lane16, wbase + (q + 4) * 1024);
+    }
+    if (piece == 0) {
+      o.u = load16(rs, lane16, own + static_cast<int>(R::kOffU * 4) + (utile * 2 + a) * 1024);
+      o.ck = load16(rs, lg16, own + static_cast<int>((R::kOffMisc + kMiscCk) * 4) + a * 64);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      o.kr[t] = load16u(rs, lane16, static_cast<int>(R::kOffKr * 4) + (2 * w + t) * 1024);
+    o.gamma = load4(rs, own + static_cast<int>(R::kOffMisc * 4));
+  }
+}
+
+__device__ __forceinline__ void load_output32(Scan32Output& o, __amdgpu_buffer_rsrc_t rs, int own,
+                                              int a, uint32_t lane16, uint32_t lg16, int piece) {
+  using R = Rec<2>;
+  if (piece < 2) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      o.qr[2 * piece + e] =
+          load16u(rs, lane16, static_cast<int>(R::kOffQr * 4) + (a * 4 + 2 * piece + e) * 1024);
+    if (piece == 0)
+      o.sq = load16(rs, lg16, own + static_cast<int>((R::kOffMisc + kMiscSq) * 4) + a * 64);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      o.p[q] = load16(rs, lane16, own + static_cast<int>(R::kOffP * 4) + (a * 2 + q) * 1024);
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads)
+void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
+                         const int32_t* chunk_start, int records) {
+  using R = Rec<2>;
+  constexpr int kCs = R::kC;                 // 32 tokens per chunk
+  constexpr int kRows = 32;                  // state rows per workgroup
+  constexpr int kBlocks = kDim / kRows;
+  // XCD-aware ids as in chunk_scan_kernel: the 4 row blocks of one (sequence, head) on one XCD
+  const int xcd = blockIdx.x & 7;
+  const int rank = blockIdx.x >> 3;
+  const int pair = (rank / kBlocks) * 8 + xcd;
+  if (pair >= num_sequences * p.num_v_heads) return;
+  const int seq = pair / p.num_v_heads;
+  const int head = pair - seq * p.num_v_heads;
+  const int row_block = rank % kBlocks;
+  const int row0 = row_block * kRows;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const uint32_t lane16 = static_cast<uint32_t>(lane) * 16;
+  const uint32_t lg16 = static_cast<uint32_t>(lg) * 16;
+  const int w = wave & 3;
+  const int a = w & 1;    // the wave's token tile
+  const int h = w >> 1;   // the wave's row tile
+  const int bos = p.cu[seq];
+  const int eos = p.cu[seq + 1];
+  const int slot = p.indices[seq];
+  const bool from_slot = slot > 0 && p.has_initial[seq] != 0;
+  const int gbase = chunk_start[seq];
+  const int chunks = min((eos - bos + kCs - 1) / kCs, max(records - gbase, 0));
+
+  constexpr int kSRow = kDim + 4;
+  constexpr int kVRow = kCs + 4;
+  __shared__ __attribute__((aligned(16))) float sS[kRows][kSRow];   // S rows [row][k]
+  __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];  // V_new^T [row][token]
+  __shared__ __attribute__((aligned(16))) float sVk[kRows][kVRow];  // ditto, token j times ck_j
+
+  const int member = head % p.group;
+  const int own = member * static_cast<int>(R::kSize * 4);
+  const int group_bytes = p.group * static_cast<int>(R::kSize * 4);
+  // chunk c's records; past the last chunk a resource over 0 bytes, whose loads return
+  // zeros without touching memory (the refills stay unconditional, so the waits that follow
+  // them stay exact)
+  auto record = [&](int c) {
+    return record_resource(
+        ws + (static_cast<int64_t>(gbase + min(c, chunks - 1)) * p.num_v_heads + head - member) *
+                 R::kSize,
+        c < chunks ? group_bytes : 0);
+  };
+  auto s_fragment = [&](int q) {   // S^T for k = 32 lg + 4 q + e, rows 16 h + li
+    return *reinterpret_cast<const f32x4*>(&sS[16 * h + li][32 * lg + 4 * q]);
+  };
+
+  if (wave < 4) {
+    // The wave's pieces of the state, S[row0 + 16 hh + li][16 (2w + t) + 4 lg + r], live in
+    // sS between chunks (re-read for the update, not held in registers through V_new).
+    float* tile_base = p.state + static_cast<int64_t>(slot) * p.state_slot +
+                       static_cast<int64_t>(head) * kDim * kDim + (row0 + li) * kDim;
+    auto own_piece = [&](int t, int hh) -> f32x4& {
+      return *reinterpret_cast<f32x4*>(&sS[16 * hh + li][16 * (2 * w + t) + 4 * lg]);
+    };
+    // the first chunk's W, U and ck go out before the state's loads, so that their latencies
+    // overlap (the state is waited for first, to reach sS)
+    const int utile = row_block * 2 + h;
+    Scan32State op;
+    if (chunks > 0) {
+      const __amdgpu_buffer_rsrc_t r = record(0);
+#pragma unroll
+      for (int piece = 0; piece < 2; ++piece) {
+        load_state32(op, r, own, w, a, utile, lane16, lg16, piece);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    {
+      const __amdgpu_buffer_rsrc_t srs = state_resource(p, slot, head, from_slot);
+      const uint32_t soff = static_cast<uint32_t>(((row0 + li) * kDim + 32 * w + 4 * lg) * 4);
+      f32x4 st[2][2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) st[t][hh] = load16(srs, soff + (16 * hh * kDim + 16 * t) * 4, 0);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) own_piece(t, hh) = st[t][hh];
+    }
+    for (int c = 0; c < chunks; ++c) {
+      const __amdgpu_buffer_rsrc_t cur = record(c);
+      const __amdgpu_buffer_rsrc_t next = record(c + 1);
+      __syncthreads();  // sS holds the state at the chunk's start
+      f32x4 vn0 = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 vn1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (q == 0) load_state32(op, cur, own, w, a, utile, lane16, lg16, 2);
+        const f32x4 b0 = s_fragment(q);
+        const f32x4 b1 = s_fragment(q + 4);
+        vn0 = mfma(op.w[q].x, b0.x, vn0);
+        vn1 = mfma(op.w[q + 4].x, b1.x, vn1);
+        vn0 = mfma(op.w[q].y, b0.y, vn0);
+        vn1 = mfma(op.w[q + 4].y, b1.y, vn1);
+        vn0 = mfma(op.w[q].z, b0.z, vn0);
+        vn1 = mfma(op.w[q + 4].z, b1.z, vn1);
+        vn0 = mfma(op.w[q].w, b0.w, vn0);
+        vn1 = mfma(op.w[q + 4].w, b1.w, vn1);
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
+      }
+      const f32x4 vn = op.u - (vn0 + vn1);
+      *reinterpret_cast<f32x4*>(&sVn[16 * h + li][16 * a + 4 * lg]) = vn;
+      *reinterpret_cast<f32x4*>(&sVk[16 * h + li][16 * a + 4 * lg]) = vn * op.ck;
+      __syncthreads();  // V_new complete; every read of sS for this chunk done
+      f32x4 st[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) st[t][hh] = own_piece(t, hh) * op.gamma;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        load_state32(op, next, own, w, a, utile, lane16, lg16, q);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          // V_new k ck for tokens j = 8 lg + 4 q + e, rows 16 hh + li
+          const f32x4 b = *reinterpret_cast<const f32x4*>(&sVk[16 * hh + li][8 * lg + 4 * q]);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const f32x4 ka = bf16x4(op.kr[t], q);
+            st[t][hh] = mfma(ka.x, b.x, st[t][hh]);
+            st[t][hh] = mfma(ka.y, b.y, st[t][hh]);
+            st[t][hh] = mfma(ka.z, b.z, st[t][hh]);
+            st[t][hh] = mfma(ka.w, b.w, st[t][hh]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) own_piece(t, hh) = st[t][hh];
+    }
+    // the wave's own pieces: its LDS accesses complete in order, so no barrier is needed
+    if (slot > 0) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          *reinterpret_cast<f32x4*>(tile_base + 16 * hh * kDim + 16 * (2 * w + t) + 4 * lg) =
+              own_piece(t, hh);
+    }
+  } else {
+    const int out_row = p.num_v_heads * kDim;   // elements per token row of out
+    uint16_t* out_block = p.out + static_cast<int64_t>(head) * kDim + row0;
+    Scan32Output op;
+    if (chunks > 0) {
+      const __amdgpu_buffer_rsrc_t r = record(0);
+#pragma unroll
+      for (int piece = 0; piece < 2; ++piece) {
+        load_output32(op, r, own, a, lane16, lg16, piece);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    for (int c = 0; c < chunks; ++c) {
+      const __amdgpu_buffer_rsrc_t cur = record(c);
+      const __amdgpu_buffer_rsrc_t next = record(c + 1);
+      __syncthreads();  // sS holds the state at the chunk's start
+      f32x4 o0 = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 o1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (q == 0) load_output32(op, cur, own, a, lane16, lg16, 2);   // P of this chunk
+        const f32x4 b0 = s_fragment(q);
+        const f32x4 b1 = s_fragment(q + 4);
+        const f32x4 a0 = bf16x4(op.qr[q >> 1], q & 1);
+        const f32x4 a1 = bf16x4(op.qr[2 + (q >> 1)], q & 1);
+        o0 = mfma(a0.x, b0.x, o0);
+        o1 = mfma(a1.x, b1.x, o1);
+        o0 = mfma(a0.y, b0.y, o0);
+        o1 = mfma(a1.y, b1.y, o1);
+        o0 = mfma(a0.z, b0.z, o0);
+        o1 = mfma(a1.z, b1.z, o1);
+        o0 = mfma(a0.w, b0.w, o0);
+        o1 = mfma(a1.w, b1.w, o1);
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
+      }
+      // rows of q S^T scaled to (q^ exp(G)) S^T; P V_new accumulates on top
+      o0 = (o0 + o1) * op.sq;
+      o1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      __syncthreads();  // V_new complete
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        load_output32(op, next, own, a, lane16, lg16, q);   // Qr and sq of the next chunk
+        // V_new for tokens j = 8 lg + 4 q + e, rows 16 h + li
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&sVn[16 * h + li][8 * lg + 4 * q]);
+        f32x4& o = q == 0 ? o0 : o1;
+        o = mfma(op.p[q].x, b.x, o);
+        o = mfma(op.p[q].y, b.y, o);
+        o = mfma(op.p[q].z, b.z, o);
+        o = mfma(op.p[q].w, b.w, o);
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
+      }
+      // raw outputs of tokens 16 a + 4 lg + r, column row0 + 16 h + li (rows past the
+      // sequence's end fall outside the buffer and are dropped)
+      const int t0 = bos + c * kCs;
+      const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+          out_block + static_cast<int64_t>(t0) * out_row, 0, min(kCs, eos - t0) * out_row * 2,
+          0x00020000);
+      const f32x4 o = o0 + o1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_raw_buffer_store_b16(
+            to_bf16(o[r]), ors, ((16 * a + 4 * lg + r) * out_row + 16 * h + li) * 2, 0, 0);
+    }
+  }
+}
+
+template <int C>
 int64_t max_chunks(int64_t num_tokens, int64_t num_sequences) {
-  return num_tokens / kC + num_sequences;  // each sequence adds at most one partial chunk
+  return num_tokens / C + num_sequences;  // each sequence adds at most one partial chunk
 }
 
 // Workspace: the records, then chunk_start (num_sequences + 1 int32, rounded up to 256 B).
+// Sized for 64-token chunks, which covers 32-token ones: with S >= 1 sequences,
+// (T / 32 + S) R32 <= (2 (T / 64) + 1 + S) R32 <= (T / 64 + S) R64 as 2 R32 <= R64.
+static_assert(2 * Rec<2>::kSize <= Rec<4>::kSize, "32-token records fit the workspace");
 int64_t records_bytes(int64_t num_tokens, int64_t num_sequences, int64_t num_v_heads) {
-  return max_chunks(num_tokens, num_sequences) * num_v_heads * kRecord * 4;
+  return max_chunks<kC>(num_tokens, num_sequences) * num_v_heads * kRecord * 4;
 }
 
-}  // namespace
-
-int64_t prefill_chunked_workspace_bytes(int64_t num_tokens, int64_t num_sequences,
-                                        int64_t num_v_heads) {
-  return records_bytes(num_tokens, num_sequences, num_v_heads) +
-         ((num_sequences + 1) * 4 + 255) / 256 * 256;
-}
-
-int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num_tokens,
-                           bool dt_bf16, void* workspace, hipStream_t stream) {
-  float* ws = static_cast<float*>(workspace);
-  int32_t* chunk_start = reinterpret_cast<int32_t*>(
-      static_cast<char*>(workspace) + records_bytes(num_tokens, num_sequences, p.num_v_heads));
-  const int64_t chunks = max_chunks(num_tokens, num_sequences);
+template <int TT>
+int launch_chunks(const DecodeParams& p, int num_sequences, int64_t num_tokens, bool dt_bf16,
+                  float* ws, int32_t* chunk_start, hipStream_t stream) {
+  constexpr int kCt = Rec<TT>::kC;
+  const int64_t chunks = max_chunks<kCt>(num_tokens, num_sequences);
   if (chunks > 0x7fffffff || p.num_v_heads > 65535)
     return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large for the chunked form");
   // one workgroup per (chunk, k-head)
   const int64_t prep_groups = chunks * p.num_k_heads;
   if (prep_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
   const dim3 per_chunk(static_cast<uint32_t>(prep_groups));
-  hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kThreads), 0, stream, p.cu, num_sequences,
-                     chunk_start);
+  hipLaunchKernelGGL(chunk_index_kernel<kCt>, dim3(1), dim3(kThreads), 0, stream, p.cu,
+                     num_sequences, chunk_start);
   // 16-byte pieces of q, k and v when every row starts at a 16-byte boundary
   const bool wide = (reinterpret_cast<uintptr_t>(p.qkv) & 15) == 0 && (p.qkv_row & 7) == 0;
 #define LD_PREP_LAUNCH(D, W)                                                                   \
-  hipLaunchKernelGGL((chunk_prep_kernel<D, W>), per_chunk, dim3(kPrepThreads), 0, stream, p,  \
-                     num_sequences, ws, chunk_start, static_cast<int>(chunks))
+  hipLaunchKernelGGL((chunk_prep_kernel<TT, D, W>), per_chunk, dim3(kPrepThreads), 0, stream, \
+                     p, num_sequences, ws, chunk_start, static_cast<int>(chunks))
   if (dt_bf16) {
     if (wide)
       LD_PREP_LAUNCH(true, true);
@@ -1128,19 +1478,45 @@ int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num
   }
 #undef LD_PREP_LAUNCH
   const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
-  // two row tiles per workgroup once they still give 2 workgroups per CU
-  const bool two_tiles = pairs * (kDim / 32) >= 512;
-  const int64_t scan_groups = (pairs + 7) / 8 * 8 * (two_tiles ? kDim / 32 : kDim / 16);
-  if (scan_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
-  if (two_tiles)
-    hipLaunchKernelGGL(chunk_scan_kernel<2>, dim3(static_cast<uint32_t>(scan_groups)),
+  if constexpr (TT == 2) {
+    const int64_t scan_groups = (pairs + 7) / 8 * 8 * (kDim / 32);
+    if (scan_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
+    hipLaunchKernelGGL(chunk_scan32_kernel, dim3(static_cast<uint32_t>(scan_groups)),
                        dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
                        static_cast<int>(chunks));
-  else
-    hipLaunchKernelGGL(chunk_scan_kernel<1>, dim3(static_cast<uint32_t>(scan_groups)),
-                       dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
-                       static_cast<int>(chunks));
+  } else {
+    // two row tiles per workgroup once they still give 2 workgroups per CU
+    const bool two_tiles = pairs * (kDim / 32) >= 512;
+    const int64_t scan_groups = (pairs + 7) / 8 * 8 * (two_tiles ? kDim / 32 : kDim / 16);
+    if (scan_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
+    if (two_tiles)
+      hipLaunchKernelGGL(chunk_scan_kernel<2>, dim3(static_cast<uint32_t>(scan_groups)),
+                         dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
+                         static_cast<int>(chunks));
+    else
+      hipLaunchKernelGGL(chunk_scan_kernel<1>, dim3(static_cast<uint32_t>(scan_groups)),
+                         dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
+                         static_cast<int>(chunks));
+  }
   return check_launch("ld_gdn_prefill (chunked)");
+}
+
+}  // namespace
+
+int64_t prefill_chunked_workspace_bytes(int64_t num_tokens, int64_t num_sequences,
+                                        int64_t num_v_heads) {
+  return records_bytes(num_tokens, num_sequences, num_v_heads) +
+         ((num_sequences + 1) * 4 + 255) / 256 * 256;
+}
+
+int launch_prefill_chunked(const DecodeParams& p, int num_sequences, int64_t num_tokens,
+                           bool dt_bf16, int chunk_tokens, void* workspace, hipStream_t stream) {
+  float* ws = static_cast<float*>(workspace);
+  int32_t* chunk_start = reinterpret_cast<int32_t*>(
+      static_cast<char*>(workspace) + records_bytes(num_tokens, num_sequences, p.num_v_heads));
+  if (chunk_tokens == 32)
+    return launch_chunks<2>(p, num_sequences, num_tokens, dt_bf16, ws, chunk_start, stream);
+  return launch_chunks<4>(p, num_sequences, num_tokens, dt_bf16, ws, chunk_start, stream);
 }
 
 }  // namespace ld

@@ -472,7 +472,7 @@ __global__ __launch_bounds__(kThreads) void prefill_norm_wide_kernel(const Decod
 int prefill(const ld_gdn_prefill_args& a, void* workspace, int64_t workspace_bytes,
             void* stream) {
   if (a.num_sequences < 0) return fail(LD_ERR_INVALID_ARGUMENT, "num_sequences must be >= 0");
-  if (a.algorithm < LD_PREFILL_AUTO || a.algorithm > LD_PREFILL_CHUNKED)
+  if (a.algorithm < LD_PREFILL_AUTO || a.algorithm > LD_PREFILL_CHUNKED_32)
     return fail(LD_ERR_INVALID_ARGUMENT, "unknown prefill algorithm");
   if (a.num_k_heads <= 0 || a.num_v_heads <= 0 || a.num_v_heads % a.num_k_heads != 0)
     return fail(LD_ERR_INVALID_ARGUMENT, "num_v_heads must be a positive multiple of num_k_heads");
@@ -521,15 +521,21 @@ int prefill(const ld_gdn_prefill_args& a, void* workspace, int64_t workspace_byt
   const int64_t ws_need = prefill_chunked_workspace_bytes(a.num_tokens, a.num_sequences,
                                                           a.num_v_heads);
   const bool ws_fits = workspace != nullptr && workspace_bytes >= ws_need;
-  if (a.algorithm == LD_PREFILL_CHUNKED && !ws_fits)
+  const bool named_chunked =
+      a.algorithm == LD_PREFILL_CHUNKED || a.algorithm == LD_PREFILL_CHUNKED_32;
+  if (named_chunked && !ws_fits)
     return fail(LD_ERR_INVALID_ARGUMENT, "chunked prefill: workspace missing or too small");
-  const bool chunked =
-      a.algorithm == LD_PREFILL_CHUNKED ||
-      (a.algorithm == LD_PREFILL_AUTO && ws_fits &&
-       prefill_auto_chunked(a.num_tokens, a.num_sequences, a.num_v_heads));
+  // tokens per chunk of the chunked form, 0 for the token-serial one
+  const int chunk_tokens =
+      a.algorithm == LD_PREFILL_CHUNKED      ? 64
+      : a.algorithm == LD_PREFILL_CHUNKED_32 ? 32
+      : a.algorithm == LD_PREFILL_AUTO && ws_fits
+          ? prefill_auto_chunk_tokens(a.num_tokens, a.num_sequences, a.num_v_heads)
+          : 0;
+  const bool chunked = chunk_tokens != 0;
   if (chunked) {
     const int rc = launch_prefill_chunked(p, a.num_sequences, a.num_tokens, dt_bf16,
-                                          workspace, s);
+                                          chunk_tokens, workspace, s);
     if (rc != LD_OK) return rc;
   }
   // Token-serial: split a head's rows over more workgroups when (sequence, head) tiles alone
@@ -647,11 +653,13 @@ extern "C" int ld_gdn_prefill_static(const ld_gdn_prefill_args* args, void* stre
     return prefill(a, nullptr, 0, stream);  // rejected there with its message
   const int64_t need = prefill_chunked_workspace_bytes(a.num_tokens, a.num_sequences,
                                                        a.num_v_heads);
+  const bool named_chunked =
+      a.algorithm == LD_PREFILL_CHUNKED || a.algorithm == LD_PREFILL_CHUNKED_32;
   const bool wants_chunked =
-      a.algorithm == LD_PREFILL_CHUNKED ||
+      named_chunked ||
       (a.algorithm == LD_PREFILL_AUTO &&
-       prefill_auto_chunked(a.num_tokens, a.num_sequences, a.num_v_heads));
-  if (a.algorithm == LD_PREFILL_CHUNKED && need > kStaticScratchBytes)
+       prefill_auto_chunk_tokens(a.num_tokens, a.num_sequences, a.num_v_heads) != 0);
+  if (named_chunked && need > kStaticScratchBytes)
     return fail(LD_ERR_INVALID_ARGUMENT,
                 "ld_gdn_prefill_static: the chunked form needs more workspace than the static "
                 "scratch holds (LD_PREFILL_STATIC_SCRATCH_BYTES); use LD_PREFILL_TOKEN_SERIAL, "
@@ -672,5 +680,5 @@ extern "C" int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t nu
 
 extern "C" int32_t ld_gdn_prefill_auto_chunked(int64_t num_tokens, int32_t num_sequences,
                                                int32_t num_v_heads) {
-  return ld::prefill_auto_chunked(num_tokens, num_sequences, num_v_heads) ? 1 : 0;
+  return ld::prefill_auto_chunk_tokens(num_tokens, num_sequences, num_v_heads);
 }

@@ -277,12 +277,13 @@ def check_prefill(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, sta
                         gate, weight, out, eps)
 
 
-# Prefill algorithm: "auto" runs 64-token chunks in the WY form for the shapes where they are
-# faster (ld_gdn_prefill_auto_chunked: prompts of 52 tokens or more on average), else the
-# token-serial recurrence; "token_serial" and "chunked" force one.  Results agree within
-# rounding; the token-serial form reproduces the decode kernel bit for bit.
+# Prefill algorithm: "auto" runs chunks in the WY form, of 64 or 32 tokens, for the shapes
+# where they are faster (ld_gdn_prefill_auto_chunked gives the chunk length, 0 for none),
+# else the token-serial recurrence; "token_serial", "chunked" (64-token chunks) and
+# "chunked_32" force one.  Results agree within rounding; the token-serial form reproduces
+# the decode kernel bit for bit.
 _PREFILL_ALGORITHMS = {"auto": _lib.PREFILL_AUTO, "token_serial": _lib.PREFILL_TOKEN_SERIAL,
-                       "chunked": _lib.PREFILL_CHUNKED}
+                       "chunked": _lib.PREFILL_CHUNKED, "chunked_32": _lib.PREFILL_CHUNKED_32}
 _prefill_algorithm = _lib.PREFILL_AUTO
 
 
@@ -339,9 +340,9 @@ def _prefill_impl(qkv, a, b, a_log, dt_bias, slots, has_initial, cu_seqlens, sta
         return
     lib = _lib.load()
     algorithm = _prefill_algorithm
-    chunked = algorithm == _lib.PREFILL_CHUNKED or (
+    chunked = algorithm in (_lib.PREFILL_CHUNKED, _lib.PREFILL_CHUNKED_32) or (
         algorithm == _lib.PREFILL_AUTO
-        and lib.ld_gdn_prefill_auto_chunked(qkv.shape[0], slots.numel(), hv) == 1)
+        and lib.ld_gdn_prefill_auto_chunked(qkv.shape[0], slots.numel(), hv) != 0)
     workspace = None
     if chunked:
         nbytes = lib.ld_gdn_prefill_workspace_bytes(qkv.shape[0], slots.numel(), hv)

@@ -165,15 +165,22 @@ def test_prefill_workspace_query_and_chunked_without_workspace():
 
 
 @pytest.mark.parametrize("tokens,sequences,heads,expected", [
-    (4096, 1, 32, 1),        # one long prompt
-    (32 * 1024, 32, 32, 1),  # long prompts that fill the GPU anyway
-    (16 * 128, 16, 32, 1),   # 128-token prompts, 512 (sequence, head) tiles
-    (512 * 64, 512, 32, 1),  # 64-token prompts, 16384 tiles
-    (4 * 64, 4, 32, 1),
-    (1024 * 52, 1024, 32, 1),  # the shortest prompts that go chunked
-    (512 * 52 - 1, 512, 32, 0),  # a mean just under 52 tokens
-    (1024 * 48, 1024, 32, 0),
-    (1024 * 32, 1024, 32, 0),  # short prompts
+    (4096, 1, 32, 64),        # one long prompt: 64-token chunks halve its chain of chunks
+    (512, 1, 32, 64),
+    (4096, 1, 63, 64),        # 63 (sequence, head) pairs
+    (4096, 1, 64, 32),        # 64 pairs
+    (2 * 2048, 2, 32, 32),
+    (255, 1, 32, 32),         # a mean under 256 tokens
+    (32 * 1024, 32, 32, 32),  # long prompts that fill the GPU anyway
+    (16 * 128, 16, 32, 32),
+    (512 * 64, 512, 32, 32),
+    (1024 * 32, 1024, 32, 32),  # short prompts: one full 32-token chunk each
+    (1024 * 20, 1024, 32, 32),  # the shortest that go chunked
+    (1024 * 20 - 1, 1024, 32, 0),
+    (1024 * 16, 1024, 32, 0),
+    (1024 * 33, 1024, 32, 0),   # a second chunk that would hold few tokens
+    (1024 * 41 - 1, 1024, 32, 0),
+    (1024 * 41, 1024, 32, 32),
     (2 * 16, 2, 32, 0),
     (0, 1, 32, 0),
     (100, 0, 32, 0),

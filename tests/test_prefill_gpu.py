@@ -1,7 +1,7 @@
 """Parity of the gfx950 prefill (torch.ops.lightdelta.prefill) with the oracle's restatement
-of the layer's prefill (oracle/decode.py expected_prefill), under both algorithms
-(token-serial, and 64-token chunks in the WY form); and, for the token-serial one, with the
-decode kernel: a prefill of n tokens must give bit for bit the states and outputs of n
+of the layer's prefill (oracle/decode.py expected_prefill), under every algorithm
+(token-serial, and 64- or 32-token chunks in the WY form); and, for the token-serial one, with
+the decode kernel: a prefill of n tokens must give bit for bit the states and outputs of n
 single-token decode steps on the same slot (the per-token arithmetic is shared)."""
 
 from __future__ import annotations
@@ -49,7 +49,10 @@ def run(case, eps=1e-6):
     torch.ops.lightdelta.prefill(*[case[k] for k in PREFILL], eps)
 
 
-@pytest.fixture(params=["token_serial", "chunked"])
+CHUNKED_FORMS = ["chunked", "chunked_32"]
+
+
+@pytest.fixture(params=["token_serial", *CHUNKED_FORMS])
 def algorithm(request):
     saved = ops.prefill_algorithm()
     ops.set_prefill_algorithm(request.param)
@@ -236,9 +239,9 @@ def test_split_and_fused_paths_agree(gpu, sequences, token_serial):
     assert torch.equal(case["pool"], batch_pool)
 
 
-def chunked_against_token_serial(case):
-    """Runs `case` under the token-serial and the chunked form from the same pool; checks the
-    chunked results within the build's tolerance of the token-serial ones."""
+def chunked_against_token_serial(case, form):
+    """Runs `case` under the token-serial and the chunked form `form` from the same pool;
+    checks the chunked results within the build's tolerance of the token-serial ones."""
     pool0 = case["pool"].clone()
     saved = ops.prefill_algorithm()
     try:
@@ -248,7 +251,7 @@ def chunked_against_token_serial(case):
         ref_out, ref_pool = case["out"].clone(), case["pool"].clone()
         case["pool"].copy_(pool0)
         case["out"].zero_()
-        ops.set_prefill_algorithm("chunked")
+        ops.set_prefill_algorithm(form)
         run(case)
         torch.cuda.synchronize()
     finally:
@@ -259,31 +262,34 @@ def chunked_against_token_serial(case):
     assert close.float().mean() > 0.999
 
 
-def test_chunked_long_prompts_match_the_token_serial_form(gpu):
+@pytest.mark.parametrize("form", CHUNKED_FORMS)
+def test_chunked_long_prompts_match_the_token_serial_form(gpu, form):
     """Two prompts of 1000 and 3000 tokens (partial last chunks) under the chunked form:
     within the build's tolerance of the token-serial results after thousands of steps."""
-    announce(test="prefill_chunked_long")
+    announce(test="prefill_chunked_long", form=form)
     case = prefill_case(gpu, [1000, 3000], seed=11)
     case["has_initial"][0] = False
-    chunked_against_token_serial(case)
+    chunked_against_token_serial(case, form)
 
 
-def test_chunked_two_row_tiles_over_many_chunks(gpu):
+@pytest.mark.parametrize("form", CHUNKED_FORMS)
+def test_chunked_two_row_tiles_over_many_chunks(gpu, form):
     """16 prompts of 200 to 330 tokens (partial last chunks), 16 qk / 32 v heads: 512
     (sequence, head) pairs, so the scan takes two 16-row state tiles per workgroup with one
     operand set refilled half a chunk ahead, over several chunks per sequence."""
-    announce(test="prefill_chunked_two_row_tiles")
+    announce(test="prefill_chunked_two_row_tiles", form=form)
     gen = torch.Generator().manual_seed(15)
     lengths = torch.randint(200, 331, (16,), generator=gen).tolist()
     case = prefill_case(gpu, lengths, seed=15)
     case["has_initial"][1::3] = False
-    chunked_against_token_serial(case)
+    chunked_against_token_serial(case, form)
 
 
-def test_chunked_many_sequences_match_the_token_serial_form(gpu):
+@pytest.mark.parametrize("form", CHUNKED_FORMS)
+def test_chunked_many_sequences_match_the_token_serial_form(gpu, form):
     """300 sequences of 0 to 150 tokens (empty ones among them; more sequences than one round
     of the chunk-index scan covers), some from zero states, one on the padding slot."""
-    announce(test="prefill_chunked_many")
+    announce(test="prefill_chunked_many", form=form)
     gen = torch.Generator().manual_seed(12)
     lengths = torch.randint(0, 151, (300,), generator=gen).tolist()
     lengths[0] = lengths[150] = lengths[299] = 0
@@ -291,20 +297,34 @@ def test_chunked_many_sequences_match_the_token_serial_form(gpu):
     case = prefill_case(gpu, lengths, seed=12)
     case["has_initial"][::7] = False
     case["slots"][3] = 0
-    chunked_against_token_serial(case)
+    chunked_against_token_serial(case, form)
 
 
+@pytest.mark.parametrize("form", CHUNKED_FORMS)
+def test_chunked_short_prompts_match_the_token_serial_form(gpu, form):
+    """1024 prompts of 1 to 48 tokens (one or two 32-token chunks each, a part of one 64-token
+    chunk), the shapes the 32-token form is for; some from zero states."""
+    announce(test="prefill_chunked_short", form=form)
+    gen = torch.Generator().manual_seed(31)
+    lengths = torch.randint(1, 49, (1024,), generator=gen).tolist()
+    lengths[5], lengths[6], lengths[7] = 32, 33, 31
+    case = prefill_case(gpu, lengths, seed=31)
+    case["has_initial"][::5] = False
+    chunked_against_token_serial(case, form)
+
+
+@pytest.mark.parametrize("form", CHUNKED_FORMS)
 @pytest.mark.parametrize("layout", ["odd_row_stride", "shifted_base"])
-def test_chunked_unaligned_rows_match_aligned_rows(gpu, layout):
+def test_chunked_unaligned_rows_match_aligned_rows(gpu, layout, form):
     """qkv rows that do not start at 16-byte boundaries (an odd row stride, or a base one
     element past one) take the chunked prep's one- and two-element loads instead of its
     16-byte pieces: the same values and arithmetic, so the same bits."""
-    announce(test="prefill_chunked_unaligned", layout=layout)
+    announce(test="prefill_chunked_unaligned", layout=layout, form=form)
     case = prefill_case(gpu, [130, 64, 7, 200, 0, 65], seed=21)
     case["has_initial"][1] = False
     pool0 = case["pool"].clone()
     saved = ops.prefill_algorithm()
-    ops.set_prefill_algorithm("chunked")
+    ops.set_prefill_algorithm(form)
     try:
         run(case)
         torch.cuda.synchronize()
@@ -376,13 +396,14 @@ def test_rows_outside_every_sequence_are_left_alone(gpu, algorithm):
         assert_states(case["pool"], exp_pool, label=f"cu={cu}")
 
 
+@pytest.mark.parametrize("form", CHUNKED_FORMS)
 @pytest.mark.parametrize("keys", ["identical", "alternating", "near_parallel"])
-def test_chunked_with_adversarial_keys(gpu, keys):
+def test_chunked_with_adversarial_keys(gpu, keys, form):
     """Keys that make I + A of the WY form as far from the identity as it gets: every token
     of a sequence with the same key, keys of alternating sign, or keys within 1e-3 of each
     other; beta near 1 and decay near 1 (b = 6, a = -8).  The chunked form against the
-    oracle's token-by-token recurrence, over 200 tokens (4 chunks)."""
-    announce(test="prefill_chunked_adversarial", keys=keys)
+    oracle's token-by-token recurrence, over 200 tokens (4 or 7 chunks)."""
+    announce(test="prefill_chunked_adversarial", keys=keys, form=form)
     case = prefill_case(gpu, [200, 70], seed=21)
     saved = ops.prefill_algorithm()
     h, hv = 16, 32
@@ -402,7 +423,7 @@ def test_chunked_with_adversarial_keys(gpu, keys):
     case["a"].fill_(-8.0)
     exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6, return_pre=True)
     try:
-        ops.set_prefill_algorithm("chunked")
+        ops.set_prefill_algorithm(form)
         run(case)
         torch.cuda.synchronize()
     finally:

@@ -80,7 +80,8 @@ def assert_same(results, label):
 
 
 def test_static_scratch_matches_caller_workspace_twice(gpu):
-    """Two calls in a row, the second with a smaller input, chunked form forced."""
+    """Two calls in a row, the second with a smaller input, chunked form forced; then AUTO
+    and the 32-token form."""
     first = prefill_case([300, 337], seed=1, device=gpu)
     need = _lib.load().ld_gdn_prefill_workspace_bytes(637, 2, HV)
     assert need <= _lib.PREFILL_STATIC_SCRATCH_BYTES
@@ -91,6 +92,8 @@ def test_static_scratch_matches_caller_workspace_twice(gpu):
     assert_same(run_both(second, _lib.PREFILL_CHUNKED), "second call")
     announce(test="no_alloc", call=3, tokens=130, algorithm="auto")
     assert_same(run_both(second, _lib.PREFILL_AUTO), "auto")
+    announce(test="no_alloc", call=4, tokens=637, algorithm="chunked_32")
+    assert_same(run_both(first, _lib.PREFILL_CHUNKED_32), "32-token chunks")
 
 
 def test_static_beyond_scratch_runs_token_serial_or_refuses(gpu):
