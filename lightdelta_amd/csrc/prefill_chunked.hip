@@ -41,46 +41,58 @@
 namespace ld {
 namespace {
 
-// Workspace record of one (chunk, v-head) for chunks of C = 16 TT tokens (TT = 4 or 2
-// token tiles), offsets in floats.  Every operand of the scan is stored in the order its
-// loads read it -- [scan wave or tile][step group][lane][16 bytes] -- so that one
-// 16-byte-per-lane load of a wave reads 1 KiB of consecutive memory.  q and k go as the
-// bf16 inputs themselves (exact), their norms and decays as per-token scales applied by the
-// scan.  With li, lg the lane's fragment coordinates:
-//   W    [w][q < 8][lane][e]   = W[16 w + li][32 lg + 4 q + e]       (W: C token x 128 k)
-//   U    [b][w][lane][r]       = U[16 w + 4 lg + r][16 b + li]        (b: block of 16 v rows)
-//   P    [w][q < TT][lane][e]  = P[16 w + li][4 TT lg + 4 q + e]
+constexpr int kC = 64;                          // tokens per chunk (64-token form)
+
+// Workspace record of one (chunk, v-head) of the 64-token form, offsets in floats.  Every
+// operand of the scan is stored in the order its loads read it -- [scan wave or tile][step
+// group][lane][16 bytes] -- so that one 16-byte-per-lane load of a wave reads 1 KiB of
+// consecutive memory.  q and k go as the bf16 inputs themselves (exact), their norms and
+// decays as per-token scales applied by the scan.  With li, lg the lane's fragment
+// coordinates:
+//   W    [w][q < 8][lane][e]  = W[16 w + li][32 lg + 4 q + e]       (W: 64 token x 128 k)
+//   U    [b][w][lane][r]      = U[16 w + 4 lg + r][16 b + li]        (b: block of 16 v rows)
+//   P    [w][q < 4][lane][e]  = P[16 w + li][16 lg + 4 q + e]
 //   Qr   [w][qq < 4][lane][e < 8] = q_i[32 lg + 8 qq + e] (bf16), i = 16 w + li
-//   Kr   [t][qq < TT/2][lane][e < 8] = k_j[16 t + li] (bf16), j = 4 TT lg + 8 qq + e
+//   Kr   [t][qq < 2][lane][e < 8] = k_j[16 t + li] (bf16), j = 16 lg + 8 qq + e
 //   misc [0] exp(G_n-1); [64 + i] sq_i = rq_i scale exp(G_i); [128 + j] ck_j = rk_j exp(G_n-1 - G_j)
 // with w a token tile, rq, rk the inverse L2 norms; rows past the chunk's end hold zeros.
 // So the scan's operands are Qg = diag(sq) Qr (applied to the product's rows) and
 // Kd = diag(ck) Kr (applied to V_new's rows in the update).  Qr and Kr depend on the k-head
 // alone: only the record of a group's first v-head holds them (the others leave that space
 // unwritten), and the scans of all the group's v-heads read them there.
-template <int TT>
-struct Rec {
-  static constexpr int kC = 16 * TT;                         // tokens per chunk
-  static constexpr int64_t kOffW = 0;
-  static constexpr int64_t kOffU = kOffW + kC * kDim;
-  static constexpr int64_t kOffP = kOffU + kDim * kC;
-  static constexpr int64_t kOffQr = kOffP + kC * kC;         // bf16 pairs: kC * kDim / 2 floats
-  static constexpr int64_t kOffKr = kOffQr + kC * kDim / 2;
-  static constexpr int64_t kOffMisc = kOffKr + kC * kDim / 2;
-  static constexpr int64_t kSize = kOffMisc + 256;           // floats (a multiple of 64: 256 B)
-};
+constexpr int64_t kOffW = 0;
+constexpr int64_t kOffU = kOffW + kC * kDim;
+constexpr int64_t kOffP = kOffU + kDim * kC;
+constexpr int64_t kOffQr = kOffP + kC * kC;          // bf16 pairs: kC * kDim / 2 floats
+constexpr int64_t kOffKr = kOffQr + kC * kDim / 2;
+constexpr int64_t kOffMisc = kOffKr + kC * kDim / 2;
 constexpr int64_t kMiscSq = 64;
 constexpr int64_t kMiscCk = 128;
-// the 64-token form's layout, which chunk_scan_kernel reads
-using R64 = Rec<4>;
-constexpr int kC = R64::kC;
-constexpr int64_t kOffW = R64::kOffW;
-constexpr int64_t kOffU = R64::kOffU;
-constexpr int64_t kOffP = R64::kOffP;
-constexpr int64_t kOffQr = R64::kOffQr;
-constexpr int64_t kOffKr = R64::kOffKr;
-constexpr int64_t kOffMisc = R64::kOffMisc;
-constexpr int64_t kRecord = R64::kSize;
+constexpr int64_t kRecord = kOffMisc + 256;          // floats (a multiple of 64: 256 B)
+
+// The 32-token form keeps (I + A)^-1 itself instead of W and U: with T = (I + A)^-1,
+//   V_new = U - W S^T = T (diag(beta) V - diag(ws) K S^T),  ws_i = beta_i exp(G_i) rk_i,
+// where the scan forms K S^T from the bf16 keys and reads V from qkv, so a record carries
+// 4 KiB of T where W and U took 32 KiB.  Record of one (chunk, v-head), offsets in floats:
+//   T    [w][q < 2][lane][e]  = T[16 w + li][8 lg + 4 q + e]         (32 x 32, lower)
+//   P    [w][q < 2][lane][e]  = P[16 w + li][8 lg + 4 q + e]
+//   Qr   [w][qq < 4][lane][e < 8] = q_i[32 lg + 8 qq + e] (bf16), i = 16 w + li
+//   Kq   [w][qq < 4][lane][e < 8] = k_i[32 lg + 8 qq + e] (bf16), i = 16 w + li
+//   Kr   [t][lane][e < 8]     = k_j[16 t + li] (bf16), j = 8 lg + e
+//   misc as above, and [160 + i] beta_i, [192 + i] ws_i
+// Qr, Kq and Kr, as in the 64-token record, only in the record of a group's first v-head.
+struct Rec32 {
+  static constexpr int kC = 32;
+  static constexpr int64_t kOffT = 0;
+  static constexpr int64_t kOffP = kOffT + kC * kC;
+  static constexpr int64_t kOffQr = kOffP + kC * kC;
+  static constexpr int64_t kOffKq = kOffQr + kC * kDim / 2;
+  static constexpr int64_t kOffKr = kOffKq + kC * kDim / 2;
+  static constexpr int64_t kOffMisc = kOffKr + kC * kDim / 2;
+  static constexpr int64_t kSize = kOffMisc + 256;
+};
+constexpr int64_t kMiscBeta = 160;
+constexpr int64_t kMiscWs = 192;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -173,19 +185,7 @@ constexpr uint32_t tile_code(int is_p, int mt, int nt) { return (is_p << 4) | (m
 constexpr uint32_t tiles3(uint32_t a, uint32_t b, uint32_t c = 0) {
   return a | (b << 5) | (c << 10);
 }
-// With 32-token chunks the 6 tiles go one each to waves 0-5.
-template <int TT>
 __device__ __forceinline__ uint32_t prep_tiles(int wave) {
-  if constexpr (TT == 2) {
-    switch (wave) {
-      case 0: return tile_code(0, 0, 0);
-      case 1: return tile_code(0, 1, 0);
-      case 2: return tile_code(0, 1, 1);
-      case 3: return tile_code(1, 0, 0);
-      case 4: return tile_code(1, 1, 0);
-      default: return tile_code(1, 1, 1);
-    }
-  }
   switch (wave) {
     case 0: return tiles3(tile_code(0, 0, 0), tile_code(1, 0, 0), tile_code(0, 3, 0));
     case 1: return tiles3(tile_code(0, 1, 0), tile_code(0, 1, 1), tile_code(1, 1, 0));
@@ -198,24 +198,9 @@ __device__ __forceinline__ uint32_t prep_tiles(int wave) {
   }
 }
 
-template <int TT>
-__device__ __forceinline__ int prep_tile_count(int wave) {
-  return TT == 4 ? (wave < 4 ? 3 : 2) : (wave < 6 ? 1 : 0);
-}
-
-// Offset (floats, from P's start) of the 16-byte piece of P holding P[16 mt + li][c .. c + 3],
-// c = 16 nt + 4 lg: piece [mt][q][lane (lg', li)] with 4 TT lg' + 4 q = c, so (lg', q) =
-// (nt, lg) for 64-token chunks and (2 nt + lg / 2, lg % 2) for 32-token ones.
-template <int TT>
-__device__ __forceinline__ int p_piece(int mt, int nt, int lg, int li) {
-  if constexpr (TT == 4)
-    return ((mt * 4 + lg) * 64 + nt * 16 + li) * 4;
-  else
-    return ((mt * 2 + (lg & 1)) * 64 + (2 * nt + (lg >> 1)) * 16 + li) * 4;
-}
-
 constexpr int kPrepThreads = 512;
 constexpr int kPrepWaves = kPrepThreads / 64;
+constexpr int kPrepTokens = kC / kPrepWaves;   // tokens normalised per wave
 
 // ---- phase 1: per (chunk, k-head), then per v-head of its group -----------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -229,19 +214,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // Wide: qkv rows at 16-byte alignment, so q, k and v come in 16-byte pieces (8 bf16 of one
 // row) instead of one or two bf16 per load: a quarter of the q / k loads and an eighth of
 // the v loads, v then transposed through LDS.  Same values, same arithmetic.
-// 32-token chunks with 16-byte loads fit 80 VGPRs: three workgroups per CU instead of two
-// (the other forms need more registers and keep two).
-template <int TT, bool DtBf16, bool Wide>
-__global__ __launch_bounds__(kPrepThreads)
-__attribute__((amdgpu_waves_per_eu(TT == 2 && Wide ? 6 : 4, TT == 2 && Wide ? 6 : 4)))
+template <bool DtBf16, bool Wide>
+__global__ __launch_bounds__(kPrepThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
                        const int32_t* chunk_start, int records) {
-  using R = Rec<TT>;
-  constexpr int kC = R::kC;
-  constexpr int64_t kOffW = R::kOffW, kOffU = R::kOffU, kOffP = R::kOffP;
-  constexpr int64_t kOffQr = R::kOffQr, kOffKr = R::kOffKr, kOffMisc = R::kOffMisc;
-  constexpr int64_t kRecord = R::kSize;
-  constexpr int kPrepTokens = kC / kPrepWaves;   // tokens normalised per wave
   const int64_t unit = blockIdx.x;   // chunk * H + k-head
   const int g = static_cast<int>(unit / p.num_k_heads);   // global chunk
   if (g >= records) return;
@@ -259,28 +235,26 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   constexpr int kARow = kC + 4;    // padded LDS row of -A
   constexpr int kTRow = 20;        // padded LDS row of a diagonal block's inverse
   constexpr int kVCol = kC / 2 + 2;  // padded column of the v staging (token pairs, dwords)
-  // q and k (the bf16 inputs, [C][136] each) for the whole workgroup; per v-head, -A
-  // ([C][C + 4] fp32) and above it (Wide) the U waves' v, column-major ([128][C + 4] bf16,
-  // while they form U's right-hand side), then W ([C][132] fp32) in their place on its way
-  // to the workspace; the inverses [TT][16][20] have their own TT * 1.25 KiB.
+  // q and k (the bf16 inputs, [64][136] each) for the whole workgroup; per v-head, -A
+  // ([64][68] fp32) and above it (Wide) the U waves' v, column-major ([128][68] bf16, while
+  // they form U's right-hand side), then W ([64][132] fp32) in their place on its way to
+  // the workspace; the four inverses [4][16][20] have their own 5 KiB.
   constexpr int kHalfBytes = kC * kHRow * 2;
-  constexpr int kABytes = kC * kARow * 4;
-  constexpr int kVBytes = kDim * kVCol * 4;
-  constexpr int kWBytes = kC * kRow * 4;
-  constexpr int kApBytes = kWBytes > kABytes + kVBytes ? kWBytes : kABytes + kVBytes;
+  constexpr int kApBytes = 2 * kC * kARow * 4;
+  static_assert(kC * kRow * 4 <= kApBytes && kDim * kVCol * 4 <= kApBytes / 2, "LDS plan");
   __shared__ __attribute__((aligned(16))) uint8_t sQk[2 * kHalfBytes];
   __shared__ __attribute__((aligned(16))) uint8_t sAp[kApBytes];
-  __shared__ __attribute__((aligned(16))) float sT[TT * 16 * kTRow];
+  __shared__ __attribute__((aligned(16))) float sT[4 * 16 * kTRow];
   // a v-head's gates, double-buffered (v-head m in buffer m & 1): G_i, beta_i, exp(G_i),
-  // exp(G_n-1 - G_i), one entry per lane of the wave that forms them
-  __shared__ float sGates[2][4][64];
+  // exp(G_n-1 - G_i)
+  __shared__ float sGates[2][4][kC];
   __shared__ float sRq[kC];     // rq_i scale (zero past the end)
   __shared__ float sRk[kC];     // rk_i (zero past the end)
   uint16_t (*const sQh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sQk);
   uint16_t (*const sKh)[kHRow] = reinterpret_cast<uint16_t (*)[kHRow]>(sQk + kHalfBytes);
   float* const sA = reinterpret_cast<float*>(sAp);
   float* const sW = reinterpret_cast<float*>(sAp);
-  uint32_t* const sV = reinterpret_cast<uint32_t*>(sAp + kABytes);
+  uint32_t* const sV = reinterpret_cast<uint32_t*>(sAp + kApBytes / 2);
 
   // Waves 0-3 solve for W's columns 32w .. 32w + 31, waves 4-7 for U's (2 column tiles
   // each).
@@ -293,8 +267,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
   // fragment layout, vr[rb][nt][r] = v of token 16 rb + 4 lg + r, column n0 + 16 nt + li,
   // or (Wide) as vw[pr][h] = columns n0 + 8 (lane & 3) .. + 7 of token 2 a + h, token pair
   // a = lane / 4 + 16 pr.
-  uint16_t vr[TT][kNt][4];
-  u32x4 vw[TT / 2][2];
+  uint16_t vr[4][kNt][4];
+  u32x4 vw[2][2];
   uint16_t gate_a = 0, gate_b = 0;
   float gate_a_log = 0.0f, gate_dt_bias = 0.0f;
   auto fetch_v = [&](int head, int li, int lg) __attribute__((always_inline)) {
@@ -302,7 +276,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     if constexpr (Wide) {
       const int lane = 16 * lg + li;
 #pragma unroll
-      for (int pr = 0; pr < TT / 2; ++pr)
+      for (int pr = 0; pr < 2; ++pr)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int64_t tok = t0 + min(2 * ((lane >> 2) + 16 * pr) + h, len - 1);
@@ -311,7 +285,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         }
     } else {
 #pragma unroll
-      for (int rb = 0; rb < TT; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int64_t tok = t0 + min(16 * rb + 4 * lg + r, len - 1);
@@ -346,7 +320,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       if (lane >= d) G += up;
     }
     const float glast = __shfl(G, len - 1);
-    float (*const gb)[64] = sGates[member & 1];
+    float (*const gb)[kC] = sGates[member & 1];
     gb[0][lane] = G;
     gb[1][lane] = beta;
     gb[2][lane] = __expf(G);
@@ -364,10 +338,9 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     const int lane = threadIdx.x & 63;
     const int l16 = lane & 15;
     const int quarter = lane >> 4;
-    constexpr int kH = kPrepTokens / 4;
-    u32x4 qv[kH], kv[kH];
+    u32x4 qv[2], kv[2];
 #pragma unroll
-    for (int h = 0; h < kH; ++h) {
+    for (int h = 0; h < 2; ++h) {
       const int64_t tok = t0 + min(wave * kPrepTokens + 4 * h + quarter, len - 1);
       const uint16_t* row = p.qkv + tok * p.qkv_row;
       qv[h] = *reinterpret_cast<const u32x4*>(row + q_col + 8 * l16);
@@ -376,7 +349,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     // v of the first v-head behind q and k (loads return in order; the norms come first)
     if (solves_u) fetch_v(key_head * p.group, threadIdx.x & 15, (threadIdx.x >> 4) & 3);
 #pragma unroll
-    for (int h = 0; h < kH; ++h) {
+    for (int h = 0; h < 2; ++h) {
       const int i = wave * kPrepTokens + 4 * h + quarter;
       float pq[4], pk[4];
 #pragma unroll
@@ -454,8 +427,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       const int i = 16 * (item >> 8) + (l & 15);
       const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
       qdst[item] = *reinterpret_cast<const u32x4*>(&sQh[i][c0]);
-      const int k = 16 * (item >> (TT == 4 ? 7 : 6)) + (l & 15);
-      const int j = 4 * TT * (l >> 4) + 8 * ((item >> 6) & (TT / 2 - 1));
+      const int k = 16 * (item >> 7) + (l & 15);
+      const int j = 16 * (l >> 4) + 8 * ((item >> 6) & 1);
       kdst[item] = u32x4{sKh[j][k] | (static_cast<uint32_t>(sKh[j + 1][k]) << 16),
                          sKh[j + 2][k] | (static_cast<uint32_t>(sKh[j + 3][k]) << 16),
                          sKh[j + 4][k] | (static_cast<uint32_t>(sKh[j + 5][k]) << 16),
@@ -487,8 +460,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     // X[row li][32 s + 8 lg + e]), 4 steps of 32 per tile; the third tile for waves 0-3 only
     // (a uniform branch).  Recomputed for each v-head (12 products), so that no register
     // carries them from one v-head to the next.
-    const uint32_t codes = prep_tiles<TT>(wave);
-    const int tiles = prep_tile_count<TT>(wave);
+    const uint32_t codes = prep_tiles(wave);
+    const int tiles = wave < 4 ? 3 : 2;
     f32x4 prod[3];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
@@ -514,14 +487,14 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 
     // the right-hand sides in the fragment layout: x[rb][nt][r] = B[16 rb + 4 lg + r][n0 + 16 nt + li]
     // (one uniform branch around two straight-line loops)
-    f32x4 x[TT][kNt];
+    f32x4 x[4][kNt];
     if (solves_u) {
       if constexpr (Wide) {
         // the wave's 32 columns of v to LDS column by column, a dword per token pair, and
         // back in the fragment layout (4 tokens of one column per 8-byte read); the wave's
         // own region, so program order is the only ordering needed
 #pragma unroll
-        for (int pr = 0; pr < TT / 2; ++pr) {
+        for (int pr = 0; pr < 2; ++pr) {
           const int a = (lane >> 2) + 16 * pr;
           const int c0 = n0 + 8 * (lane & 3);
 #pragma unroll
@@ -533,7 +506,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
           }
         }
 #pragma unroll
-        for (int rb = 0; rb < TT; ++rb)
+        for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
           for (int nt = 0; nt < kNt; ++nt) {
             const uint2 t4 = *reinterpret_cast<const uint2*>(
@@ -546,7 +519,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
           }
       } else {
 #pragma unroll
-        for (int rb = 0; rb < TT; ++rb)
+        for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float beta = sBeta[16 * rb + 4 * lg + r];  // zero past the end
@@ -556,7 +529,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
     } else {
 #pragma unroll
-      for (int rb = 0; rb < TT; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * rb + 4 * lg + r;
@@ -573,8 +546,8 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     else if (tid < 2 * kC)
       rec[kOffMisc + kMiscCk + tid - kC] = sRk[tid - kC] * sEk[tid - kC];
 
-    // scale the tiles: A (negated) to LDS; P straight to the record, a lane's four results
-    // P[16 mt + li][16 nt + 4 lg + r] being one 16-byte piece of it (p_piece)
+    // scale the tiles: A (negated) to LDS; P straight to the record, where its piece
+    // [row tile mt][q = lg][lane (li, column tile nt)] holds P[16 mt + li][16 nt + 4 lg + r]
     // (the products are of the raw inputs: q^_i . k^_m = (rq_i scale rk_m) (q_i . k_m))
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
@@ -593,7 +566,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
           const float gam = __expf(gi - sG[m]);
           piece[r] = (m <= i && i < len) ? gam * ((rqi * sRk[m]) * prod[t][r]) : 0.0f;
         }
-        *reinterpret_cast<f32x4*>(rec + kOffP + p_piece<TT>(mt, nt, lg, li)) = piece;
+        *reinterpret_cast<f32x4*>(rec + kOffP + ((mt * 4 + lg) * 64 + nt * 16 + li) * 4) = piece;
       } else {
         const int m = 16 * nt + li;
         const float gm = sG[m];
@@ -606,21 +579,22 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
         }
       }
     }
-    // P's tiles above the diagonal, (row tile, column tile) = (0, 1..3), (1, 2..3), (2, 3)
-    // (64-token chunks) or (0, 1): zeros, one 16-byte piece per thread
-    if (tid < TT * (TT - 1) / 2 * 64) {
+    // P's six tiles above the diagonal, (row tile, column tile) = (0, 1..3), (1, 2..3),
+    // (2, 3): zeros, one 16-byte piece per thread
+    if (tid < 6 * 64) {
       const int z = tid >> 6;
       const int mt = z < 3 ? 0 : (z < 5 ? 1 : 2);
       const int nt = z < 3 ? z + 1 : (z < 5 ? z - 1 : 3);
-      *reinterpret_cast<f32x4*>(rec + kOffP + p_piece<TT>(mt, nt, lg, li)) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      *reinterpret_cast<f32x4*>(rec + kOffP + ((mt * 4 + lg) * 64 + nt * 16 + li) * 4) =
+          f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     __syncthreads();
     if (wave == 4 && next) gates(member + 1, lane);
     // the U waves are idle here; the next v-head forms its right-hand side from these
     if (solves_u && next) fetch_v(head + 1, li, lg);
     // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
-    // (block w by wave w < TT)
-    if (wave < TT && lane < 16) {
+    // (block w by wave w < 4)
+    if (wave < 4 && lane < 16) {
       const float* ab = sA + (16 * wave) * kARow + 16 * wave;
       // row by row: col[i] = delta(i, li) + sum over m < i of (-A)[i][m] col[m], the terms in
       // order of m (row i of -A read as it is needed)
@@ -640,7 +614,7 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
 
     // blocked forward substitution: X_rb = T_rb (B_rb - sum over j < rb of A_rb,j X_j)
 #pragma unroll
-    for (int rb = 0; rb < TT; ++rb) {
+    for (int rb = 0; rb < 4; ++rb) {
       f32x4 y[kNt];
 #pragma unroll
       for (int nt = 0; nt < kNt; ++nt) y[nt] = x[rb][nt];
@@ -672,16 +646,16 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     // the region of -A and the v staging)
     if (solves_u) {
 #pragma unroll
-      for (int rb = 0; rb < TT; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
         for (int nt = 0; nt < kNt; ++nt)
-          *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * TT + rb) * 256 + lane * 4) =
+          *reinterpret_cast<f32x4*>(rec + kOffU + (((n0 >> 4) + nt) * 4 + rb) * 256 + lane * 4) =
               x[rb][nt];
     }
     __syncthreads();
     if (!solves_u) {
 #pragma unroll
-      for (int rb = 0; rb < TT; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
         for (int nt = 0; nt < kNt; ++nt)
 #pragma unroll
@@ -702,6 +676,332 @@ void chunk_prep_kernel(const DecodeParams p, int num_sequences, float* ws,
     }
     // the next v-head rewrites the gates, -A, P and W
     __syncthreads();
+  }
+}
+
+// ---- phase 1, 32-token chunks: per (chunk, k-head), then per v-head of its group -----------
+// Four waves.  The q/k part -- loads, inverse norms, the raw q.k and k.k tiles on the bf16
+// matrix cores, the bf16 queries and keys to the record -- once; then per v-head the gates,
+// the per-token scales, the scaled A (to LDS) and P (to the record), the inverses T0, T1 of
+// I + A's diagonal blocks, the block T10 = -T1 A10 T0 below them, and T to the record.  No
+// forward substitution over v or k columns, and no v: the scan applies T itself.
+constexpr int kPrep32Threads = 256;
+
+// Offset (floats, from the start of P or T) of the 16-byte piece holding X[16 mt + li][c ..
+// c + 3], c = 16 nt + 4 lg, in the layout [mt][q][lane (lg', li)][e] with 8 lg' + 4 q = c.
+__device__ __forceinline__ int piece32(int mt, int nt, int lg, int li) {
+  return ((mt * 2 + (lg & 1)) * 64 + (2 * nt + (lg >> 1)) * 16 + li) * 4;
+}
+
+// The 6 tiles of A (K K^T) and P (Q K^T) on or below the diagonal, as tile_code: A00, A10,
+// A11, P00, P10, P11; wave w takes tiles w and w + 4.
+__device__ __forceinline__ uint32_t prep32_tile(int index) {
+  switch (index) {
+    case 0: return tile_code(0, 0, 0);
+    case 1: return tile_code(0, 1, 0);
+    case 2: return tile_code(0, 1, 1);
+    case 3: return tile_code(1, 0, 0);
+    case 4: return tile_code(1, 1, 0);
+    default: return tile_code(1, 1, 1);
+  }
+}
+
+template <bool DtBf16, bool Wide>
+__global__ __launch_bounds__(kPrep32Threads)
+void chunk_prep32_kernel(const DecodeParams p, int num_sequences, float* ws,
+                         const int32_t* chunk_start, int records) {
+  using R = Rec32;
+  constexpr int kCs = R::kC;
+  constexpr int kTokens = kCs / (kPrep32Threads / 64);   // tokens normalised per wave
+  const int64_t unit = blockIdx.x;   // chunk * H + k-head
+  const int g = static_cast<int>(unit / p.num_k_heads);
+  if (g >= records) return;
+  const int key_head = static_cast<int>(unit - static_cast<int64_t>(g) * p.num_k_heads);
+  int seq = 0, t0 = 0, len = 0;
+  if (!find_chunk<kCs>(p.cu, chunk_start, num_sequences, g, seq, t0, len)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q_col = key_head * kDim;
+  const int k_col = (p.num_k_heads + key_head) * kDim;
+
+  constexpr int kHRow = kDim + 8;   // padded LDS row of the bf16 q / k (272 bytes)
+  constexpr int kARow = kCs + 4;    // padded LDS row of -A
+  constexpr int kTRow = 20;         // padded LDS row of a 16 x 16 block of T
+  __shared__ __attribute__((aligned(16))) uint16_t sQh[kCs][kHRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sKh[kCs][kHRow];
+  __shared__ __attribute__((aligned(16))) float sA[kCs][kARow];     // -A of the v-head
+  __shared__ __attribute__((aligned(16))) float sT[3][16][kTRow];   // T0, T1, T10
+  // a v-head's gates, double-buffered (v-head m in buffer m & 1): G_i, beta_i, exp(G_i),
+  // exp(G_n-1 - G_i), one entry per lane of the wave that forms them
+  __shared__ float sGates[2][4][64];
+  __shared__ float sRq[kCs];   // rq_i scale (zero past the end)
+  __shared__ float sRk[kCs];   // rk_i (zero past the end)
+
+  // The gate inputs of a v-head (wave 3, lane = token), fetched one v-head ahead, and the
+  // gates and in-chunk cumulative log decay from them: the 64-token prep's arithmetic.
+  uint16_t gate_a = 0, gate_b = 0;
+  float gate_a_log = 0.0f, gate_dt_bias = 0.0f;
+  auto fetch_gates = [&](int head) __attribute__((always_inline)) {
+    const int64_t tok = t0 + min(lane, len - 1);
+    gate_a = p.a[tok * p.a_row + head];
+    gate_b = p.b[tok * p.b_row + head];
+    gate_a_log = p.a_log[head];
+    gate_dt_bias = load_param(p.dt_bias, head, DtBf16);
+  };
+  auto gates = [&](int member) __attribute__((always_inline)) {
+    const int head = key_head * p.group + member;
+    const bool live = lane < len;
+    const float x = bf16_to_f32(gate_a) + gate_dt_bias;
+    const float gl = live ? -__expf(gate_a_log) * softplus(x) : 0.0f;
+    const float beta = live ? sigmoid(bf16_to_f32(gate_b)) : 0.0f;
+    if (member + 1 < p.group) fetch_gates(head + 1);
+    float G = gl;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float up = __shfl_up(G, d);
+      if (lane >= d) G += up;
+    }
+    const float glast = __shfl(G, len - 1);
+    float (*const gb)[64] = sGates[member & 1];
+    gb[0][lane] = G;
+    gb[1][lane] = beta;
+    gb[2][lane] = __expf(G);
+    gb[3][lane] = __expf(glast - G);
+    if (lane == 0)
+      ws[(static_cast<int64_t>(g) * p.num_v_heads + head) * R::kSize + R::kOffMisc] = __expf(glast);
+  };
+  if (wave == 3) fetch_gates(key_head * p.group);
+
+  // q and k of the chunk's tokens and their inverse norms (zero rows past its end), as the
+  // 64-token prep: wave w does tokens 8w .. 8w + 7
+  if constexpr (Wide) {
+    const int quarter = lane >> 4;
+    u32x4 qv[kTokens / 4], kv[kTokens / 4];
+#pragma unroll
+    for (int h = 0; h < kTokens / 4; ++h) {
+      const int64_t tok = t0 + min(wave * kTokens + 4 * h + quarter, len - 1);
+      const uint16_t* row = p.qkv + tok * p.qkv_row;
+      qv[h] = *reinterpret_cast<const u32x4*>(row + q_col + 8 * li);
+      kv[h] = *reinterpret_cast<const u32x4*>(row + k_col + 8 * li);
+    }
+#pragma unroll
+    for (int h = 0; h < kTokens / 4; ++h) {
+      const int i = wave * kTokens + 4 * h + quarter;
+      float pq[4], pk[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float q0 = __builtin_bit_cast(float, qv[h][m] << 16);
+        const float q1 = __builtin_bit_cast(float, qv[h][m] & 0xffff0000u);
+        const float k0 = __builtin_bit_cast(float, kv[h][m] << 16);
+        const float k1 = __builtin_bit_cast(float, kv[h][m] & 0xffff0000u);
+        pq[m] = fmaf(q1, q1, q0 * q0);
+        pk[m] = fmaf(k1, k1, k0 * k0);
+      }
+      float qq = (pq[0] + pq[1]) + (pq[2] + pq[3]);
+      float kk = (pk[0] + pk[1]) + (pk[2] + pk[3]);
+      qq += dpp<kDppQuadXor1>(qq);
+      kk += dpp<kDppQuadXor1>(kk);
+      qq += dpp<kDppQuadXor2>(qq);
+      kk += dpp<kDppQuadXor2>(kk);
+      qq += dpp<kDppRowHalfMirror>(qq);
+      kk += dpp<kDppRowHalfMirror>(kk);
+      qq += dpp<kDppRowMirror>(qq);
+      kk += dpp<kDppRowMirror>(kk);
+      const bool live = i < len;
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(&sQh[i][8 * li]) = live ? qv[h] : zero;
+      *reinterpret_cast<u32x4*>(&sKh[i][8 * li]) = live ? kv[h] : zero;
+      if (li == 0) {
+        sRq[i] = live ? fast_rsqrt(qq + 1e-6f) * p.scale : 0.0f;
+        sRk[i] = live ? fast_rsqrt(kk + 1e-6f) : 0.0f;
+      }
+    }
+  } else {
+    uint32_t qr[kTokens], kr[kTokens];
+#pragma unroll
+    for (int ii = 0; ii < kTokens; ++ii) {
+      const int64_t tok = t0 + min(wave * kTokens + ii, len - 1);
+      const uint16_t* row = p.qkv + tok * p.qkv_row;
+      qr[ii] = row[q_col + 2 * lane] | (static_cast<uint32_t>(row[q_col + 2 * lane + 1]) << 16);
+      kr[ii] = row[k_col + 2 * lane] | (static_cast<uint32_t>(row[k_col + 2 * lane + 1]) << 16);
+    }
+#pragma unroll
+    for (int ii = 0; ii < kTokens; ++ii) {
+      const int i = wave * kTokens + ii;
+      const float q0 = __builtin_bit_cast(float, qr[ii] << 16);
+      const float q1 = __builtin_bit_cast(float, qr[ii] & 0xffff0000u);
+      const float k0 = __builtin_bit_cast(float, kr[ii] << 16);
+      const float k1 = __builtin_bit_cast(float, kr[ii] & 0xffff0000u);
+      const float qq = wave_sum(fmaf(q1, q1, q0 * q0));
+      const float kk = wave_sum(fmaf(k1, k1, k0 * k0));
+      const bool live = i < len;
+      *reinterpret_cast<uint32_t*>(&sQh[i][2 * lane]) = live ? qr[ii] : 0u;
+      *reinterpret_cast<uint32_t*>(&sKh[i][2 * lane]) = live ? kr[ii] : 0u;
+      if (lane == 0) {
+        sRq[i] = live ? fast_rsqrt(qq + 1e-6f) * p.scale : 0.0f;
+        sRk[i] = live ? fast_rsqrt(kk + 1e-6f) : 0.0f;
+      }
+    }
+  }
+  if (wave == 3) gates(0);
+  __syncthreads();
+
+  // Qr, Kq and Kr (the bf16 inputs in the scan's load order, item = one 16-byte piece) to
+  // the record of the group's first v-head
+  {
+    float* rec0 = ws + (static_cast<int64_t>(g) * p.num_v_heads + key_head * p.group) * R::kSize;
+    u32x4* qdst = reinterpret_cast<u32x4*>(rec0 + R::kOffQr);
+    u32x4* kqdst = reinterpret_cast<u32x4*>(rec0 + R::kOffKq);
+    u32x4* krdst = reinterpret_cast<u32x4*>(rec0 + R::kOffKr);
+#pragma unroll
+    for (int it = 0; it < kCs * kDim / 8 / kPrep32Threads; ++it) {
+      const int item = it * kPrep32Threads + tid;
+      const int l = item & 63;
+      const int i = 16 * (item >> 8) + (l & 15);
+      const int c0 = 32 * (l >> 4) + 8 * ((item >> 6) & 3);
+      qdst[item] = *reinterpret_cast<const u32x4*>(&sQh[i][c0]);
+      kqdst[item] = *reinterpret_cast<const u32x4*>(&sKh[i][c0]);
+      const int k = 16 * (item >> 6) + (l & 15);
+      const int j = 8 * (l >> 4);
+      krdst[item] = u32x4{sKh[j][k] | (static_cast<uint32_t>(sKh[j + 1][k]) << 16),
+                          sKh[j + 2][k] | (static_cast<uint32_t>(sKh[j + 3][k]) << 16),
+                          sKh[j + 4][k] | (static_cast<uint32_t>(sKh[j + 5][k]) << 16),
+                          sKh[j + 6][k] | (static_cast<uint32_t>(sKh[j + 7][k]) << 16)};
+    }
+  }
+
+  // The raw tiles, q_i . k_m and k_i . k_m of the bf16 inputs (exact products, fp32 sums),
+  // once for all the group's v-heads: A tiles as K K^T (row tile mt, column tile nt), P tiles
+  // transposed, as K Q^T, so that a lane's four results are four consecutive columns of one
+  // row of P
+  const int tiles = wave < 2 ? 2 : 1;
+  f32x4 prod[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (t >= tiles) break;
+    const uint32_t code = prep32_tile(wave + 4 * t);
+    const int mt = (code >> 2) & 3;
+    const int nt = code & 3;
+    const bool is_p = (code & 16u) != 0;
+    const uint16_t* arow = &sKh[16 * (is_p ? nt : mt) + li][8 * lg];
+    const uint16_t* brow = is_p ? &sQh[16 * mt + li][8 * lg] : &sKh[16 * nt + li][8 * lg];
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + 32 * s4);
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(brow + 32 * s4);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+    }
+    prod[t] = acc;
+  }
+
+  for (int member = 0; member < p.group; ++member) {
+    const int head = key_head * p.group + member;
+    const bool next = member + 1 < p.group;
+    float* rec = ws + (static_cast<int64_t>(g) * p.num_v_heads + head) * R::kSize;
+    const float* const sG = sGates[member & 1][0];
+    const float* const sBeta = sGates[member & 1][1];
+    const float* const sEg = sGates[member & 1][2];
+    const float* const sEk = sGates[member & 1][3];
+
+    // the per-token scales: sq = rq scale exp(G), beta, ck = rk exp(G_n-1 - G),
+    // ws = beta exp(G) rk (the 64-token prep's W scale)
+    if (tid < kCs) {
+      rec[R::kOffMisc + kMiscSq + tid] = sRq[tid] * sEg[tid];
+      rec[R::kOffMisc + kMiscBeta + tid] = sBeta[tid];
+    } else if (tid < 2 * kCs) {
+      const int j = tid - kCs;
+      rec[R::kOffMisc + kMiscCk + j] = sRk[j] * sEk[j];
+      rec[R::kOffMisc + kMiscWs + j] = sBeta[j] * sEg[j] * sRk[j];
+    }
+
+    // scale the tiles: A (negated) to LDS, P to the record (the products are of the raw
+    // inputs: q^_i . k^_m = (rq_i scale rk_m) (q_i . k_m)); P's tile above the diagonal
+    // gets zeros
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t >= tiles) break;
+      const uint32_t code = prep32_tile(wave + 4 * t);
+      const int mt = (code >> 2) & 3;
+      const int nt = code & 3;
+      if (code & 16u) {
+        const int i = 16 * mt + li;
+        const float gi = sG[i];
+        const float rqi = sRq[i];
+        f32x4 piece;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * nt + 4 * lg + r;
+          const float gam = __expf(gi - sG[m]);
+          piece[r] = (m <= i && i < len) ? gam * ((rqi * sRk[m]) * prod[t][r]) : 0.0f;
+        }
+        *reinterpret_cast<f32x4*>(rec + R::kOffP + piece32(mt, nt, lg, li)) = piece;
+      } else {
+        const int m = 16 * nt + li;
+        const float gm = sG[m];
+        const float rkm = sRk[m];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * mt + 4 * lg + r;
+          const float gam = __expf(sG[i] - gm);
+          sA[i][m] = m < i ? -(sBeta[i] * gam * ((sRk[i] * rkm) * prod[t][r])) : 0.0f;
+        }
+      }
+    }
+    if (wave == 2)
+      *reinterpret_cast<f32x4*>(rec + R::kOffP + piece32(0, 1, lg, li)) =
+          f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();   // -A complete
+    if (wave == 3 && next) gates(member + 1);
+    // inverses of the unit lower-triangular diagonal blocks (I + A_bb), column li per lane
+    // (block w by wave w < 2), row by row: col[i] = delta(i, li) + sum over m < i of
+    // (-A)[i][m] col[m], the terms in order of m
+    if (wave < 2 && lane < 16) {
+      float col[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float acc = i == li ? 1.0f : 0.0f;
+#pragma unroll
+        for (int m = 0; m < i; ++m) acc = fmaf(sA[16 * wave + i][16 * wave + m], col[m], acc);
+        col[i] = acc;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sT[wave][i][li] = col[i];
+    }
+    __syncthreads();   // T0, T1 complete
+    // T10 = T1 ((-A10) T0) on the fp32 matrix cores, summation index k = 4 lg + step, so the
+    // first product's d[r] is the second's b operand of step r
+    if (wave == 0) {
+      const f32x4 a10 = *reinterpret_cast<const f32x4*>(&sA[16 + li][4 * lg]);
+      f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) z = mfma(a10[st], sT[0][4 * lg + st][li], z);
+      const f32x4 t1 = *reinterpret_cast<const f32x4*>(&sT[1][li][4 * lg]);
+      f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) d = mfma(t1[st], z[st], d);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sT[2][4 * lg + r][li] = d[r];
+    }
+    __syncthreads();   // T10 complete
+    // T to the record, one piece per thread: piece (w, q) = tid / 64 holds
+    // T[16 w + li][8 lg + 4 q ..]: T0 and zeros for w = 0, T10 and T1 for w = 1
+    {
+      const int w = tid >> 7;
+      const int c = 8 * lg + 4 * ((tid >> 6) & 1);
+      f32x4 v;
+      if (w == 0)
+        v = c < 16 ? *reinterpret_cast<const f32x4*>(&sT[0][li][c]) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      else
+        v = c < 16 ? *reinterpret_cast<const f32x4*>(&sT[2][li][c])
+                   : *reinterpret_cast<const f32x4*>(&sT[1][li][c - 16]);
+      *reinterpret_cast<f32x4*>(rec + R::kOffT + tid * 4) = v;
+    }
+    // the next v-head writes -A after its first barrier (every read of -A and T above is
+    // behind one of this v-head's) and its gates went to the other buffer
   }
 }
 
@@ -1154,15 +1454,20 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 
 // ---- phase 2, 32-token chunks: per (sequence, v-head, block of 32 state rows) ----------
 // Eight waves, two per SIMD, each on one (token tile a, row tile h) = (w & 1, w >> 1) of the
-// chunk: state wave w (0..3) forms V_new of that tile, then updates k tiles 2w and 2w + 1 of
-// both row tiles; output wave 4 + w forms the raw outputs of that tile.  Per chunk and SIMD
-// that is 104 products of 16 x 16 x 4 for 32 tokens, against 224 for 64 tokens in
-// chunk_scan_kernel<2> (P V_new grows with the square of the chunk).
+// chunk.  State wave w (0..3): Y = K_a S_h^T from the bf16 keys, X = diag(beta) V -
+// diag(ws) Y with V read from qkv; after a barrier V_new = T_a X_h (all 32 tokens of X);
+// after another, the update of k tiles 2w and 2w + 1 of both row tiles.  Output wave 4 + w:
+// the raw outputs of its tile.  Per chunk and SIMD 112 products of 16 x 16 x 4 for 32
+// tokens, against 224 for 64 tokens in chunk_scan_kernel<2> (P V_new grows with the square
+// of the chunk).
 struct Scan32State {
-  f32x4 w[8];   // W [16 a + li][32 lg + 4 q + e]
-  u32x4 kr[2];  // Kr^T [16 (2w + t) + li][8 lg + e] (bf16)
-  f32x4 u;      // U [16 a + 4 lg + r][row0 + 16 h + li]
+  u32x4 kq[4];  // Kq [16 a + li][32 lg + 8 qq + e] (bf16)
+  f32x4 beta;   // beta of tokens 16 a + 4 lg + r
+  f32x4 ws;     // ws of tokens 16 a + 4 lg + r
+  uint16_t v[4];  // V [16 a + 4 lg + r][row0 + 16 h + li] (bf16)
+  f32x4 t[2];   // T [16 a + li][8 lg + 4 q + e]
   f32x4 ck;     // ck of tokens 16 a + 4 lg + r
+  u32x4 kr[2];  // Kr^T [16 (2w + t) + li][8 lg + e] (bf16)
   float gamma;  // exp(G_n-1)
 };
 
@@ -1172,27 +1477,31 @@ struct Scan32Output {
   f32x4 p[2];   // P [16 a + li][8 lg + 4 q + e]
 };
 
-// The operand loads in pieces, as in chunk_scan_kernel: a state wave's W, U and ck pieces
-// (q < 2: W step groups 2q, 2q + 1, 2q + 4, 2q + 5, with U and ck at q = 0) are refilled
-// for the next chunk during the update, its Kr pieces and gamma (piece 2) during this
-// chunk's V_new products; an output wave's P (piece 2) during this chunk's q S^T products,
-// its Qr and sq (q < 2: step groups 2q, 2q + 1, with sq at q = 0) during P V_new.
-__device__ __forceinline__ void load_state32(Scan32State& o, __amdgpu_buffer_rsrc_t rs, int own,
-                                             int w, int a, int utile, uint32_t lane16,
-                                             uint32_t lg16, int piece) {
-  using R = Rec<2>;
-  if (piece < 2) {
-    const int wbase = own + static_cast<int>(R::kOffW * 4) + a * 8 * 1024;
+// The operand loads in pieces, as in chunk_scan_kernel.  State wave: piece 0 (Kq, beta, ws
+// and v: the first products) and piece 1 (T and ck: V_new) of the next chunk during the
+// update, piece 2 (Kr and gamma: the update) during this chunk's first products.  Output
+// wave: piece 2 (P) of this chunk during its q S^T products, pieces 0 and 1 (Qr, sq) of the
+// next during P V_new.  `vs`: a resource over the chunk's rows of qkv, `voff` the lane's
+// byte offset of V[16 a + 4 lg][row0 + 16 h + li] in it.
+__device__ __forceinline__ void load_state32(Scan32State& o, __amdgpu_buffer_rsrc_t rs,
+                                             __amdgpu_buffer_rsrc_t vs, uint32_t voff,
+                                             uint32_t vrow, int own, int w, int a,
+                                             uint32_t lane16, uint32_t lg16, int piece) {
+  using R = Rec32;
+  if (piece == 0) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int q = 2 * piece + e;
-      o.w[q] = load16(rs, lane16, wbase + q * 1024);
-      o.w[q + 4] = load16(rs, lane16, wbase + (q + 4) * 1024);
-    }
-    if (piece == 0) {
-      o.u = load16(rs, lane16, own + static_cast<int>(R::kOffU * 4) + (utile * 2 + a) * 1024);
-      o.ck = load16(rs, lg16, own + static_cast<int>((R::kOffMisc + kMiscCk) * 4) + a * 64);
-    }
+    for (int qq = 0; qq < 4; ++qq)
+      o.kq[qq] = load16u(rs, lane16, static_cast<int>(R::kOffKq * 4) + (a * 4 + qq) * 1024);
+    o.beta = load16(rs, lg16, own + static_cast<int>((R::kOffMisc + kMiscBeta) * 4) + a * 64);
+    o.ws = load16(rs, lg16, own + static_cast<int>((R::kOffMisc + kMiscWs) * 4) + a * 64);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      o.v[r] = __builtin_amdgcn_raw_buffer_load_b16(vs, static_cast<int>(voff + r * vrow), 0, 0);
+  } else if (piece == 1) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      o.t[q] = load16(rs, lane16, own + static_cast<int>(R::kOffT * 4) + (a * 2 + q) * 1024);
+    o.ck = load16(rs, lg16, own + static_cast<int>((R::kOffMisc + kMiscCk) * 4) + a * 64);
   } else {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -1203,7 +1512,7 @@ __device__ __forceinline__ void load_state32(Scan32State& o, __amdgpu_buffer_rsr
 
 __device__ __forceinline__ void load_output32(Scan32Output& o, __amdgpu_buffer_rsrc_t rs, int own,
                                               int a, uint32_t lane16, uint32_t lg16, int piece) {
-  using R = Rec<2>;
+  using R = Rec32;
   if (piece < 2) {
 #pragma unroll
     for (int e = 0; e < 2; ++e)
@@ -1221,7 +1530,7 @@ __device__ __forceinline__ void load_output32(Scan32Output& o, __amdgpu_buffer_r
 __global__ __launch_bounds__(kScanThreads)
 void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
                          const int32_t* chunk_start, int records) {
-  using R = Rec<2>;
+  using R = Rec32;
   constexpr int kCs = R::kC;                 // 32 tokens per chunk
   constexpr int kRows = 32;                  // state rows per workgroup
   constexpr int kBlocks = kDim / kRows;
@@ -1256,6 +1565,7 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
   __shared__ __attribute__((aligned(16))) float sS[kRows][kSRow];   // S rows [row][k]
   __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];  // V_new^T [row][token]
   __shared__ __attribute__((aligned(16))) float sVk[kRows][kVRow];  // ditto, token j times ck_j
+  __shared__ __attribute__((aligned(16))) float sX[kRows][kVRow];   // X^T [row][token]
 
   const int member = head % p.group;
   const int own = member * static_cast<int>(R::kSize * 4);
@@ -1272,6 +1582,17 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
   auto s_fragment = [&](int q) {   // S^T for k = 32 lg + 4 q + e, rows 16 h + li
     return *reinterpret_cast<const f32x4*>(&sS[16 * h + li][32 * lg + 4 * q]);
   };
+  // chunk c's rows of qkv (0 bytes past the last chunk, or a sequence's rows past its end:
+  // their v reads as zeros), and the lane's offset of v[16 a + 4 lg][row0 + 16 h + li] in it
+  const int v_col = (2 * p.num_k_heads + head) * kDim + row0 + 16 * h + li;
+  auto v_rows = [&](int c) {
+    const int t0 = bos + min(c, max(chunks - 1, 0)) * kCs;
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.qkv + static_cast<int64_t>(t0) * p.qkv_row), 0,
+        c < chunks ? min(kCs, eos - t0) * static_cast<int>(p.qkv_row) * 2 : 0, 0x00020000);
+  };
+  const uint32_t vrow = static_cast<uint32_t>(p.qkv_row) * 2;
+  const uint32_t voff = (16 * a + 4 * lg) * vrow + static_cast<uint32_t>(v_col) * 2;
 
   if (wave < 4) {
     // The wave's pieces of the state, S[row0 + 16 hh + li][16 (2w + t) + 4 lg + r], live in
@@ -1281,15 +1602,15 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
     auto own_piece = [&](int t, int hh) -> f32x4& {
       return *reinterpret_cast<f32x4*>(&sS[16 * hh + li][16 * (2 * w + t) + 4 * lg]);
     };
-    // the first chunk's W, U and ck go out before the state's loads, so that their latencies
-    // overlap (the state is waited for first, to reach sS)
-    const int utile = row_block * 2 + h;
+    // the first chunk's pieces 0 and 1 go out before the state's loads, so that their
+    // latencies overlap (the state is waited for first, to reach sS)
     Scan32State op;
     if (chunks > 0) {
       const __amdgpu_buffer_rsrc_t r = record(0);
+      const __amdgpu_buffer_rsrc_t vr = v_rows(0);
 #pragma unroll
       for (int piece = 0; piece < 2; ++piece) {
-        load_state32(op, r, own, w, a, utile, lane16, lg16, piece);
+        load_state32(op, r, vr, voff, vrow, own, w, a, lane16, lg16, piece);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -1309,25 +1630,51 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
     for (int c = 0; c < chunks; ++c) {
       const __amdgpu_buffer_rsrc_t cur = record(c);
       const __amdgpu_buffer_rsrc_t next = record(c + 1);
+      const __amdgpu_buffer_rsrc_t vnext = v_rows(c + 1);
       __syncthreads();  // sS holds the state at the chunk's start
+      // Y = K_a S_h^T, two accumulation chains (k < 64, k >= 64 of each lane group)
+      f32x4 y0 = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 y1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (q == 0) load_state32(op, cur, vnext, voff, vrow, own, w, a, lane16, lg16, 2);
+        const f32x4 b0 = s_fragment(q);
+        const f32x4 b1 = s_fragment(q + 4);
+        const f32x4 a0 = bf16x4(op.kq[q >> 1], q & 1);
+        const f32x4 a1 = bf16x4(op.kq[2 + (q >> 1)], q & 1);
+        y0 = mfma(a0.x, b0.x, y0);
+        y1 = mfma(a1.x, b1.x, y1);
+        y0 = mfma(a0.y, b0.y, y0);
+        y1 = mfma(a1.y, b1.y, y1);
+        y0 = mfma(a0.z, b0.z, y0);
+        y1 = mfma(a1.z, b1.z, y1);
+        y0 = mfma(a0.w, b0.w, y0);
+        y1 = mfma(a1.w, b1.w, y1);
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
+      }
+      // X = diag(beta) V - diag(ws) Y for tokens 16 a + 4 lg + r, row 16 h + li (beta and ws
+      // are zero past the chunk's end, and so is v)
+      {
+        const f32x4 y = y0 + y1;
+        f32x4 x;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = op.beta[r] * bf16_to_f32(op.v[r]) - op.ws[r] * y[r];
+        *reinterpret_cast<f32x4*>(&sX[16 * h + li][16 * a + 4 * lg]) = x;
+      }
+      __syncthreads();  // X complete
+      // V_new = T_a X_h over the chunk's 32 tokens j = 8 lg + 4 q + e
       f32x4 vn0 = {0.0f, 0.0f, 0.0f, 0.0f};
       f32x4 vn1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q == 0) load_state32(op, cur, own, w, a, utile, lane16, lg16, 2);
-        const f32x4 b0 = s_fragment(q);
-        const f32x4 b1 = s_fragment(q + 4);
-        vn0 = mfma(op.w[q].x, b0.x, vn0);
-        vn1 = mfma(op.w[q + 4].x, b1.x, vn1);
-        vn0 = mfma(op.w[q].y, b0.y, vn0);
-        vn1 = mfma(op.w[q + 4].y, b1.y, vn1);
-        vn0 = mfma(op.w[q].z, b0.z, vn0);
-        vn1 = mfma(op.w[q + 4].z, b1.z, vn1);
-        vn0 = mfma(op.w[q].w, b0.w, vn0);
-        vn1 = mfma(op.w[q + 4].w, b1.w, vn1);
-        __builtin_amdgcn_sched_barrier(kLoadGroup);
+      for (int q = 0; q < 2; ++q) {
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&sX[16 * h + li][8 * lg + 4 * q]);
+        f32x4& vn = q == 0 ? vn0 : vn1;
+        vn = mfma(op.t[q].x, b.x, vn);
+        vn = mfma(op.t[q].y, b.y, vn);
+        vn = mfma(op.t[q].z, b.z, vn);
+        vn = mfma(op.t[q].w, b.w, vn);
       }
-      const f32x4 vn = op.u - (vn0 + vn1);
+      const f32x4 vn = vn0 + vn1;
       *reinterpret_cast<f32x4*>(&sVn[16 * h + li][16 * a + 4 * lg]) = vn;
       *reinterpret_cast<f32x4*>(&sVk[16 * h + li][16 * a + 4 * lg]) = vn * op.ck;
       __syncthreads();  // V_new complete; every read of sS for this chunk done
@@ -1338,7 +1685,7 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
         for (int hh = 0; hh < 2; ++hh) st[t][hh] = own_piece(t, hh) * op.gamma;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        load_state32(op, next, own, w, a, utile, lane16, lg16, q);
+        load_state32(op, next, vnext, voff, vrow, own, w, a, lane16, lg16, q);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           // V_new k ck for tokens j = 8 lg + 4 q + e, rows 16 hh + li
@@ -1406,6 +1753,7 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
       // rows of q S^T scaled to (q^ exp(G)) S^T; P V_new accumulates on top
       o0 = (o0 + o1) * op.sq;
       o1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      __syncthreads();  // X complete
       __syncthreads();  // V_new complete
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
@@ -1442,7 +1790,7 @@ int64_t max_chunks(int64_t num_tokens, int64_t num_sequences) {
 // Workspace: the records, then chunk_start (num_sequences + 1 int32, rounded up to 256 B).
 // Sized for 64-token chunks, which covers 32-token ones: with S >= 1 sequences,
 // (T / 32 + S) R32 <= (2 (T / 64) + 1 + S) R32 <= (T / 64 + S) R64 as 2 R32 <= R64.
-static_assert(2 * Rec<2>::kSize <= Rec<4>::kSize, "32-token records fit the workspace");
+static_assert(2 * Rec32::kSize <= kRecord, "32-token records fit the workspace");
 int64_t records_bytes(int64_t num_tokens, int64_t num_sequences, int64_t num_v_heads) {
   return max_chunks<kC>(num_tokens, num_sequences) * num_v_heads * kRecord * 4;
 }
@@ -1450,7 +1798,7 @@ int64_t records_bytes(int64_t num_tokens, int64_t num_sequences, int64_t num_v_h
 template <int TT>
 int launch_chunks(const DecodeParams& p, int num_sequences, int64_t num_tokens, bool dt_bf16,
                   float* ws, int32_t* chunk_start, hipStream_t stream) {
-  constexpr int kCt = Rec<TT>::kC;
+  constexpr int kCt = TT == 2 ? Rec32::kC : kC;
   const int64_t chunks = max_chunks<kCt>(num_tokens, num_sequences);
   if (chunks > 0x7fffffff || p.num_v_heads > 65535)
     return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large for the chunked form");
@@ -1460,22 +1808,29 @@ int launch_chunks(const DecodeParams& p, int num_sequences, int64_t num_tokens, 
   const dim3 per_chunk(static_cast<uint32_t>(prep_groups));
   hipLaunchKernelGGL(chunk_index_kernel<kCt>, dim3(1), dim3(kThreads), 0, stream, p.cu,
                      num_sequences, chunk_start);
-  // 16-byte pieces of q, k and v when every row starts at a 16-byte boundary
+  // 16-byte pieces of q and k (and v) when every row starts at a 16-byte boundary
   const bool wide = (reinterpret_cast<uintptr_t>(p.qkv) & 15) == 0 && (p.qkv_row & 7) == 0;
-#define LD_PREP_LAUNCH(D, W)                                                                   \
-  hipLaunchKernelGGL((chunk_prep_kernel<TT, D, W>), per_chunk, dim3(kPrepThreads), 0, stream, \
-                     p, num_sequences, ws, chunk_start, static_cast<int>(chunks))
-  if (dt_bf16) {
-    if (wide)
-      LD_PREP_LAUNCH(true, true);
-    else
-      LD_PREP_LAUNCH(true, false);
-  } else {
-    if (wide)
-      LD_PREP_LAUNCH(false, true);
-    else
-      LD_PREP_LAUNCH(false, false);
+#define LD_PREP_LAUNCH(K, D, W, N)                                                             \
+  hipLaunchKernelGGL((K<D, W>), per_chunk, dim3(N), 0, stream, p, num_sequences, ws,          \
+                     chunk_start, static_cast<int>(chunks))
+#define LD_PREP_LAUNCHES(K, N)                                                                 \
+  if (dt_bf16) {                                                                               \
+    if (wide)                                                                                  \
+      LD_PREP_LAUNCH(K, true, true, N);                                                        \
+    else                                                                                       \
+      LD_PREP_LAUNCH(K, true, false, N);                                                       \
+  } else {                                                                                     \
+    if (wide)                                                                                  \
+      LD_PREP_LAUNCH(K, false, true, N);                                                       \
+    else                                                                                       \
+      LD_PREP_LAUNCH(K, false, false, N);                                                      \
   }
+  if constexpr (TT == 2) {
+    LD_PREP_LAUNCHES(chunk_prep32_kernel, kPrep32Threads)
+  } else {
+    LD_PREP_LAUNCHES(chunk_prep_kernel, kPrepThreads)
+  }
+#undef LD_PREP_LAUNCHES
 #undef LD_PREP_LAUNCH
   const int64_t pairs = static_cast<int64_t>(num_sequences) * p.num_v_heads;
   if constexpr (TT == 2) {
