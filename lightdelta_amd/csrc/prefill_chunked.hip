@@ -1460,6 +1460,61 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 // the raw outputs of its tile.  Per chunk and SIMD 112 products of 16 x 16 x 4 for 32
 // tokens, against 224 for 64 tokens in chunk_scan_kernel<2> (P V_new grows with the square
 // of the chunk).
+// x = s1 + s2 + s3 exactly, in bf16 (each part the round-to-nearest-even of what the
+// earlier ones leave, and every remainder exact in fp32: 8 + 8 + 8 bits of x's 24), so a
+// product of an exact bf16 operand with x runs on the bf16 matrix cores as three products
+// with exact terms and fp32 sums.  p[i] holds part i + 1 of four values.
+struct Split4 {
+  uint2 p[3];
+};
+
+__device__ __forceinline__ Split4 split4(f32x4 x) {
+  Split4 sp;
+  uint16_t part[3][4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float r = x[e];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      part[i][e] = to_bf16(r);
+      r -= bf16_to_f32(part[i][e]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    sp.p[i] = uint2{part[i][0] | (static_cast<uint32_t>(part[i][1]) << 16),
+                    part[i][2] | (static_cast<uint32_t>(part[i][3]) << 16)};
+  return sp;
+}
+
+// The four values back: (s1 + s2) + s3, exact (each partial sum is x less a tail it lacks).
+__device__ __forceinline__ f32x4 join4(const Split4& sp) {
+  f32x4 x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t shift = (e & 1) * 16;
+    const uint32_t w0 = e < 2 ? sp.p[0].x : sp.p[0].y;
+    const uint32_t w1 = e < 2 ? sp.p[1].x : sp.p[1].y;
+    const uint32_t w2 = e < 2 ? sp.p[2].x : sp.p[2].y;
+    x[e] = (bf16_to_f32(static_cast<uint16_t>(w0 >> shift)) +
+            bf16_to_f32(static_cast<uint16_t>(w1 >> shift))) +
+           bf16_to_f32(static_cast<uint16_t>(w2 >> shift));
+  }
+  return x;
+}
+
+// scan32's LDS for S and V_new ck: three bf16 planes each (Split) or fp32
+template <bool Split>
+struct Scan32Lds {
+  typedef uint16_t S[3][32][kDim + 8];   // rows of 272 bytes
+  typedef uint16_t Vk[3][32][32 + 8];
+};
+template <>
+struct Scan32Lds<false> {
+  typedef float S[32][kDim + 4];
+  typedef float Vk[32][32 + 4];
+};
+
 struct Scan32State {
   u32x4 kq[4];  // Kq [16 a + li][32 lg + 8 qq + e] (bf16)
   f32x4 beta;   // beta of tokens 16 a + 4 lg + r
@@ -1527,7 +1582,13 @@ __device__ __forceinline__ void load_output32(Scan32Output& o, __amdgpu_buffer_r
   }
 }
 
-__global__ __launch_bounds__(kScanThreads)
+// Split: the products with S and with V_new ck on the bf16 matrix cores, each as three
+// products against split3's parts (fp32-exact operands, fp32 sums, 80 VGPRs); else all on
+// the fp32 matrix cores.  The split halves the scan's matrix time and pays for it in
+// splitting VALU work and LDS traffic, which prompts of one chunk (latency-bound) do not
+// recover.
+template <bool Split>
+__global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(6)))
 void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
                          const int32_t* chunk_start, int records) {
   using R = Rec32;
@@ -1560,12 +1621,14 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
   const int gbase = chunk_start[seq];
   const int chunks = min((eos - bos + kCs - 1) / kCs, max(records - gbase, 0));
 
-  constexpr int kSRow = kDim + 4;
-  constexpr int kVRow = kCs + 4;
-  __shared__ __attribute__((aligned(16))) float sS[kRows][kSRow];   // S rows [row][k]
-  __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];  // V_new^T [row][token]
-  __shared__ __attribute__((aligned(16))) float sVk[kRows][kVRow];  // ditto, token j times ck_j
-  __shared__ __attribute__((aligned(16))) float sX[kRows][kVRow];   // X^T [row][token]
+  constexpr int kVRow = kCs + 4;    // fp32 row of V_new or X
+  // S [row][k] and V_new with its rows scaled by ck [row][token]: fp32, or (Split) three
+  // bf16 planes each (split4: their sum is the fp32 value exactly); V_new and X in fp32 for
+  // the fp32 products
+  __shared__ __attribute__((aligned(16))) typename Scan32Lds<Split>::S sS;
+  __shared__ __attribute__((aligned(16))) typename Scan32Lds<Split>::Vk sVk;
+  __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];   // V_new^T [row][token]
+  __shared__ __attribute__((aligned(16))) float sX[kRows][kVRow];    // X^T [row][token]
 
   const int member = head % p.group;
   const int own = member * static_cast<int>(R::kSize * 4);
@@ -1579,8 +1642,42 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
                  R::kSize,
         c < chunks ? group_bytes : 0);
   };
-  auto s_fragment = [&](int q) {   // S^T for k = 32 lg + 4 q + e, rows 16 h + li
-    return *reinterpret_cast<const f32x4*>(&sS[16 * h + li][32 * lg + 4 * q]);
+  // X_a S_h^T for bf16 rows X, the lane's values k = 32 lg + 8 qq .. + 7 in x[qq], row
+  // 16 h + li of S.  Split: instruction qq of a bf16 product takes those 8 values against
+  // each of S's planes, smallest first.  fp32: two chains of 16 products (k < 64, k >= 64 of
+  // each lane group), 4 values each; `load(q)` issues operand loads before step q's group.
+  auto times_st = [&](const u32x4 (&x)[4], auto&& load) __attribute__((always_inline)) {
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (Split) {
+      load(0);
+      __builtin_amdgcn_sched_barrier(kLoadGroup);
+#pragma unroll
+      for (int pl = 2; pl >= 0; --pl)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, x[qq]),
+              *reinterpret_cast<const bf16x8*>(&sS[pl][16 * h + li][32 * lg + 8 * qq]), acc, 0,
+              0, 0);
+    } else {
+      f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        load(q);
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(&sS[16 * h + li][32 * lg + 4 * q]);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(&sS[16 * h + li][32 * lg + 16 + 4 * q]);
+        const f32x4 a0 = bf16x4(x[q >> 1], q & 1);
+        const f32x4 a1 = bf16x4(x[2 + (q >> 1)], q & 1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc = mfma(a0[e], b0[e], acc);
+          acc1 = mfma(a1[e], b1[e], acc1);
+        }
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
+      }
+      acc += acc1;
+    }
+    return acc;
   };
   // chunk c's rows of qkv (0 bytes past the last chunk, or a sequence's rows past its end:
   // their v reads as zeros), and the lane's offset of v[16 a + 4 lg][row0 + 16 h + li] in it
@@ -1596,11 +1693,30 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
 
   if (wave < 4) {
     // The wave's pieces of the state, S[row0 + 16 hh + li][16 (2w + t) + 4 lg + r], live in
-    // sS between chunks (re-read for the update, not held in registers through V_new).
-    float* tile_base = p.state + static_cast<int64_t>(slot) * p.state_slot +
-                       static_cast<int64_t>(head) * kDim * kDim + (row0 + li) * kDim;
-    auto own_piece = [&](int t, int hh) -> f32x4& {
-      return *reinterpret_cast<f32x4*>(&sS[16 * hh + li][16 * (2 * w + t) + 4 * lg]);
+    // sS between chunks (Split: in its planes, split on the way in and summed on the way out,
+    // exactly).
+    auto put_own = [&](int t, int hh, f32x4 v) __attribute__((always_inline)) {
+      const int k = 16 * (2 * w + t) + 4 * lg;
+      if constexpr (Split) {
+        const Split4 sp = split4(v);
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint2*>(&sS[pl][16 * hh + li][k]) = sp.p[pl];
+      } else {
+        *reinterpret_cast<f32x4*>(&sS[16 * hh + li][k]) = v;
+      }
+    };
+    auto get_own = [&](int t, int hh) __attribute__((always_inline)) {
+      const int k = 16 * (2 * w + t) + 4 * lg;
+      if constexpr (Split) {
+        Split4 sp;
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          sp.p[pl] = *reinterpret_cast<const uint2*>(&sS[pl][16 * hh + li][k]);
+        return join4(sp);
+      } else {
+        return *reinterpret_cast<const f32x4*>(&sS[16 * hh + li][k]);
+      }
     };
     // the first chunk's pieces 0 and 1 go out before the state's loads, so that their
     // latencies overlap (the state is waited for first, to reach sS)
@@ -1625,37 +1741,20 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) own_piece(t, hh) = st[t][hh];
+        for (int t = 0; t < 2; ++t) put_own(t, hh, st[t][hh]);
     }
     for (int c = 0; c < chunks; ++c) {
       const __amdgpu_buffer_rsrc_t cur = record(c);
       const __amdgpu_buffer_rsrc_t next = record(c + 1);
       const __amdgpu_buffer_rsrc_t vnext = v_rows(c + 1);
       __syncthreads();  // sS holds the state at the chunk's start
-      // Y = K_a S_h^T, two accumulation chains (k < 64, k >= 64 of each lane group)
-      f32x4 y0 = {0.0f, 0.0f, 0.0f, 0.0f};
-      f32x4 y1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      // Y = K_a S_h^T (this chunk's Kr and gamma loaded beside it)
+      const f32x4 y = times_st(op.kq, [&](int q) {
         if (q == 0) load_state32(op, cur, vnext, voff, vrow, own, w, a, lane16, lg16, 2);
-        const f32x4 b0 = s_fragment(q);
-        const f32x4 b1 = s_fragment(q + 4);
-        const f32x4 a0 = bf16x4(op.kq[q >> 1], q & 1);
-        const f32x4 a1 = bf16x4(op.kq[2 + (q >> 1)], q & 1);
-        y0 = mfma(a0.x, b0.x, y0);
-        y1 = mfma(a1.x, b1.x, y1);
-        y0 = mfma(a0.y, b0.y, y0);
-        y1 = mfma(a1.y, b1.y, y1);
-        y0 = mfma(a0.z, b0.z, y0);
-        y1 = mfma(a1.z, b1.z, y1);
-        y0 = mfma(a0.w, b0.w, y0);
-        y1 = mfma(a1.w, b1.w, y1);
-        __builtin_amdgcn_sched_barrier(kLoadGroup);
-      }
+      });
       // X = diag(beta) V - diag(ws) Y for tokens 16 a + 4 lg + r, row 16 h + li (beta and ws
       // are zero past the chunk's end, and so is v)
       {
-        const f32x4 y = y0 + y1;
         f32x4 x;
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = op.beta[r] * bf16_to_f32(op.v[r]) - op.ws[r] * y[r];
@@ -1676,44 +1775,83 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
       const f32x4 vn = vn0 + vn1;
       *reinterpret_cast<f32x4*>(&sVn[16 * h + li][16 * a + 4 * lg]) = vn;
-      *reinterpret_cast<f32x4*>(&sVk[16 * h + li][16 * a + 4 * lg]) = vn * op.ck;
+      if constexpr (Split) {
+        const Split4 sp = split4(vn * op.ck);
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint2*>(&sVk[pl][16 * h + li][16 * a + 4 * lg]) = sp.p[pl];
+      } else {
+        *reinterpret_cast<f32x4*>(&sVk[16 * h + li][16 * a + 4 * lg]) = vn * op.ck;
+      }
       __syncthreads();  // V_new complete; every read of sS for this chunk done
-      f32x4 st[2][2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) st[t][hh] = own_piece(t, hh) * op.gamma;
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        load_state32(op, next, vnext, voff, vrow, own, w, a, lane16, lg16, q);
+      // the update: Kr^T (exact bf16; the lane's k row 16 (2w + t) + li, tokens
+      // j = 8 lg + e) against V_new ck (tokens j, rows 16 hh + li); the next chunk's
+      // pieces 0 and 1 loaded beside it
+      if constexpr (Split) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          // V_new k ck for tokens j = 8 lg + 4 q + e, rows 16 hh + li
-          const f32x4 b = *reinterpret_cast<const f32x4*>(&sVk[16 * hh + li][8 * lg + 4 * q]);
+          load_state32(op, next, vnext, voff, vrow, own, w, a, lane16, lg16, hh);
+          // V_new ck's three planes, smallest first
+          bf16x8 vk[3];
+#pragma unroll
+          for (int pl = 0; pl < 3; ++pl)
+            vk[pl] = *reinterpret_cast<const bf16x8*>(&sVk[pl][16 * hh + li][8 * lg]);
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            const f32x4 ka = bf16x4(op.kr[t], q);
-            st[t][hh] = mfma(ka.x, b.x, st[t][hh]);
-            st[t][hh] = mfma(ka.y, b.y, st[t][hh]);
-            st[t][hh] = mfma(ka.z, b.z, st[t][hh]);
-            st[t][hh] = mfma(ka.w, b.w, st[t][hh]);
+            f32x4 st = get_own(t, hh) * op.gamma;
+#pragma unroll
+            for (int pl = 2; pl >= 0; --pl)
+              st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, op.kr[t]),
+                                                           vk[pl], st, 0, 0, 0);
+            put_own(t, hh, st);
           }
+          __builtin_amdgcn_sched_barrier(kLoadGroup);
         }
-        __builtin_amdgcn_sched_barrier(kLoadGroup);
+      } else {
+        f32x4 st[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) st[t][hh] = get_own(t, hh) * op.gamma;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          load_state32(op, next, vnext, voff, vrow, own, w, a, lane16, lg16, q);
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            // tokens j = 8 lg + 4 q + e
+            const f32x4 b = *reinterpret_cast<const f32x4*>(&sVk[16 * hh + li][8 * lg + 4 * q]);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              const f32x4 ka = bf16x4(op.kr[t], q);
+              st[t][hh] = mfma(ka.x, b.x, st[t][hh]);
+              st[t][hh] = mfma(ka.y, b.y, st[t][hh]);
+              st[t][hh] = mfma(ka.z, b.z, st[t][hh]);
+              st[t][hh] = mfma(ka.w, b.w, st[t][hh]);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(kLoadGroup);
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) put_own(t, hh, st[t][hh]);
       }
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) own_piece(t, hh) = st[t][hh];
     }
-    // the wave's own pieces: its LDS accesses complete in order, so no barrier is needed
+    // The final state from the wave's own pieces (its LDS accesses complete in order, so no
+    // barrier is needed), through the tile's resource.  Split: the lane's offset formed anew
+    // from the lane count (mbcnt), as a work-item id or offset held across the chunk loop
+    // took a register that loop needs (a spill); the fp32 form's loop leaves room for it.
     if (slot > 0) {
+      const int l = Split ? __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) : lane;
+      const __amdgpu_buffer_rsrc_t srs = state_resource(p, slot, head, true);
+      const uint32_t soff = static_cast<uint32_t>(((row0 + (l & 15)) * kDim + 32 * w + 4 * (l >> 4)) * 4);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-          *reinterpret_cast<f32x4*>(tile_base + 16 * hh * kDim + 16 * (2 * w + t) + 4 * lg) =
-              own_piece(t, hh);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, get_own(t, hh)), srs,
+                                                 static_cast<int>(soff + (16 * hh * kDim + 16 * t) * 4),
+                                                 0, 0);
     }
   } else {
     const int out_row = p.num_v_heads * kDim;   // elements per token row of out
@@ -1731,28 +1869,12 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
       const __amdgpu_buffer_rsrc_t cur = record(c);
       const __amdgpu_buffer_rsrc_t next = record(c + 1);
       __syncthreads();  // sS holds the state at the chunk's start
-      f32x4 o0 = {0.0f, 0.0f, 0.0f, 0.0f};
-      f32x4 o1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q == 0) load_output32(op, cur, own, a, lane16, lg16, 2);   // P of this chunk
-        const f32x4 b0 = s_fragment(q);
-        const f32x4 b1 = s_fragment(q + 4);
-        const f32x4 a0 = bf16x4(op.qr[q >> 1], q & 1);
-        const f32x4 a1 = bf16x4(op.qr[2 + (q >> 1)], q & 1);
-        o0 = mfma(a0.x, b0.x, o0);
-        o1 = mfma(a1.x, b1.x, o1);
-        o0 = mfma(a0.y, b0.y, o0);
-        o1 = mfma(a1.y, b1.y, o1);
-        o0 = mfma(a0.z, b0.z, o0);
-        o1 = mfma(a1.z, b1.z, o1);
-        o0 = mfma(a0.w, b0.w, o0);
-        o1 = mfma(a1.w, b1.w, o1);
-        __builtin_amdgcn_sched_barrier(kLoadGroup);
-      }
+      f32x4 o0 = times_st(op.qr, [&](int q) {   // P of this chunk beside it
+        if (q == 0) load_output32(op, cur, own, a, lane16, lg16, 2);
+      });
       // rows of q S^T scaled to (q^ exp(G)) S^T; P V_new accumulates on top
-      o0 = (o0 + o1) * op.sq;
-      o1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      o0 = o0 * op.sq;
+      f32x4 o1 = {0.0f, 0.0f, 0.0f, 0.0f};
       __syncthreads();  // X complete
       __syncthreads();  // V_new complete
 #pragma unroll
@@ -1836,9 +1958,15 @@ int launch_chunks(const DecodeParams& p, int num_sequences, int64_t num_tokens, 
   if constexpr (TT == 2) {
     const int64_t scan_groups = (pairs + 7) / 8 * 8 * (kDim / 32);
     if (scan_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
-    hipLaunchKernelGGL(chunk_scan32_kernel, dim3(static_cast<uint32_t>(scan_groups)),
-                       dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
-                       static_cast<int>(chunks));
+    // the split products once the prompts average more than one chunk
+    if (num_tokens > 32 * static_cast<int64_t>(num_sequences))
+      hipLaunchKernelGGL(chunk_scan32_kernel<true>, dim3(static_cast<uint32_t>(scan_groups)),
+                         dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
+                         static_cast<int>(chunks));
+    else
+      hipLaunchKernelGGL(chunk_scan32_kernel<false>, dim3(static_cast<uint32_t>(scan_groups)),
+                         dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
+                         static_cast<int>(chunks));
   } else {
     // two row tiles per workgroup once they still give 2 workgroups per CU
     const bool two_tiles = pairs * (kDim / 32) >= 512;
