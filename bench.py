@@ -610,12 +610,13 @@ def prefill(device):
                 ms = start.elapsed_time(end) / reps
                 entry[algorithm] = {"ms": round(ms, 3), "tokens_per_s": round(total / ms * 1e3, 1)}
                 if algorithm != "token_serial":
-                    # matrix-core work of the WY form per (chunk, v-head): for 64 tokens the
-                    # scan's 3,584 fp32 16x16x4 products and the prep's 640 fp32 16x16x4
-                    # (forward substitution) and 80 bf16 16x16x32 ones (the q.k and k.k
-                    # tiles); for 32 tokens 1,664, 192 and 24
+                    # matrix-core work of the WY form per (chunk, v-head), in 16x16x4 fp32
+                    # products and 16x16x32 bf16 ones: for 64 tokens the scan's 3,584 and the
+                    # prep's 640 (forward substitution) and 80 bf16 (the q.k and k.k tiles);
+                    # for 32 tokens the scan's 1,792 (counted once, as fp32 products, where it
+                    # runs them as three bf16 ones), the prep's 8 (T10) and 12 bf16
                     c, scan, subst, tiles = ((64, 3584, 640, 80) if algorithm == "chunked"
-                                             else (32, 1664, 192, 24))
+                                             else (32, 1792, 8, 12))
                     chunk_flop = (scan + subst) * 2048 + tiles * 16384
                     flop = seqs * -(-length // c) * HV * chunk_flop
                     entry[algorithm]["mfma_TFLOPs"] = round(flop / ms / 1e9, 1)
