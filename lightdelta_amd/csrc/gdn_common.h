@@ -118,23 +118,23 @@ __device__ __forceinline__ float softplus(float x) {
 // num_sequences sequences and num_v_heads heads, and the launch of its three phases; the
 // raw outputs go to p.out for prefill_norm_kernel.
 // The form AUTO runs, from the mean prompt length L = num_tokens / num_sequences, measured
-// on MI355X over 1 x 64 .. 4096 x 16 tokens at 32 v heads (ms, token-serial / 64-token
+// on MI355X over 1 x 16 .. 4096 x 16 tokens at 32 v heads (ms, token-serial / 64-token
 // chunks / 32-token chunks):
-//   * token-serial below 20 tokens (1024 x 16: 1.50 / 3.46 / 1.88) and for 33 .. 40, where a
-//     second 32-token chunk would hold few tokens (1024 x 36: 2.86 / 3.60 / 3.27; at 44:
-//     3.44 / 3.67 / 3.31);
-//   * 64-token chunks for long prompts in fewer than 64 (sequence, head) pairs, where the
-//     chunk-by-chunk chain is the time and 64-token chunks halve it (1 x 4096: 2.72 / 0.25 /
-//     0.39; 1 x 512: 0.36 / 0.059 / 0.067; 2 x 2048, 64 pairs: 1.40 / 0.247 / 0.237);
-//   * 32-token chunks otherwise (1024 x 32: 2.61 / 3.56 / 2.07; 32 x 1024: 2.65 / 1.59 /
-//     1.48; 1 x 64: 0.054 / 0.034 / 0.031).
+//   * token-serial below 20 tokens (1024 x 16: 1.54 / 3.47 / 1.70; 512 x 20: 0.90 / 1.76 /
+//     0.89; 1 x 16: 0.028 / 0.033 / 0.029);
+//   * 64-token chunks for prompts of 512 tokens or more in fewer than 64 (sequence, head)
+//     pairs, where the chunk-by-chunk chain is the time and 64-token chunks halve it
+//     (1 x 4096: 2.73 / 0.250 / 0.296; 1 x 512: 0.358 / 0.0565 / 0.0571; 1 x 256: 0.185 /
+//     0.046 / 0.040; 2 x 2048, 64 pairs: 1.39 / 0.243 / 0.175);
+//   * 32-token chunks otherwise (1024 x 32: 2.63 / 3.53 / 1.85; 1024 x 36: 2.91 / 3.58 /
+//     2.63; 32 x 1024: 2.66 / 1.58 / 1.07; 1 x 64: 0.053 / 0.032 / 0.028).
 // Returns the tokens per chunk (64 or 32), or 0 for the token-serial form.
 inline int prefill_auto_chunk_tokens(int64_t num_tokens, int64_t num_sequences,
                                      int64_t num_v_heads) {
   if (num_sequences <= 0 || num_tokens <= 0) return 0;
   const int64_t mean = num_tokens / num_sequences;
-  if (mean < 20 || (mean > 32 && mean <= 40)) return 0;
-  if (num_sequences * num_v_heads < 64 && mean >= 256) return 64;
+  if (mean < 20) return 0;
+  if (num_sequences * num_v_heads < 64 && mean >= 512) return 64;
   return 32;
 }
 

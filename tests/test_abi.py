@@ -170,17 +170,15 @@ def test_prefill_workspace_query_and_chunked_without_workspace():
     (4096, 1, 63, 64),        # 63 (sequence, head) pairs
     (4096, 1, 64, 32),        # 64 pairs
     (2 * 2048, 2, 32, 32),
-    (255, 1, 32, 32),         # a mean under 256 tokens
+    (511, 1, 32, 32),         # a mean under 512 tokens
     (32 * 1024, 32, 32, 32),  # long prompts that fill the GPU anyway
     (16 * 128, 16, 32, 32),
     (512 * 64, 512, 32, 32),
     (1024 * 32, 1024, 32, 32),  # short prompts: one full 32-token chunk each
+    (1024 * 36, 1024, 32, 32),  # a second chunk that holds few tokens
     (1024 * 20, 1024, 32, 32),  # the shortest that go chunked
     (1024 * 20 - 1, 1024, 32, 0),
     (1024 * 16, 1024, 32, 0),
-    (1024 * 33, 1024, 32, 0),   # a second chunk that would hold few tokens
-    (1024 * 41 - 1, 1024, 32, 0),
-    (1024 * 41, 1024, 32, 32),
     (2 * 16, 2, 32, 0),
     (0, 1, 32, 0),
     (100, 0, 32, 0),
