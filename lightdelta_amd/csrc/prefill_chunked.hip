@@ -1457,9 +1457,11 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 // chunk.  State wave w (0..3): Y = K_a S_h^T from the bf16 keys, X = diag(beta) V -
 // diag(ws) Y with V read from qkv; after a barrier V_new = T_a X_h (all 32 tokens of X);
 // after another, the update of k tiles 2w and 2w + 1 of both row tiles.  Output wave 4 + w:
-// the raw outputs of its tile.  Per chunk and SIMD 112 products of 16 x 16 x 4 for 32
-// tokens, against 224 for 64 tokens in chunk_scan_kernel<2> (P V_new grows with the square
-// of the chunk).
+// the raw outputs of its tile.  Per chunk and SIMD the work of 112 products of 16 x 16 x 4
+// for 32 tokens, as chunk_scan_kernel<2> does 224 for 64 tokens; with Split, the 96 of them
+// with S or V_new ck as an operand run as 36 bf16 products of 16 x 16 x 32 (a third of the
+// matrix time), the other 16 (T X, P V_new) stay fp32.
+
 // x = s1 + s2 + s3 exactly, in bf16 (each part the round-to-nearest-even of what the
 // earlier ones leave, and every remainder exact in fp32: 8 + 8 + 8 bits of x's 24), so a
 // product of an exact bf16 operand with x runs on the bf16 matrix cores as three products
