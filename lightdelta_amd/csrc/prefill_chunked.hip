@@ -1470,22 +1470,32 @@ struct Split4 {
   uint2 p[3];
 };
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two values to a packed bf16 pair (round to nearest even, one v_cvt_pk_bf16_f32), and back
+__device__ __forceinline__ uint32_t bf16_pair(f32x2 v) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ f32x2 pair_f32(uint32_t w) {
+  return f32x2{__builtin_bit_cast(float, w << 16), __builtin_bit_cast(float, w & 0xffff0000u)};
+}
+
 __device__ __forceinline__ Split4 split4(f32x4 x) {
   Split4 sp;
-  uint16_t part[3][4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float r = x[e];
+  for (int j = 0; j < 2; ++j) {
+    f32x2 r = {x[2 * j], x[2 * j + 1]};
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      part[i][e] = to_bf16(r);
-      r -= bf16_to_f32(part[i][e]);
+      const uint32_t w = bf16_pair(r);
+      (j == 0 ? sp.p[i].x : sp.p[i].y) = w;
+      if (i < 2) {
+        const f32x2 back = pair_f32(w);
+        r = f32x2{r.x - back.x, r.y - back.y};
+      }
     }
   }
-#pragma unroll
-  for (int i = 0; i < 3; ++i)
-    sp.p[i] = uint2{part[i][0] | (static_cast<uint32_t>(part[i][1]) << 16),
-                    part[i][2] | (static_cast<uint32_t>(part[i][3]) << 16)};
   return sp;
 }
 
@@ -1493,14 +1503,12 @@ __device__ __forceinline__ Split4 split4(f32x4 x) {
 __device__ __forceinline__ f32x4 join4(const Split4& sp) {
   f32x4 x;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t shift = (e & 1) * 16;
-    const uint32_t w0 = e < 2 ? sp.p[0].x : sp.p[0].y;
-    const uint32_t w1 = e < 2 ? sp.p[1].x : sp.p[1].y;
-    const uint32_t w2 = e < 2 ? sp.p[2].x : sp.p[2].y;
-    x[e] = (bf16_to_f32(static_cast<uint16_t>(w0 >> shift)) +
-            bf16_to_f32(static_cast<uint16_t>(w1 >> shift))) +
-           bf16_to_f32(static_cast<uint16_t>(w2 >> shift));
+  for (int j = 0; j < 2; ++j) {
+    const f32x2 s1 = pair_f32(j == 0 ? sp.p[0].x : sp.p[0].y);
+    const f32x2 s2 = pair_f32(j == 0 ? sp.p[1].x : sp.p[1].y);
+    const f32x2 s3 = pair_f32(j == 0 ? sp.p[2].x : sp.p[2].y);
+    x[2 * j] = (s1.x + s2.x) + s3.x;
+    x[2 * j + 1] = (s1.y + s2.y) + s3.y;
   }
   return x;
 }
