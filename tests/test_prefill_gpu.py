@@ -83,6 +83,28 @@ def test_prefill_matches_oracle(gpu, heads, algorithm):
     assert torch.equal(case["pool"][0], before[0])
 
 
+@pytest.mark.parametrize("heads", [(16, 32), (4, 8), (16, 48), (8, 8)])
+@pytest.mark.parametrize("form", CHUNKED_FORMS)
+def test_prefill_longer_prompts_match_oracle(gpu, heads, form):
+    """Prompts of 40 tokens or more on average (the 32-token form's split products, several
+    chunks per prompt), every head layout, against the oracle."""
+    announce(test="prefill_oracle_longer", heads=heads, form=form)
+    saved = ops.prefill_algorithm()
+    ops.set_prefill_algorithm(form)
+    try:
+        case = prefill_case(gpu, [40, 0, 97, 33, 65], heads=heads, seed=heads[1] + 1)
+        case["has_initial"][2] = False
+        case["slots"][4] = 0  # padding slot
+        exp_out, exp_pool, pre = expected_prefill(*[case[k] for k in PREFILL], 1e-6,
+                                                  return_pre=True)
+        run(case)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_prefill_algorithm(saved)
+    assert_bf16_outputs(case["out"], exp_out, pre)
+    assert_states(case["pool"], exp_pool)
+
+
 @pytest.mark.parametrize("dt_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("w_dtype", [torch.float32, torch.bfloat16])
 def test_prefill_parameter_dtypes(gpu, dt_dtype, w_dtype, algorithm):

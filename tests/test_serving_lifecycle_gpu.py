@@ -1,6 +1,7 @@
 """Requests through the ops in the order a serving layer calls them, one pool throughout:
 
-1. a prefill of three new prompts (70, 130 and 5 tokens; chunked form) into their slots;
+1. a prefill of three new prompts (70, 130 and 5 tokens; chunked form, 64- or 32-token
+   chunks) into their slots;
 2. three single-token decode steps on those slots;
 3. a 4-token speculative verify per request: the state after token t goes to column t of the
    request's slot row [home, s1, s2, s3], then a random accepted length per request;
@@ -91,8 +92,9 @@ def decode(tok, case, pool, ref_pool, indices, accepted, tokens_each, label):
     return exp_pool
 
 
-def test_request_lifecycle(gpu):
-    print("case: serving lifecycle, 16/32 heads, 16-slot pool", flush=True)
+@pytest.mark.parametrize("form", ["chunked", "chunked_32"])
+def test_request_lifecycle(gpu, form):
+    print(f"case: serving lifecycle, 16/32 heads, 16-slot pool, {form} prefill", flush=True)
     tok = Tokens(70 + 130 + 5 + 3 * 3 + 3 * 4 + 3 + 40, gpu)
     case = tok.case
     pool = case["pool"]
@@ -100,7 +102,7 @@ def test_request_lifecycle(gpu):
     home = [3, 7, 9]
     scratch = torch.tensor([[1, 2, 4], [5, 6, 8], [10, 11, 12]], dtype=torch.int32)
     saved = ops.prefill_algorithm()
-    ops.set_prefill_algorithm("chunked")
+    ops.set_prefill_algorithm(form)
     try:
         ref_pool = prefill(tok, case, pool, ref_pool, home, [False] * 3, [70, 130, 5],
                            "prefill of 3 prompts")
