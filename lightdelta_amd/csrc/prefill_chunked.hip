@@ -204,6 +204,7 @@ constexpr int kPrepTokens = kC / kPrepWaves;   // tokens normalised per wave
 
 // ---- phase 1: per (chunk, k-head), then per v-head of its group -----------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16v4 __attribute__((ext_vector_type(4)));
 
 // One workgroup per (chunk, k-head).  What depends on q and k alone -- their loads, inverse
 // norms, the raw q.k and k.k tiles on the bf16 matrix cores -- is done once; then the
@@ -1481,8 +1482,18 @@ __device__ __forceinline__ f32x2 pair_f32(uint32_t w) {
   return f32x2{__builtin_bit_cast(float, w << 16), __builtin_bit_cast(float, w & 0xffff0000u)};
 }
 
+// Each remainder r - s in one instruction: a dot product of the rounded pair with (-1, 0)
+// or (0, -1) added to r (v_dot2c_f32_bf16; exact products, and the sum is r - s, which
+// fp32 holds exactly).  (-1, 0) is set in an SGPR: as an operand the compiler encodes it
+// as the inline constant -1.0, which this instruction reads as the fp32 word 0xbf800000,
+// i.e. (0, -1).  Being an intrinsic, the first remainder also keeps a product passed as x
+// rounded to fp32 (x - s1 written out would be contracted into an fma of its factors).
 __device__ __forceinline__ Split4 split4(f32x4 x) {
   Split4 sp;
+  uint32_t minus_lo_bits;
+  asm("s_mov_b32 %0, 0xbf80" : "=s"(minus_lo_bits));
+  const bf16x2 minus_lo = __builtin_bit_cast(bf16x2, minus_lo_bits);
+  const bf16x2 minus_hi = __builtin_bit_cast(bf16x2, 0xbf800000u);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     f32x2 r = {x[2 * j], x[2 * j + 1]};
@@ -1491,26 +1502,13 @@ __device__ __forceinline__ Split4 split4(f32x4 x) {
       const uint32_t w = bf16_pair(r);
       (j == 0 ? sp.p[i].x : sp.p[i].y) = w;
       if (i < 2) {
-        const f32x2 back = pair_f32(w);
-        r = f32x2{r.x - back.x, r.y - back.y};
+        const bf16x2 s = __builtin_bit_cast(bf16x2, w);
+        r = f32x2{__builtin_amdgcn_fdot2_f32_bf16(s, minus_lo, r.x, false),
+                  __builtin_amdgcn_fdot2_f32_bf16(s, minus_hi, r.y, false)};
       }
     }
   }
   return sp;
-}
-
-// The four values back: (s1 + s2) + s3, exact (each partial sum is x less a tail it lacks).
-__device__ __forceinline__ f32x4 join4(const Split4& sp) {
-  f32x4 x;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const f32x2 s1 = pair_f32(j == 0 ? sp.p[0].x : sp.p[0].y);
-    const f32x2 s2 = pair_f32(j == 0 ? sp.p[1].x : sp.p[1].y);
-    const f32x2 s3 = pair_f32(j == 0 ? sp.p[2].x : sp.p[2].y);
-    x[2 * j] = (s1.x + s2.x) + s3.x;
-    x[2 * j + 1] = (s1.y + s2.y) + s3.y;
-  }
-  return x;
 }
 
 // scan32's LDS for S and V_new ck: three bf16 planes each (Split) or fp32
@@ -1716,14 +1714,23 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
         *reinterpret_cast<f32x4*>(&sS[16 * hh + li][k]) = v;
       }
     };
+    // (Split) the identity in the A layout of v_mfma_f32_16x16x16_bf16 (lane (li, lg): row
+    // li, columns 4 lg .. 4 lg + 3), so that I B hands each lane its own four B values:
+    // three such products sum the planes in fp32, (s1 + s2) + s3, exactly (every partial
+    // sum is the value less a tail it lacks), on the matrix pipe instead of 20 VALU
+    // instructions per piece
+    const uint32_t one_at = static_cast<uint32_t>(li - 4 * lg);
+    const bf16v4 ident = __builtin_bit_cast(
+        bf16v4, one_at < 4 ? 0x3f80ull << (16 * one_at) : 0ull);
     auto get_own = [&](int t, int hh) __attribute__((always_inline)) {
       const int k = 16 * (2 * w + t) + 4 * lg;
       if constexpr (Split) {
-        Split4 sp;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl)
-          sp.p[pl] = *reinterpret_cast<const uint2*>(&sS[pl][16 * hh + li][k]);
-        return join4(sp);
+          acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+              ident, *reinterpret_cast<const bf16v4*>(&sS[pl][16 * hh + li][k]), acc, 0, 0, 0);
+        return acc;
       } else {
         return *reinterpret_cast<const f32x4*>(&sS[16 * hh + li][k]);
       }
