@@ -708,7 +708,7 @@ __device__ __forceinline__ uint32_t prep32_tile(int index) {
 }
 
 template <bool DtBf16, bool Wide>
-__global__ __launch_bounds__(kPrep32Threads)
+__global__ __launch_bounds__(kPrep32Threads) __attribute__((amdgpu_waves_per_eu(5)))
 void chunk_prep32_kernel(const DecodeParams p, int num_sequences, float* ws,
                          const int32_t* chunk_start, int records) {
   using R = Rec32;
