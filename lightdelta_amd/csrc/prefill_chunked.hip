@@ -3,7 +3,9 @@
 // (v_mfma_f32_16x16x4_f32: fp32 operands, fp32 accumulation, so the arithmetic is the
 // vector ALUs' up to summation order), the dot products of the bf16 inputs q . k and k . k
 // on the bf16 ones (v_mfma_f32_16x16x32_bf16: the inputs as they are, exact products, fp32
-// sums; the norms are applied to the sums).
+// sums; the norms are applied to the sums), and in the scans a product of q or k as stored
+// (exact bf16) with fp32 data as three bf16 products against the data's exact three-way
+// bf16 split (the same exact terms, fp32 sums).
 //
 // Per chunk (tokens i = 0 .. n-1, n <= C, C = 64 or 32), with g_i the log decay,
 // G_i = g_0 + .. + g_i, Gam_ij = exp(G_i - G_j), beta_i, normalised q^_i (scaled) and k^_i,
@@ -1015,7 +1017,56 @@ void chunk_prep32_kernel(const DecodeParams p, int num_sequences, float* ws,
 // products, so with RT = 2 the chunk operands cross each CU half as often per product (for
 // many sequences, where the workgroups are plentiful); RT = 1 has twice the workgroups, for
 // few sequences, where the scan's latency is the time.
+// Per chunk and SIMD: W S^T (32 RT products of 16 x 16 x 4) and P V_new (16 RT) in fp32;
+// Qr S^T and the update as 12 RT bf16 products of 16 x 16 x 32 each (split operands), where
+// in fp32 they took 32 RT each: 1,920 matrix cycles per chunk, SIMD and row tile, where
+// all-fp32 products took 3,584.
 constexpr int kScanThreads = 512;
+
+// x = s1 + s2 + s3 exactly, in bf16 (each part the round-to-nearest-even of what the
+// earlier ones leave, and every remainder exact in fp32: 8 + 8 + 8 bits of x's 24), so a
+// product of an exact bf16 operand with x runs on the bf16 matrix cores as three products
+// with exact terms and fp32 sums.  p[i] holds part i + 1 of four values.
+struct Split4 {
+  uint2 p[3];
+};
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two values to a packed bf16 pair (round to nearest even, one v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t bf16_pair(f32x2 v) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// Each remainder r - s in one instruction: a dot product of the rounded pair with (-1, 0)
+// or (0, -1) added to r (v_dot2c_f32_bf16; exact products, and the sum is r - s, which
+// fp32 holds exactly).  (-1, 0) is set in an SGPR: as an operand the compiler encodes it
+// as the inline constant -1.0, which this instruction reads as the fp32 word 0xbf800000,
+// i.e. (0, -1).  Being an intrinsic, the first remainder also keeps a product passed as x
+// rounded to fp32 (x - s1 written out would be contracted into an fma of its factors).
+__device__ __forceinline__ Split4 split4(f32x4 x) {
+  Split4 sp;
+  uint32_t minus_lo_bits;
+  asm("s_mov_b32 %0, 0xbf80" : "=s"(minus_lo_bits));
+  const bf16x2 minus_lo = __builtin_bit_cast(bf16x2, minus_lo_bits);
+  const bf16x2 minus_hi = __builtin_bit_cast(bf16x2, 0xbf800000u);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    f32x2 r = {x[2 * j], x[2 * j + 1]};
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const uint32_t w = bf16_pair(r);
+      (j == 0 ? sp.p[i].x : sp.p[i].y) = w;
+      if (i < 2) {
+        const bf16x2 s = __builtin_bit_cast(bf16x2, w);
+        r = f32x2{__builtin_amdgcn_fdot2_f32_bf16(s, minus_lo, r.x, false),
+                  __builtin_amdgcn_fdot2_f32_bf16(s, minus_hi, r.y, false)};
+      }
+    }
+  }
+  return sp;
+}
 
 template <int RT>
 struct StateOperands {
@@ -1147,6 +1198,10 @@ __device__ __forceinline__ void ring_scan(Step& step, Operands& ring0, Operands&
   }
 }
 
+// The products with an exact bf16 operand -- the update's Kr^T (V_new ck) and the outputs'
+// Qr S^T -- run on the bf16 matrix cores as three products against the other operand's
+// exact three-way split, which the state waves keep in LDS (S's planes beside its fp32
+// values, V_new ck's planes beside V_new); W S^T and P V_new stay fp32.
 template <int RT>
 __global__ __launch_bounds__(kScanThreads)
 void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
@@ -1194,7 +1249,9 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   constexpr int kVRow = kC + 4;
   __shared__ __attribute__((aligned(16))) float sS[kRows][kSRow];   // S rows [row][k]
   __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];  // V_new^T [row][token]
-  __shared__ __attribute__((aligned(16))) float sVk[kRows][kVRow];  // ditto, token j times ck_j
+  // the three planes of V_new^T with token j times ck_j, and of S
+  __shared__ __attribute__((aligned(16))) uint16_t sVk[3][kRows][kC + 8];     // rows of 144 B
+  __shared__ __attribute__((aligned(16))) uint16_t sSp[3][kRows][kDim + 8];   // rows of 272 B
 
   // The operands of chunk c: through a resource over the records of the head's group (the
   // first v-head's record holds the group's Qr and Kr), the head's own at byte `own`.
@@ -1214,8 +1271,13 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
   auto vn_fragment = [&](int h, int q) {
     return *reinterpret_cast<const f32x4*>(&sVn[16 * h + li][16 * lg + 4 * q]);
   };
-  auto vk_fragment = [&](int h, int q) {
-    return *reinterpret_cast<const f32x4*>(&sVk[16 * h + li][16 * lg + 4 * q]);
+  // the state waves' pieces of S to LDS: fp32, and the three planes
+  auto put_state = [&](int t, int h, f32x4 v) __attribute__((always_inline)) {
+    const int k = 16 * (2 * w + t) + 4 * lg;
+    *reinterpret_cast<f32x4*>(&sS[16 * h + li][k]) = v;
+    const Split4 sp = split4(v);
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) *reinterpret_cast<uint2*>(&sSp[pl][16 * h + li][k]) = sp.p[pl];
   };
   const uint32_t lg16 = static_cast<uint32_t>(lg) * 16;
 
@@ -1233,8 +1295,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
     for (int h = 0; h < RT; ++h)
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        *reinterpret_cast<f32x4*>(&sS[16 * h + li][16 * (2 * w + t) + 4 * lg]) = st[t][h];
+      for (int t = 0; t < 2; ++t) put_state(t, h, st[t][h]);
     // Operands of later chunks are loaded while chunk c computes: into a ring of three
     // register sets (the loop is unrolled by three, so no set is copied: each is waited for
     // only where it is used), or into the one set as its pieces fall free.
@@ -1274,7 +1335,10 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
       for (int h = 0; h < RT; ++h) {
         const f32x4 vn = op.u[h] - (vn0[h] + vn1[h]);
         *reinterpret_cast<f32x4*>(&sVn[16 * h + li][16 * w + 4 * lg]) = vn;
-        *reinterpret_cast<f32x4*>(&sVk[16 * h + li][16 * w + 4 * lg]) = vn * op.ck;
+        const Split4 sp = split4(vn * op.ck);
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint2*>(&sVk[pl][16 * h + li][16 * w + 4 * lg]) = sp.p[pl];
       }
       __syncthreads();  // V_new complete; every read of sS for this chunk done
 #pragma unroll
@@ -1284,16 +1348,22 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         load_state_piece(fill, next, own, w, lane16, lg16, row_block * RT, kHalf ? q : 4 + q);
+        // after every second piece, token block qq: Kr^T's tokens 16 lg + 8 qq + e (exact
+        // bf16) against V_new ck's three planes, smallest first
+        if (q & 1) {
+          const int qq = q >> 1;
 #pragma unroll
-        for (int h = 0; h < RT; ++h) {
-          const f32x4 b = vk_fragment(h, q);
+          for (int h = 0; h < RT; ++h) {
+            bf16x8 vk[3];
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const f32x4 a = bf16x4(op.kr[t][q >> 1], q & 1);
-            st[t][h] = mfma(a.x, b.x, st[t][h]);
-            st[t][h] = mfma(a.y, b.y, st[t][h]);
-            st[t][h] = mfma(a.z, b.z, st[t][h]);
-            st[t][h] = mfma(a.w, b.w, st[t][h]);
+            for (int pl = 0; pl < 3; ++pl)
+              vk[pl] = *reinterpret_cast<const bf16x8*>(&sVk[pl][16 * h + li][16 * lg + 8 * qq]);
+#pragma unroll
+            for (int pl = 2; pl >= 0; --pl)
+#pragma unroll
+              for (int t = 0; t < 2; ++t)
+                st[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, op.kr[t][qq]), vk[pl], st[t][h], 0, 0, 0);
           }
         }
         __builtin_amdgcn_sched_barrier(kLoadGroup);
@@ -1301,8 +1371,7 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
       for (int h = 0; h < RT; ++h)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          *reinterpret_cast<f32x4*>(&sS[16 * h + li][16 * (2 * w + t) + 4 * lg]) = st[t][h];
+        for (int t = 0; t < 2; ++t) put_state(t, h, st[t][h]);
     };
     // The first sets, piece by piece in the loop's order, so that the wait counts at the
     // loop head are the same from either side.
@@ -1362,18 +1431,15 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
           load_output_piece(fill, cur, own, w, lane16, lg16, 4 + q);   // P of this chunk
 #pragma unroll
         for (int h = 0; h < RT; ++h) {
-          const f32x4 b0 = s_fragment(h, q);
-          const f32x4 b1 = s_fragment(h, q + 4);
-          const f32x4 a0 = bf16x4(op.qr[q >> 1], q & 1);
-          const f32x4 a1 = bf16x4(op.qr[2 + (q >> 1)], q & 1);
-          o0[h] = mfma(a0.x, b0.x, o0[h]);
-          o1[h] = mfma(a1.x, b1.x, o1[h]);
-          o0[h] = mfma(a0.y, b0.y, o0[h]);
-          o1[h] = mfma(a1.y, b1.y, o1[h]);
-          o0[h] = mfma(a0.z, b0.z, o0[h]);
-          o1[h] = mfma(a1.z, b1.z, o1[h]);
-          o0[h] = mfma(a0.w, b0.w, o0[h]);
-          o1[h] = mfma(a1.w, b1.w, o1[h]);
+          // Qr's k = 32 lg + 8 q + e (exact bf16) against S's three planes, smallest first,
+          // on two accumulation chains
+          f32x4& o = (q & 1) ? o1[h] : o0[h];
+#pragma unroll
+          for (int pl = 2; pl >= 0; --pl)
+            o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, op.qr[q]),
+                *reinterpret_cast<const bf16x8*>(&sSp[pl][16 * h + li][32 * lg + 8 * q]), o, 0, 0,
+                0);
         }
         __builtin_amdgcn_sched_barrier(kLoadGroup);
       }
@@ -1459,57 +1525,9 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 // diag(ws) Y with V read from qkv; after a barrier V_new = T_a X_h (all 32 tokens of X);
 // after another, the update of k tiles 2w and 2w + 1 of both row tiles.  Output wave 4 + w:
 // the raw outputs of its tile.  Per chunk and SIMD the work of 112 products of 16 x 16 x 4
-// for 32 tokens, as chunk_scan_kernel<2> does 224 for 64 tokens; with Split, the 96 of them
-// with S or V_new ck as an operand run as 36 bf16 products of 16 x 16 x 32 (a third of the
-// matrix time), the other 16 (T X, P V_new) stay fp32.
-
-// x = s1 + s2 + s3 exactly, in bf16 (each part the round-to-nearest-even of what the
-// earlier ones leave, and every remainder exact in fp32: 8 + 8 + 8 bits of x's 24), so a
-// product of an exact bf16 operand with x runs on the bf16 matrix cores as three products
-// with exact terms and fp32 sums.  p[i] holds part i + 1 of four values.
-struct Split4 {
-  uint2 p[3];
-};
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// two values to a packed bf16 pair (round to nearest even, one v_cvt_pk_bf16_f32), and back
-__device__ __forceinline__ uint32_t bf16_pair(f32x2 v) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-}
-__device__ __forceinline__ f32x2 pair_f32(uint32_t w) {
-  return f32x2{__builtin_bit_cast(float, w << 16), __builtin_bit_cast(float, w & 0xffff0000u)};
-}
-
-// Each remainder r - s in one instruction: a dot product of the rounded pair with (-1, 0)
-// or (0, -1) added to r (v_dot2c_f32_bf16; exact products, and the sum is r - s, which
-// fp32 holds exactly).  (-1, 0) is set in an SGPR: as an operand the compiler encodes it
-// as the inline constant -1.0, which this instruction reads as the fp32 word 0xbf800000,
-// i.e. (0, -1).  Being an intrinsic, the first remainder also keeps a product passed as x
-// rounded to fp32 (x - s1 written out would be contracted into an fma of its factors).
-__device__ __forceinline__ Split4 split4(f32x4 x) {
-  Split4 sp;
-  uint32_t minus_lo_bits;
-  asm("s_mov_b32 %0, 0xbf80" : "=s"(minus_lo_bits));
-  const bf16x2 minus_lo = __builtin_bit_cast(bf16x2, minus_lo_bits);
-  const bf16x2 minus_hi = __builtin_bit_cast(bf16x2, 0xbf800000u);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    f32x2 r = {x[2 * j], x[2 * j + 1]};
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const uint32_t w = bf16_pair(r);
-      (j == 0 ? sp.p[i].x : sp.p[i].y) = w;
-      if (i < 2) {
-        const bf16x2 s = __builtin_bit_cast(bf16x2, w);
-        r = f32x2{__builtin_amdgcn_fdot2_f32_bf16(s, minus_lo, r.x, false),
-                  __builtin_amdgcn_fdot2_f32_bf16(s, minus_hi, r.y, false)};
-      }
-    }
-  }
-  return sp;
-}
+// for 32 tokens; with Split, the 96 of them with S or V_new ck as an operand run as 36 bf16
+// products of 16 x 16 x 32 (a third of the matrix time), the other 16 (T X, P V_new) stay
+// fp32.
 
 // scan32's LDS for S and V_new ck: three bf16 planes each (Split) or fp32
 template <bool Split>
