@@ -98,13 +98,6 @@ constexpr int64_t kMiscWs = 192;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// four consecutive bf16 of a 16-byte piece (half 0: elements 0..3, half 1: 4..7) as fp32
-__device__ __forceinline__ f32x4 bf16x4(const u32x4& v, int half) {
-  const uint32_t a = half ? v.z : v.x;
-  const uint32_t b = half ? v.w : v.y;
-  return f32x4{__builtin_bit_cast(float, a << 16), __builtin_bit_cast(float, a & 0xffff0000u),
-               __builtin_bit_cast(float, b << 16), __builtin_bit_cast(float, b & 0xffff0000u)};
-}
 
 __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -1525,21 +1518,9 @@ void chunk_scan_kernel(const DecodeParams p, int num_sequences, float* ws,
 // diag(ws) Y with V read from qkv; after a barrier V_new = T_a X_h (all 32 tokens of X);
 // after another, the update of k tiles 2w and 2w + 1 of both row tiles.  Output wave 4 + w:
 // the raw outputs of its tile.  Per chunk and SIMD the work of 112 products of 16 x 16 x 4
-// for 32 tokens; with Split, the 96 of them with S or V_new ck as an operand run as 36 bf16
-// products of 16 x 16 x 32 (a third of the matrix time), the other 16 (T X, P V_new) stay
-// fp32.
-
-// scan32's LDS for S and V_new ck: three bf16 planes each (Split) or fp32
-template <bool Split>
-struct Scan32Lds {
-  typedef uint16_t S[3][32][kDim + 8];   // rows of 272 bytes
-  typedef uint16_t Vk[3][32][32 + 8];
-};
-template <>
-struct Scan32Lds<false> {
-  typedef float S[32][kDim + 4];
-  typedef float Vk[32][32 + 4];
-};
+// for 32 tokens: the 96 of them with S or V_new ck as an operand run as 36 bf16 products of
+// 16 x 16 x 32 against their exact three-way splits (a third of the matrix time), the other
+// 16 (T X, P V_new) stay fp32.
 
 struct Scan32State {
   u32x4 kq[4];  // Kq [16 a + li][32 lg + 8 qq + e] (bf16)
@@ -1608,12 +1589,9 @@ __device__ __forceinline__ void load_output32(Scan32Output& o, __amdgpu_buffer_r
   }
 }
 
-// Split: the products with S and with V_new ck on the bf16 matrix cores, each as three
-// products against split3's parts (fp32-exact operands, fp32 sums, 80 VGPRs); else all on
-// the fp32 matrix cores.  The split halves the scan's matrix time and pays for it in
-// splitting VALU work and LDS traffic, which prompts of one chunk (latency-bound) do not
-// recover.
-template <bool Split>
+// The products with S and with V_new ck on the bf16 matrix cores, each as three products
+// against split4's parts (fp32-exact operands, fp32 sums, 80 VGPRs).  (Prompts of one
+// chunk once kept fp32 products, before the splits took one instruction per remainder.)
 __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(6)))
 void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
                          const int32_t* chunk_start, int records) {
@@ -1648,11 +1626,10 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
   const int chunks = min((eos - bos + kCs - 1) / kCs, max(records - gbase, 0));
 
   constexpr int kVRow = kCs + 4;    // fp32 row of V_new or X
-  // S [row][k] and V_new with its rows scaled by ck [row][token]: fp32, or (Split) three
-  // bf16 planes each (split4: their sum is the fp32 value exactly); V_new and X in fp32 for
-  // the fp32 products
-  __shared__ __attribute__((aligned(16))) typename Scan32Lds<Split>::S sS;
-  __shared__ __attribute__((aligned(16))) typename Scan32Lds<Split>::Vk sVk;
+  // S [row][k] and V_new with its rows scaled by ck [row][token] as three bf16 planes each
+  // (split4: their sum is the fp32 value exactly); V_new and X in fp32 for the fp32 products
+  __shared__ __attribute__((aligned(16))) uint16_t sS[3][32][kDim + 8];   // rows of 272 bytes
+  __shared__ __attribute__((aligned(16))) uint16_t sVk[3][32][32 + 8];
   __shared__ __attribute__((aligned(16))) float sVn[kRows][kVRow];   // V_new^T [row][token]
   __shared__ __attribute__((aligned(16))) float sX[kRows][kVRow];    // X^T [row][token]
 
@@ -1669,40 +1646,20 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
         c < chunks ? group_bytes : 0);
   };
   // X_a S_h^T for bf16 rows X, the lane's values k = 32 lg + 8 qq .. + 7 in x[qq], row
-  // 16 h + li of S.  Split: instruction qq of a bf16 product takes those 8 values against
-  // each of S's planes, smallest first.  fp32: two chains of 16 products (k < 64, k >= 64 of
-  // each lane group), 4 values each; `load(q)` issues operand loads before step q's group.
+  // 16 h + li of S: instruction qq of a bf16 product takes those 8 values against each of
+  // S's planes, smallest first; `load()` issues operand loads ahead of the products.
   auto times_st = [&](const u32x4 (&x)[4], auto&& load) __attribute__((always_inline)) {
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (Split) {
-      load(0);
-      __builtin_amdgcn_sched_barrier(kLoadGroup);
+    load();
+    __builtin_amdgcn_sched_barrier(kLoadGroup);
 #pragma unroll
-      for (int pl = 2; pl >= 0; --pl)
+    for (int pl = 2; pl >= 0; --pl)
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, x[qq]),
-              *reinterpret_cast<const bf16x8*>(&sS[pl][16 * h + li][32 * lg + 8 * qq]), acc, 0,
-              0, 0);
-    } else {
-      f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        load(q);
-        const f32x4 b0 = *reinterpret_cast<const f32x4*>(&sS[16 * h + li][32 * lg + 4 * q]);
-        const f32x4 b1 = *reinterpret_cast<const f32x4*>(&sS[16 * h + li][32 * lg + 16 + 4 * q]);
-        const f32x4 a0 = bf16x4(x[q >> 1], q & 1);
-        const f32x4 a1 = bf16x4(x[2 + (q >> 1)], q & 1);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc = mfma(a0[e], b0[e], acc);
-          acc1 = mfma(a1[e], b1[e], acc1);
-        }
-        __builtin_amdgcn_sched_barrier(kLoadGroup);
-      }
-      acc += acc1;
-    }
+      for (int qq = 0; qq < 4; ++qq)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, x[qq]),
+            *reinterpret_cast<const bf16x8*>(&sS[pl][16 * h + li][32 * lg + 8 * qq]), acc, 0, 0,
+            0);
     return acc;
   };
   // chunk c's rows of qkv (0 bytes past the last chunk, or a sequence's rows past its end:
@@ -1719,20 +1676,15 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
 
   if (wave < 4) {
     // The wave's pieces of the state, S[row0 + 16 hh + li][16 (2w + t) + 4 lg + r], live in
-    // sS between chunks (Split: in its planes, split on the way in and summed on the way out,
-    // exactly).
+    // sS between chunks, in its planes: split on the way in and summed on the way out,
+    // exactly.
     auto put_own = [&](int t, int hh, f32x4 v) __attribute__((always_inline)) {
       const int k = 16 * (2 * w + t) + 4 * lg;
-      if constexpr (Split) {
-        const Split4 sp = split4(v);
+      const Split4 sp = split4(v);
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
-          *reinterpret_cast<uint2*>(&sS[pl][16 * hh + li][k]) = sp.p[pl];
-      } else {
-        *reinterpret_cast<f32x4*>(&sS[16 * hh + li][k]) = v;
-      }
+      for (int pl = 0; pl < 3; ++pl) *reinterpret_cast<uint2*>(&sS[pl][16 * hh + li][k]) = sp.p[pl];
     };
-    // (Split) the identity in the A layout of v_mfma_f32_16x16x16_bf16 (lane (li, lg): row
+    // The identity in the A layout of v_mfma_f32_16x16x16_bf16 (lane (li, lg): row
     // li, columns 4 lg .. 4 lg + 3), so that I B hands each lane its own four B values:
     // three such products sum the planes in fp32, (s1 + s2) + s3, exactly (every partial
     // sum is the value less a tail it lacks), on the matrix pipe instead of 20 VALU
@@ -1742,16 +1694,12 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
         bf16v4, one_at < 4 ? 0x3f80ull << (16 * one_at) : 0ull);
     auto get_own = [&](int t, int hh) __attribute__((always_inline)) {
       const int k = 16 * (2 * w + t) + 4 * lg;
-      if constexpr (Split) {
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
-          acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-              ident, *reinterpret_cast<const bf16v4*>(&sS[pl][16 * hh + li][k]), acc, 0, 0, 0);
-        return acc;
-      } else {
-        return *reinterpret_cast<const f32x4*>(&sS[16 * hh + li][k]);
-      }
+      for (int pl = 0; pl < 3; ++pl)
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+            ident, *reinterpret_cast<const bf16v4*>(&sS[pl][16 * hh + li][k]), acc, 0, 0, 0);
+      return acc;
     };
     // the first chunk's pieces 0 and 1 go out before the state's loads, so that their
     // latencies overlap (the state is waited for first, to reach sS)
@@ -1784,8 +1732,8 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
       const __amdgpu_buffer_rsrc_t vnext = v_rows(c + 1);
       __syncthreads();  // sS holds the state at the chunk's start
       // Y = K_a S_h^T (this chunk's Kr and gamma loaded beside it)
-      const f32x4 y = times_st(op.kq, [&](int q) {
-        if (q == 0) load_state32(op, cur, vnext, voff, vrow, own, w, a, lane16, lg16, 2);
+      const f32x4 y = times_st(op.kq, [&]() {
+        load_state32(op, cur, vnext, voff, vrow, own, w, a, lane16, lg16, 2);
       });
       // X = diag(beta) V - diag(ws) Y for tokens 16 a + 4 lg + r, row 16 h + li (beta and ws
       // are zero past the chunk's end, and so is v)
@@ -1810,74 +1758,42 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
       }
       const f32x4 vn = vn0 + vn1;
       *reinterpret_cast<f32x4*>(&sVn[16 * h + li][16 * a + 4 * lg]) = vn;
-      if constexpr (Split) {
+      {
         const Split4 sp = split4(vn * op.ck);
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl)
           *reinterpret_cast<uint2*>(&sVk[pl][16 * h + li][16 * a + 4 * lg]) = sp.p[pl];
-      } else {
-        *reinterpret_cast<f32x4*>(&sVk[16 * h + li][16 * a + 4 * lg]) = vn * op.ck;
       }
       __syncthreads();  // V_new complete; every read of sS for this chunk done
       // the update: Kr^T (exact bf16; the lane's k row 16 (2w + t) + li, tokens
       // j = 8 lg + e) against V_new ck (tokens j, rows 16 hh + li); the next chunk's
       // pieces 0 and 1 loaded beside it
-      if constexpr (Split) {
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          load_state32(op, next, vnext, voff, vrow, own, w, a, lane16, lg16, hh);
-          // V_new ck's three planes, smallest first
-          bf16x8 vk[3];
+      for (int hh = 0; hh < 2; ++hh) {
+        load_state32(op, next, vnext, voff, vrow, own, w, a, lane16, lg16, hh);
+        // V_new ck's three planes, smallest first
+        bf16x8 vk[3];
 #pragma unroll
-          for (int pl = 0; pl < 3; ++pl)
-            vk[pl] = *reinterpret_cast<const bf16x8*>(&sVk[pl][16 * hh + li][8 * lg]);
+        for (int pl = 0; pl < 3; ++pl)
+          vk[pl] = *reinterpret_cast<const bf16x8*>(&sVk[pl][16 * hh + li][8 * lg]);
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            f32x4 st = get_own(t, hh) * op.gamma;
+        for (int t = 0; t < 2; ++t) {
+          f32x4 st = get_own(t, hh) * op.gamma;
 #pragma unroll
-            for (int pl = 2; pl >= 0; --pl)
-              st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, op.kr[t]),
-                                                           vk[pl], st, 0, 0, 0);
-            put_own(t, hh, st);
-          }
-          __builtin_amdgcn_sched_barrier(kLoadGroup);
+          for (int pl = 2; pl >= 0; --pl)
+            st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, op.kr[t]),
+                                                         vk[pl], st, 0, 0, 0);
+          put_own(t, hh, st);
         }
-      } else {
-        f32x4 st[2][2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) st[t][hh] = get_own(t, hh) * op.gamma;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          load_state32(op, next, vnext, voff, vrow, own, w, a, lane16, lg16, q);
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            // tokens j = 8 lg + 4 q + e
-            const f32x4 b = *reinterpret_cast<const f32x4*>(&sVk[16 * hh + li][8 * lg + 4 * q]);
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              const f32x4 ka = bf16x4(op.kr[t], q);
-              st[t][hh] = mfma(ka.x, b.x, st[t][hh]);
-              st[t][hh] = mfma(ka.y, b.y, st[t][hh]);
-              st[t][hh] = mfma(ka.z, b.z, st[t][hh]);
-              st[t][hh] = mfma(ka.w, b.w, st[t][hh]);
-            }
-          }
-          __builtin_amdgcn_sched_barrier(kLoadGroup);
-        }
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) put_own(t, hh, st[t][hh]);
+        __builtin_amdgcn_sched_barrier(kLoadGroup);
       }
     }
     // The final state from the wave's own pieces (its LDS accesses complete in order, so no
-    // barrier is needed), through the tile's resource.  Split: the lane's offset formed anew
-    // from the lane count (mbcnt), as a work-item id or offset held across the chunk loop
-    // took a register that loop needs (a spill); the fp32 form's loop leaves room for it.
+    // barrier is needed), through the tile's resource.  The lane's offset is formed anew from
+    // the lane count (mbcnt): a work-item id or offset held across the chunk loop took a
+    // register that loop needs (a spill).
     if (slot > 0) {
-      const int l = Split ? __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) : lane;
+      const int l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
       const __amdgpu_buffer_rsrc_t srs = state_resource(p, slot, head, true);
       const uint32_t soff = static_cast<uint32_t>(((row0 + (l & 15)) * kDim + 32 * w + 4 * (l >> 4)) * 4);
 #pragma unroll
@@ -1904,8 +1820,8 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
       const __amdgpu_buffer_rsrc_t cur = record(c);
       const __amdgpu_buffer_rsrc_t next = record(c + 1);
       __syncthreads();  // sS holds the state at the chunk's start
-      f32x4 o0 = times_st(op.qr, [&](int q) {   // P of this chunk beside it
-        if (q == 0) load_output32(op, cur, own, a, lane16, lg16, 2);
+      f32x4 o0 = times_st(op.qr, [&]() {   // P of this chunk beside it
+        load_output32(op, cur, own, a, lane16, lg16, 2);
       });
       // rows of q S^T scaled to (q^ exp(G)) S^T; P V_new accumulates on top
       o0 = o0 * op.sq;
@@ -1993,15 +1909,9 @@ int launch_chunks(const DecodeParams& p, int num_sequences, int64_t num_tokens, 
   if constexpr (TT == 2) {
     const int64_t scan_groups = (pairs + 7) / 8 * 8 * (kDim / 32);
     if (scan_groups > 0x7fffffff) return fail(LD_ERR_INVALID_ARGUMENT, "prefill too large");
-    // the split products once the prompts average more than one chunk
-    if (num_tokens > 32 * static_cast<int64_t>(num_sequences))
-      hipLaunchKernelGGL(chunk_scan32_kernel<true>, dim3(static_cast<uint32_t>(scan_groups)),
-                         dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
-                         static_cast<int>(chunks));
-    else
-      hipLaunchKernelGGL(chunk_scan32_kernel<false>, dim3(static_cast<uint32_t>(scan_groups)),
-                         dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
-                         static_cast<int>(chunks));
+    hipLaunchKernelGGL(chunk_scan32_kernel, dim3(static_cast<uint32_t>(scan_groups)),
+                       dim3(kScanThreads), 0, stream, p, num_sequences, ws, chunk_start,
+                       static_cast<int>(chunks));
   } else {
     // two row tiles per workgroup once they still give 2 workgroups per CU
     const bool two_tiles = pairs * (kDim / 32) >= 512;
