@@ -1726,7 +1726,22 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
 #pragma unroll
         for (int t = 0; t < 2; ++t) put_own(t, hh, st[t][hh]);
     }
-    for (int c = 0; c < chunks; ++c) {
+    // The state's final pieces straight to the tile (through its resource; the lane's offset
+    // formed anew from the lane count, mbcnt, as a work-item id or offset held across the
+    // chunk loop took a register that loop needs: a spill).
+    auto store_own = [&](int t, int hh, f32x4 v) __attribute__((always_inline)) {
+      const int l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+      const __amdgpu_buffer_rsrc_t srs = state_resource(p, slot, head, true);
+      const uint32_t soff =
+          static_cast<uint32_t>(((row0 + (l & 15)) * kDim + 32 * w + 4 * (l >> 4)) * 4);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), srs,
+                                             static_cast<int>(soff + (16 * hh * kDim + 16 * t) * 4),
+                                             0, 0);
+    };
+    // One chunk; the last one's updated pieces go to the tile instead of through sS's planes
+    // (nothing reads them there again), which spares prompts of one chunk a split and a sum
+    // per piece.
+    auto chunk = [&](int c, auto last) __attribute__((always_inline)) {
       const __amdgpu_buffer_rsrc_t cur = record(c);
       const __amdgpu_buffer_rsrc_t next = record(c + 1);
       const __amdgpu_buffer_rsrc_t vnext = v_rows(c + 1);
@@ -1783,26 +1798,25 @@ void chunk_scan32_kernel(const DecodeParams p, int num_sequences, float* ws,
           for (int pl = 2; pl >= 0; --pl)
             st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, op.kr[t]),
                                                          vk[pl], st, 0, 0, 0);
-          put_own(t, hh, st);
+          if constexpr (decltype(last)::value) {
+            if (slot > 0) store_own(t, hh, st);
+          } else {
+            put_own(t, hh, st);
+          }
         }
         __builtin_amdgcn_sched_barrier(kLoadGroup);
       }
-    }
-    // The final state from the wave's own pieces (its LDS accesses complete in order, so no
-    // barrier is needed), through the tile's resource.  The lane's offset is formed anew from
-    // the lane count (mbcnt): a work-item id or offset held across the chunk loop took a
-    // register that loop needs (a spill).
-    if (slot > 0) {
-      const int l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-      const __amdgpu_buffer_rsrc_t srs = state_resource(p, slot, head, true);
-      const uint32_t soff = static_cast<uint32_t>(((row0 + (l & 15)) * kDim + 32 * w + 4 * (l >> 4)) * 4);
+    };
+    for (int c = 0; c + 1 < chunks; ++c) chunk(c, std::false_type{});
+    if (chunks > 0) {
+      chunk(chunks - 1, std::true_type{});
+    } else if (slot > 0) {
+      // no chunk: the state as it came in (zeros for a sequence that does not start from
+      // its slot; its LDS accesses complete in order, so no barrier is needed)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, get_own(t, hh)), srs,
-                                                 static_cast<int>(soff + (16 * hh * kDim + 16 * t) * 4),
-                                                 0, 0);
+        for (int t = 0; t < 2; ++t) store_own(t, hh, get_own(t, hh));
     }
   } else {
     const int out_row = p.num_v_heads * kDim;   // elements per token row of out
