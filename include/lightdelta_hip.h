@@ -241,7 +241,7 @@ int64_t ld_gdn_prefill_workspace_bytes(int64_t num_tokens, int32_t num_sequences
 
 /*
  * The tokens per chunk LD_PREFILL_AUTO runs for this shape (given a workspace), 64 or 32, or
- * 0 when it runs the token-serial form.  With L = num_tokens / num_sequences: 0 for L < 20;
+ * 0 when it runs the token-serial form.  With L = num_tokens / num_sequences: 0 for L < 17;
  * 64 for L >= 512 in fewer than 64 (sequence, head) pairs; else 32.
  * Callers use it to decide whether to provide the workspace.  No counterpart in the
  * reference (its prefill always runs chunk_gated_delta_rule).

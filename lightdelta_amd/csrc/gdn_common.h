@@ -118,22 +118,23 @@ __device__ __forceinline__ float softplus(float x) {
 // num_sequences sequences and num_v_heads heads, and the launch of its three phases; the
 // raw outputs go to p.out for prefill_norm_kernel.
 // The form AUTO runs, from the mean prompt length L = num_tokens / num_sequences, measured
-// on MI355X over 1 x 16 .. 4096 x 16 tokens at 32 v heads (ms, token-serial / 64-token
+// on MI355X over 1 x 8 .. 4096 x 8 tokens at 32 v heads (ms, token-serial / 64-token
 // chunks / 32-token chunks):
-//   * token-serial below 20 tokens (1024 x 16: 1.54 / 3.47 / 1.70; 512 x 20: 0.90 / 1.76 /
-//     0.89; 1 x 16: 0.028 / 0.033 / 0.029);
+//   * token-serial below 17 tokens (1024 x 12: 1.30 / - / 1.51; 1024 x 16: 1.53-1.78 /
+//     3.03 / 1.50-1.55, where boxes of the pool disagree on the order; 1 x 16: 0.026 /
+//     0.032 / 0.030);
 //   * 64-token chunks for prompts of 512 tokens or more in fewer than 64 (sequence, head)
 //     pairs, where the chunk-by-chunk chain is the time and 64-token chunks halve it
-//     (1 x 4096: 2.73 / 0.250 / 0.296; 1 x 512: 0.358 / 0.0565 / 0.0571; 1 x 256: 0.185 /
-//     0.046 / 0.040; 2 x 2048, 64 pairs: 1.39 / 0.243 / 0.175);
-//   * 32-token chunks otherwise (1024 x 32: 2.63 / 3.53 / 1.85; 1024 x 36: 2.91 / 3.58 /
-//     2.63; 32 x 1024: 2.66 / 1.58 / 1.07; 1 x 64: 0.053 / 0.032 / 0.028).
+//     (1 x 4096: 2.74 / 0.201 / 0.279; 1 x 512: 0.357 / 0.051 / 0.056; 1 x 256: 0.183 /
+//     0.043 / 0.038; 2 x 2048, 64 pairs: 1.38 / 0.199 / 0.167);
+//   * 32-token chunks otherwise (1024 x 17: 1.63 / 3.06 / 1.53; 1024 x 32: 2.66 / 3.12 /
+//     1.72; 32 x 1024: 2.66 / 1.36 / 1.06; 1 x 64: 0.053 / 0.033 / 0.030).
 // Returns the tokens per chunk (64 or 32), or 0 for the token-serial form.
 inline int prefill_auto_chunk_tokens(int64_t num_tokens, int64_t num_sequences,
                                      int64_t num_v_heads) {
   if (num_sequences <= 0 || num_tokens <= 0) return 0;
   const int64_t mean = num_tokens / num_sequences;
-  if (mean < 20) return 0;
+  if (mean < 17) return 0;
   if (num_sequences * num_v_heads < 64 && mean >= 512) return 64;
   return 32;
 }

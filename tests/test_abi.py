@@ -176,8 +176,9 @@ def test_prefill_workspace_query_and_chunked_without_workspace():
     (512 * 64, 512, 32, 32),
     (1024 * 32, 1024, 32, 32),  # short prompts: one full 32-token chunk each
     (1024 * 36, 1024, 32, 32),  # a second chunk that holds few tokens
-    (1024 * 20, 1024, 32, 32),  # the shortest that go chunked
-    (1024 * 20 - 1, 1024, 32, 0),
+    (1024 * 20, 1024, 32, 32),
+    (1024 * 17, 1024, 32, 32),  # the shortest that go chunked
+    (1024 * 17 - 1, 1024, 32, 0),
     (1024 * 16, 1024, 32, 0),
     (2 * 16, 2, 32, 0),
     (0, 1, 32, 0),
