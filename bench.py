@@ -620,12 +620,27 @@ def prefill(device):
                     chunk_flop = (scan + subst) * 2048 + tiles * 16384
                     flop = seqs * -(-length // c) * HV * chunk_flop
                     entry[algorithm]["mfma_TFLOPs"] = round(flop / ms / 1e9, 1)
+            # new prompts (the serving case): no state read, zeros to start from; the form
+            # AUTO picks
+            ops.set_prefill_algorithm("auto")
+            case["has_initial"].zero_()
+            run()
+            torch.cuda.synchronize()
+            start, end = events()
+            start.record()
+            for _ in range(reps):
+                run()
+            end.record()
+            torch.cuda.synchronize()
+            ms = start.elapsed_time(end) / reps
+            entry["fresh_auto"] = {"ms": round(ms, 3), "tokens_per_s": round(total / ms * 1e3, 1)}
         finally:
             ops.set_prefill_algorithm(saved)
         result[label] = entry
         del case
     result["workload"] = ("prefill (state from the slot, recurrence over the prompt, gated "
-                          "RMSNorm, final state to the slot), 16 qk / 32 v heads")
+                          "RMSNorm, final state to the slot), 16 qk / 32 v heads; fresh_auto: "
+                          "new prompts (zero initial state, no state read) under AUTO")
     return result
 
 
