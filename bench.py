@@ -99,6 +99,8 @@ def parse_args():
                    help="bound on the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-cold", action="store_true")
+    p.add_argument("--no-tp", action="store_true",
+                   help="skip the step at one GPU's share under head parallelism (TP = 2, 4)")
     p.add_argument("--no-conv", action="store_true")
     p.add_argument("--no-stack", action="store_true",
                    help="skip the 48-layer, 96 GiB stack measurement")
@@ -556,6 +558,64 @@ def host_cost(device, calls=2000):
         result[f"B{batch}_us_per_call"] = round((t1 - t0) / calls * 1e6, 2)
     result["workload"] = ("host time per eager GDNBackend call (validation, argument packing, "
                           "launch), 16/48 heads, T=1")
+    return result
+
+
+def tp_shares(steps, device):
+    """The step at one GPU's share of the layer under head (tensor) parallelism: TP = 2 (8 qk
+    / 16 v heads) and TP = 4 (4 qk / 8 v heads) at B = 32 and B = 128 requests per GPU.  Each
+    GPU of a TP group runs exactly this launch on its own heads and state shard, with nothing
+    exchanged inside the op.  `hot`: the same slots every step (keep policy); `cold`: disjoint
+    slot sets rotated through at least 1 GiB of pool (stream policy)."""
+    import torch
+
+    from lightdelta_amd import ops
+    from lightdelta_amd.workloads import decode_case
+
+    saved = ops.state_cache_policy()
+    slots_at, pool_at = ORDER.index("slots"), ORDER.index("pool")
+    result = {"workload": "one GPU's share of the B-request step under head parallelism: "
+                          "TP=2 (8 qk / 16 v heads), TP=4 (4 qk / 8 v heads); frac on state "
+                          "bytes (one read + one write per tile)"}
+    try:
+        for tp in (2, 4):
+            h, hv = H // tp, HV // tp
+            for batch in (32, 128):
+                case = decode_case(batch, 1, num_k_heads=h, num_v_heads=hv, seed=3,
+                                   device=device)
+                args = [case[k] for k in ORDER]
+                tile_bytes = DIM * DIM * 4
+                step_bytes = batch * hv * tile_bytes * 2
+                ops.set_state_cache_policy("keep")
+                hot = _graph_us(lambda: torch.ops.lightdelta.decode(*args, 1e-6), steps)
+                per_set = batch * hv * tile_bytes
+                sets = max(16, -(-(1 << 30) // per_set))
+                big = torch.empty(sets * batch + 1, hv, DIM, DIM, device=device).normal_(0.0, 0.02)
+                perm = torch.randperm(sets * batch, device=device) + 1
+                slot_sets = [perm[i * batch:(i + 1) * batch].to(torch.int32).view(batch, 1)
+                             for i in range(sets)]
+                cold_args = list(args)
+                cold_args[pool_at] = big
+
+                def cold_pass():
+                    for slots in slot_sets:
+                        cold_args[slots_at] = slots
+                        torch.ops.lightdelta.decode(*cold_args, 1e-6)
+
+                ops.set_state_cache_policy("stream")
+                cold = _graph_us(cold_pass, max(1, steps // sets)) / sets
+                result[f"tp{tp}_b{batch}"] = {
+                    "qk_heads": h, "v_heads": hv, "tiles": batch * hv,
+                    "hot_us": round(hot, 3),
+                    "hot_frac": round(step_bytes / hot / 1e3 / HBM_PEAK_GBS, 4),
+                    "cold_us": round(cold, 3),
+                    "cold_TBps": round(step_bytes / cold / 1e6, 3),
+                    "cold_frac": round(step_bytes / cold / 1e3 / HBM_PEAK_GBS, 4),
+                    "cold_pool_GiB": round(big.numel() * 4 / 2**30, 2),
+                }
+                del big, case, args, cold_args
+    finally:
+        ops.set_state_cache_policy(saved)
     return result
 
 
@@ -1026,6 +1086,9 @@ def main():
         result["roofline"]["cold_frac"] = result["cold"]["frac"]
         result["roofline"]["cold_us_per_step"] = round(1e6 / cold_rate, 3)
         del big
+
+    if not args.no_tp:
+        result["tp_shares"] = tp_shares(args.steps, device)
 
     if not args.no_conv:
         result["conv_fused"] = conv_fused(case, op_args, args.steps, device)
