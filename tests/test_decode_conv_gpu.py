@@ -94,7 +94,7 @@ def test_first_workload_config_zero_conv_state(gpu):
     run_and_check(case, 16, torch.Generator().manual_seed(1), label="cfg1")
 
 
-@pytest.mark.parametrize("heads", [(16, 16), (16, 32), (16, 48)])
+@pytest.mark.parametrize("heads", [(16, 16), (16, 32), (16, 48), (8, 16)])
 def test_head_groups_and_shared_conv_state(gpu, heads, policy):
     announce(test="conv_groups", heads=heads, policy=policy)
     case = conv_case(gpu, 8, heads, pool_slots=12, seed=heads[1])

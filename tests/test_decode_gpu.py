@@ -50,7 +50,7 @@ def policy(request):
     ops.set_state_cache_policy(saved)
 
 
-@pytest.mark.parametrize("heads", [(16, 48), (16, 32), (4, 8), (8, 8)])
+@pytest.mark.parametrize("heads", [(16, 48), (16, 32), (8, 16), (4, 8), (8, 8)])
 @pytest.mark.parametrize("width", [1, 2, 3, 4])
 @pytest.mark.parametrize("state_io", ["indexed", "packed"])
 def test_matches_oracle(gpu, heads, width, state_io, policy):
