@@ -11,6 +11,8 @@ import pytest
 import torch
 
 from lightdelta_amd import ops
+from lightdelta_amd.backend import GDNBackend
+from lightdelta_amd.config import BackendConfig
 from lightdelta_amd.workloads import decode_case
 from oracle.decode import expected_decode, expected_decode_conv, expected_prefill
 from tests.parity import assert_bf16_outputs, assert_states
@@ -56,13 +58,14 @@ def padded_slots(d: Draw, count: int, pool_slots: int) -> torch.Tensor:
     return torch.where(pad, fill, ids).to(torch.int32)
 
 
-def random_step_case(gpu, seed: int, conv: bool = False):
-    """A decode (or conv-fused decode) launch drawn from `seed`: returns (case, description)."""
+def random_step_case(gpu, seed: int, conv: bool = False, longer: bool = True):
+    """A decode (or conv-fused decode) launch drawn from `seed`: returns (case, cache policy,
+    description).  `longer`: sometimes one request with more tokens than its width."""
     d = Draw(seed)
     h, hv = d.pick(HEADS)
     batch, width = d.int(1, 40), d.int(1, 4)
     lengths = torch.randint(0, width + 1, (batch,), generator=d.gen)
-    if not conv and d.int(0, 3) == 0:  # one request longer than its width: rejected
+    if longer and not conv and d.int(0, 3) == 0:  # a request longer than its width: rejected
         lengths[d.int(0, batch - 1)] = width + 1
     tokens = int(lengths.sum())
     pool_slots = batch * width + 3
@@ -114,6 +117,24 @@ def test_decode_sweep(gpu, seed, restore_settings):
     exp_out, exp_pool, pre = expected_decode(*args, 1e-6, return_pre=True)
     before = case["pool"].clone()
     torch.ops.lightdelta.decode(*args, 1e-6)
+    torch.cuda.synchronize()
+    assert_bf16_outputs(case["out"], exp_out, pre, label=f"seed {seed}")
+    assert_states(case["pool"], exp_pool, label=f"seed {seed}", **STEP_STATE)
+    assert torch.equal(case["pool"][0], before[0])
+
+
+@pytest.mark.parametrize("seed", range(300, 320))
+def test_backend_packed_sweep(gpu, seed, restore_settings):
+    """GDNBackend's packed path (packed_plan, gather_state, the step on the scratch,
+    scatter_state) on the same draws, token counts within the width (device metadata the
+    backend trusts, as the reference's does)."""
+    case, policy, what = random_step_case(gpu, seed, longer=False)
+    announce(dict(test="backend_packed_sweep", **what))
+    ops.set_state_cache_policy(policy)
+    args = [case[k] for k in ORDER]
+    exp_out, exp_pool, pre = expected_decode(*args, 1e-6, return_pre=True)
+    before = case["pool"].clone()
+    GDNBackend(BackendConfig(compute="cuda_fused", state_io="packed"))(*args, 1e-6)
     torch.cuda.synchronize()
     assert_bf16_outputs(case["out"], exp_out, pre, label=f"seed {seed}")
     assert_states(case["pool"], exp_pool, label=f"seed {seed}", **STEP_STATE)
