@@ -576,7 +576,10 @@ def tp_shares(steps, device):
     slots_at, pool_at = ORDER.index("slots"), ORDER.index("pool")
     result = {"workload": "one GPU's share of the B-request step under head parallelism: "
                           "TP=2 (8 qk / 16 v heads), TP=4 (4 qk / 8 v heads); frac on state "
-                          "bytes (one read + one write per tile)"}
+                          "bytes (one read + one write per tile) against the 8 TB/s HBM peak; "
+                          "hot = the same slots every step, Infinity-Cache resident (keep "
+                          "policy); cold = disjoint slot sets rotated through >= 1 GiB "
+                          "(stream policy), the HBM-bound figure"}
     try:
         for tp in (2, 4):
             h, hv = H // tp, HV // tp
